@@ -1,0 +1,191 @@
+/*
+ * zorse_amd.h -- C ABI of libzorse_amd.so, the MI355X (gfx950) kernels for the
+ * Llama/Mistral decoder-layer hot path and the flat-shard AdamW step.
+ *
+ * Conventions shared by every entry point:
+ *   - Device buffers are plain pointers; sizes and strides are int64 element
+ *     counts (never bytes unless the name says so).
+ *   - `stream` is a hipStream_t passed as void* (0 = the null stream).  Work is
+ *     only enqueued; no entry point synchronises or allocates device memory.
+ *     Workspaces are sized by the *_workspace() queries and passed in.
+ *   - Return value: 0 on success, a negative ZK_E* code on a rejected argument,
+ *     or a positive hipError_t from the launch.  zk_last_error() returns a
+ *     thread-local message describing the last failure.  No C++ exception
+ *     crosses this boundary.
+ *   - dtype codes: ZK_F32, ZK_F16, ZK_BF16.  Arithmetic is fp32 inside every
+ *     kernel; activations are rounded to their storage type on write.
+ *
+ * Each entry point names the reference code whose computation it replaces
+ * (paths relative to the benson-guo/zorse tree; "HF" = transformers'
+ * modeling_llama.py / modeling_mistral.py, which the reference imports).
+ */
+#ifndef ZORSE_AMD_H
+#define ZORSE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* zk_stream_t;
+
+enum zk_dtype { ZK_F32 = 0, ZK_F16 = 1, ZK_BF16 = 2 };
+
+enum zk_status {
+  ZK_OK = 0,
+  ZK_EINVAL = -1,       /* bad size / stride / null pointer                  */
+  ZK_EDTYPE = -2,       /* unsupported dtype combination                     */
+  ZK_EALIGN = -3,       /* pointer or stride not aligned for vector access   */
+  ZK_EUNSUPPORTED = -4, /* valid but not implemented (e.g. head_dim 96)      */
+  ZK_EWORKSPACE = -5    /* workspace too small                               */
+};
+
+/* Thread-local text of the last error (empty string if none). */
+const char* zk_last_error(void);
+
+/* ABI version; bumped whenever a signature below changes. */
+int zk_abi_version(void);
+
+/* Device facts used for roofline denominators.  arch receives e.g. "gfx950". */
+int zk_device_info(int device, char* arch, int arch_len, int* num_cus,
+                   int* max_clock_khz, int64_t* hbm_bytes);
+
+/* ---------------------------------------------------------------- RMSNorm --
+ * Replaces HF LlamaRMSNorm / MistralRMSNorm.forward as used by the decoder
+ * layer (models/llama_simple.py:419-422, 458, 475; models/mistral_simple.py:82)
+ * and the torchtitan RMSNorm (models/llama_v2.py:24-51):
+ *     h   = x (+ residual)                       rounded to act dtype
+ *     r   = rsqrt(mean(h^2) + eps)               fp32, stored in rstd[rows]
+ *     y   = w * round_act(h * r)                 rounded to act dtype
+ * When residual != NULL the residual add of models/llama_simple.py:471 is
+ * fused in and h is written to h_out.  x, residual, h_out, y: [rows, hidden]
+ * contiguous, act dtype; w: [hidden] in w_dtype.
+ */
+int zk_rmsnorm_fwd(const void* x, const void* residual, void* h_out,
+                   const void* w, void* y, float* rstd, int64_t rows,
+                   int64_t hidden, float eps, int act_dtype, int w_dtype,
+                   zk_stream_t stream);
+
+/* fp32 elements of workspace zk_rmsnorm_bwd needs for (rows, hidden). */
+int64_t zk_rmsnorm_bwd_workspace(int64_t rows, int64_t hidden);
+
+/* Backward of zk_rmsnorm_fwd (autograd of the same reference lines):
+ *     g  = dy * w ;  xh = h * r
+ *     dx = r * (g - xh * mean(g * xh))  (+ dres when dres != NULL)
+ *     dw = sum_rows dy * round_act(xh)   (written to dw in w_dtype, or added
+ *                                          to it when accumulate != 0)
+ * h is the normalised input (the fwd's h_out, or x when no residual). */
+int zk_rmsnorm_bwd(const void* dy, const void* h, const void* w,
+                   const float* rstd, const void* dres, void* dx, void* dw,
+                   int accumulate, float* workspace, int64_t workspace_elems,
+                   int64_t rows, int64_t hidden, int act_dtype, int w_dtype,
+                   zk_stream_t stream);
+
+/* ----------------------------------------------------------------- SwiGLU --
+ * Replaces the activation of HF LlamaMLP.forward, act_fn(gate(x)) * up(x)
+ * (imported at models/llama_simple.py:10, built at :418; torchtitan
+ * FeedForward.forward, models/llama_v2.py:319-320):
+ *     z = round(round(silu(g)) * u)
+ * g = gate[r, c], u = up[r, c] read with row stride ld_in (so gate and up can
+ * be the two halves of one [rows, 2F] GEMM output); z has row stride ld_z. */
+int zk_swiglu_fwd(const void* gate, const void* up, int64_t ld_in, void* z,
+                  int64_t ld_z, int64_t rows, int64_t cols, int dtype,
+                  zk_stream_t stream);
+
+/* Backward: s = silu(g), sg = sigmoid(g)
+ *     dup   = dz * round(s)
+ *     dgate = round(dz * u) * sg * (1 + g * (1 - sg))
+ * dgate / dup share row stride ld_out (halves of one [rows, 2F] buffer). */
+int zk_swiglu_bwd(const void* dz, int64_t ld_dz, const void* gate,
+                  const void* up, int64_t ld_in, void* dgate, void* dup,
+                  int64_t ld_out, int64_t rows, int64_t cols, int dtype,
+                  zk_stream_t stream);
+
+/* ------------------------------------------------------------------- RoPE --
+ * Replaces apply_rotary_pos_emb / rotate_half (models/llama_simple.py:27-58,
+ * HF-style half-split pairing, per-op rounding in the act dtype) and
+ * apply_rotary_emb (models/llama_v2.py:151-177, interleaved complex pairing
+ * in fp32).  Rotates q [B,S,Hq,d] and k [B,S,Hkv,d] IN PLACE (element strides
+ * per batch / seq / head; d contiguous).  cos/sin: fp32 tables [n_pos, d/2]
+ * holding the reference's values (already rounded to the act dtype for the
+ * half-split pairing, as models/llama_simple.py:137 does).  positions: int64
+ * [S] row index into the tables, or NULL for 0..S-1.  inverse != 0 applies
+ * the transpose rotation (the backward of the forward rotation).
+ * k may be NULL (rotate q only). */
+enum zk_rope_pairing { ZK_ROPE_HALF = 0, ZK_ROPE_INTERLEAVED = 1 };
+int zk_rope(void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh, void* k,
+            int64_t k_sb, int64_t k_ss, int64_t k_sh, int64_t B, int64_t S,
+            int64_t Hq, int64_t Hkv, int64_t d, const float* cos,
+            const float* sin, int64_t n_pos, const int64_t* positions,
+            int pairing, int inverse, int dtype, zk_stream_t stream);
+
+/* -------------------------------------------------------------- Attention --
+ * Replaces the attention core of the decoder layer: softmax(Q K^T * scale +
+ * mask) V with GQA (repeat_kv never materialised: kv head = q head / n_rep)
+ * -- models/llama_simple.py:320-342 (eager), the FA2/SDPA classes it selects
+ * at :376-416, models/llama_v2.py:265-273 (SDPA is_causal=True) and HF
+ * MistralAttention (sliding window).  Mask: causal keeps key j <= query i;
+ * window > 0 additionally keeps only j > i - window (W keys including self).
+ * Q/K/V/O are [B, S, H, d] with element strides per batch / seq / head and
+ * d contiguous.  lse: fp32 [B, Hq, Sq] natural-log row logsumexp of the
+ * scaled, masked scores (saved for the backward). */
+typedef struct zk_attn_desc {
+  int64_t B, Sq, Skv, Hq, Hkv, d;
+  int64_t q_sb, q_ss, q_sh;
+  int64_t k_sb, k_ss, k_sh;
+  int64_t v_sb, v_ss, v_sh;
+  int64_t o_sb, o_ss, o_sh;   /* O and dO (forward output / its gradient) */
+  int64_t dq_sb, dq_ss, dq_sh;
+  int64_t dk_sb, dk_ss, dk_sh;
+  int64_t dv_sb, dv_ss, dv_sh;
+  float scale;
+  int causal;
+  int64_t window;             /* 0 = unlimited */
+  int dtype;                  /* ZK_BF16, ZK_F16 (MFMA) or ZK_F32 */
+} zk_attn_desc;
+
+int zk_attn_fwd(const zk_attn_desc* desc, const void* q, const void* k,
+                const void* v, void* o, float* lse, zk_stream_t stream);
+
+/* Bytes of workspace zk_attn_bwd needs (fp32 dQ accumulator + row deltas). */
+int64_t zk_attn_bwd_workspace(const zk_attn_desc* desc);
+
+/* Backward (FlashAttention-2 recomputation from lse): writes dq, dk, dv
+ * (overwrites, no accumulation) in the layout given by the dq/dk/dv strides;
+ * dO uses the o strides. */
+int zk_attn_bwd(const zk_attn_desc* desc, const void* q, const void* k,
+                const void* v, const void* o, const void* dout,
+                const float* lse, void* dq, void* dk, void* dv,
+                void* workspace, int64_t workspace_bytes, zk_stream_t stream);
+
+/* ------------------------------------------------------------------ AdamW --
+ * Replaces torch.optim.Adam(fused=True).step() on the layer's flat fp32
+ * parameter shard as run in the reduce-grad callback
+ * (zorse_utils/pipeline.py:176-179, utils/patch.py:115-138), with decoupled
+ * weight decay (torch.optim.AdamW semantics; weight_decay 0 == Adam):
+ *     p <- p * (1 - lr*wd)
+ *     m <- m + (1-b1) (g - m)         v <- b2 v + (1-b2) g^2
+ *     p <- p - lr/(1-b1^t) * m / (sqrt(v)/sqrt(1-b2^t) + eps)
+ * g is read in grad_dtype and widened to fp32 (the cast of utils/patch.py:
+ * 115-119 fused in).  When param_lowp != NULL the updated parameter is also
+ * written rounded to lowp_dtype (the compute copy).  n elements, step t >= 1.
+ */
+int zk_adamw_step(float* param, const void* grad, int grad_dtype,
+                  float* exp_avg, float* exp_avg_sq, void* param_lowp,
+                  int lowp_dtype, int64_t n, double lr, double beta1,
+                  double beta2, double eps, double weight_decay, int64_t step,
+                  zk_stream_t stream);
+
+/* ------------------------------------------------------------- Utilities --
+ * Dtype conversion of a contiguous buffer (the autocast weight cast and the
+ * grad cast of utils/patch.py:115-119 when done outside the AdamW kernel).
+ * y = round(x); when accumulate != 0, y = round(y + x). */
+int zk_cast(const void* x, int x_dtype, void* y, int y_dtype, int64_t n,
+            int accumulate, zk_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ZORSE_AMD_H */

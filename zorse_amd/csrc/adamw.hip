@@ -1,0 +1,205 @@
+// Fused AdamW step on one flat fp32 parameter shard.
+//
+// One pass over HBM: read p, g, m, v; write p, m, v (and the low-precision
+// compute copy of p when requested).  28 bytes per element with an fp32
+// grad, 26 with a bf16/fp16 grad, +2 for the low-precision copy.  Each thread
+// handles 4 consecutive elements per iteration (16-byte fp32 accesses) in a
+// grid-stride loop sized to keep every CU busy with several workgroups.
+#include <cmath>
+
+#include "zk_common.h"
+
+namespace zk {
+
+struct AdamScalars {
+  float decay;         // 1 - lr * weight_decay
+  float one_minus_b1;  // lerp weight of the first moment
+  float b2, one_minus_b2;
+  float step_size;     // lr / (1 - b1^t)
+  float bc2_sqrt;      // sqrt(1 - b2^t)
+  float eps;
+};
+
+template <typename G>
+__device__ __forceinline__ void load_grad4(const G* g, int64_t i, float (&o)[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) o[k] = to_f32(g[i + k]);
+}
+template <>
+__device__ __forceinline__ void load_grad4<float>(const float* g, int64_t i,
+                                                  float (&o)[4]) {
+  const float4 a = *reinterpret_cast<const float4*>(g + i);
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+}
+template <>
+__device__ __forceinline__ void load_grad4<bf16>(const bf16* g, int64_t i,
+                                                 float (&o)[4]) {
+  const bf16x4 a = *reinterpret_cast<const bf16x4*>(g + i);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) o[k] = static_cast<float>(a[k]);
+}
+template <>
+__device__ __forceinline__ void load_grad4<f16>(const f16* g, int64_t i,
+                                                float (&o)[4]) {
+  const f16x4 a = *reinterpret_cast<const f16x4*>(g + i);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) o[k] = static_cast<float>(a[k]);
+}
+
+template <typename L>
+__device__ __forceinline__ void store4(L* dst, const float4& v) {
+  dst[0] = from_f32<L>(v.x); dst[1] = from_f32<L>(v.y);
+  dst[2] = from_f32<L>(v.z); dst[3] = from_f32<L>(v.w);
+}
+template <>
+__device__ __forceinline__ void store4<bf16>(bf16* dst, const float4& v) {
+  bf16x4 a;
+  a[0] = static_cast<bf16>(v.x); a[1] = static_cast<bf16>(v.y);
+  a[2] = static_cast<bf16>(v.z); a[3] = static_cast<bf16>(v.w);
+  *reinterpret_cast<bf16x4*>(dst) = a;
+}
+template <>
+__device__ __forceinline__ void store4<f16>(f16* dst, const float4& v) {
+  f16x4 a;
+  a[0] = static_cast<f16>(v.x); a[1] = static_cast<f16>(v.y);
+  a[2] = static_cast<f16>(v.z); a[3] = static_cast<f16>(v.w);
+  *reinterpret_cast<f16x4*>(dst) = a;
+}
+template <>
+__device__ __forceinline__ void store4<float>(float* dst, const float4& v) {
+  *reinterpret_cast<float4*>(dst) = v;
+}
+
+__device__ __forceinline__ float adam_one(float& p, float g, float& m, float& v,
+                                          const AdamScalars& s) {
+  p = p * s.decay;
+  m = fmaf(s.one_minus_b1, g - m, m);
+  v = fmaf(s.one_minus_b2, g * g, v * s.b2);
+  const float denom = sqrtf(v) / s.bc2_sqrt + s.eps;
+  p = p - s.step_size * (m / denom);
+  return p;
+}
+
+// L = low-precision copy type; L = float means "no copy".
+template <typename G, typename L, bool kCopy>
+__global__ __launch_bounds__(256) void adamw_vec4(
+    float* __restrict__ p, const G* __restrict__ g, float* __restrict__ m,
+    float* __restrict__ v, L* __restrict__ lowp, int64_t n4, AdamScalars s) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       q < n4; q += stride) {
+    const int64_t i = q * 4;
+    float4 pv = *reinterpret_cast<const float4*>(p + i);
+    float4 mv = *reinterpret_cast<const float4*>(m + i);
+    float4 vv = *reinterpret_cast<const float4*>(v + i);
+    float gv[4];
+    load_grad4<G>(g, i, gv);
+    adam_one(pv.x, gv[0], mv.x, vv.x, s);
+    adam_one(pv.y, gv[1], mv.y, vv.y, s);
+    adam_one(pv.z, gv[2], mv.z, vv.z, s);
+    adam_one(pv.w, gv[3], mv.w, vv.w, s);
+    *reinterpret_cast<float4*>(p + i) = pv;
+    *reinterpret_cast<float4*>(m + i) = mv;
+    *reinterpret_cast<float4*>(v + i) = vv;
+    if (kCopy) store4<L>(lowp + i, pv);
+  }
+}
+
+// Any alignment / tail: one element per thread, dtypes by runtime code.
+__global__ __launch_bounds__(256) void adamw_scalar(
+    float* __restrict__ p, const void* __restrict__ g, int gdt,
+    float* __restrict__ m, float* __restrict__ v, void* __restrict__ lowp,
+    int ldt, int64_t begin, int64_t n, AdamScalars s) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = begin + static_cast<int64_t>(blockIdx.x) * blockDim.x +
+                   threadIdx.x;
+       i < n; i += stride) {
+    float pv = p[i], mv = m[i], vv = v[i];
+    adam_one(pv, load_dt(g, i, gdt), mv, vv, s);
+    p[i] = pv;
+    m[i] = mv;
+    v[i] = vv;
+    if (lowp != nullptr) store_dt(lowp, i, ldt, pv);
+  }
+}
+
+template <typename G>
+static void launch_vec(float* p, const void* g, float* m, float* v, void* lowp,
+                       int ldt, int64_t n4, const AdamScalars& s, int grid,
+                       hipStream_t st) {
+  if (lowp == nullptr)
+    hipLaunchKernelGGL((adamw_vec4<G, float, false>), dim3(grid), dim3(256), 0,
+                       st, p, (const G*)g, m, v, (float*)nullptr, n4, s);
+  else if (ldt == ZK_BF16)
+    hipLaunchKernelGGL((adamw_vec4<G, bf16, true>), dim3(grid), dim3(256), 0,
+                       st, p, (const G*)g, m, v, (bf16*)lowp, n4, s);
+  else if (ldt == ZK_F16)
+    hipLaunchKernelGGL((adamw_vec4<G, f16, true>), dim3(grid), dim3(256), 0,
+                       st, p, (const G*)g, m, v, (f16*)lowp, n4, s);
+  else
+    hipLaunchKernelGGL((adamw_vec4<G, float, true>), dim3(grid), dim3(256), 0,
+                       st, p, (const G*)g, m, v, (float*)lowp, n4, s);
+}
+
+}  // namespace zk
+
+using namespace zk;
+
+extern "C" int zk_adamw_step(float* param, const void* grad, int grad_dtype,
+                             float* exp_avg, float* exp_avg_sq,
+                             void* param_lowp, int lowp_dtype, int64_t n,
+                             double lr, double beta1, double beta2, double eps,
+                             double weight_decay, int64_t step,
+                             zk_stream_t stream) {
+  ZK_REQUIRE(valid_dtype(grad_dtype), ZK_EDTYPE,
+             "zk_adamw_step: bad grad dtype %d", grad_dtype);
+  ZK_REQUIRE(param_lowp == nullptr || valid_dtype(lowp_dtype), ZK_EDTYPE,
+             "zk_adamw_step: bad low-precision dtype %d", lowp_dtype);
+  ZK_REQUIRE(n >= 0, ZK_EINVAL, "zk_adamw_step: negative n");
+  ZK_REQUIRE(step >= 1, ZK_EINVAL, "zk_adamw_step: step must be >= 1 (got %lld)",
+             (long long)step);
+  ZK_REQUIRE(n == 0 || (param && grad && exp_avg && exp_avg_sq), ZK_EINVAL,
+             "zk_adamw_step: null pointer");
+  ZK_REQUIRE(lr >= 0 && beta1 >= 0 && beta1 < 1 && beta2 >= 0 && beta2 < 1 &&
+                 eps >= 0 && weight_decay >= 0,
+             ZK_EINVAL, "zk_adamw_step: hyper-parameter out of range");
+  if (n == 0) return ZK_OK;
+  AdamScalars s;
+  s.decay = static_cast<float>(1.0 - lr * weight_decay);
+  s.one_minus_b1 = static_cast<float>(1.0 - beta1);
+  s.b2 = static_cast<float>(beta2);
+  s.one_minus_b2 = static_cast<float>(1.0 - beta2);
+  const double bc1 = 1.0 - std::pow(beta1, static_cast<double>(step));
+  const double bc2 = 1.0 - std::pow(beta2, static_cast<double>(step));
+  s.step_size = static_cast<float>(lr / bc1);
+  s.bc2_sqrt = static_cast<float>(std::sqrt(bc2));
+  s.eps = static_cast<float>(eps);
+
+  hipStream_t st = as_stream(stream);
+  const int gbytes = dtype_bytes(grad_dtype);
+  const bool vec = aligned(param, 16) && aligned(exp_avg, 16) &&
+                   aligned(exp_avg_sq, 16) && aligned(grad, 4 * gbytes) &&
+                   (param_lowp == nullptr ||
+                    aligned(param_lowp, 4 * dtype_bytes(lowp_dtype)));
+  const int64_t n4 = vec ? n / 4 : 0;
+  const int max_grid = device_cus() * 8;
+  if (n4 > 0) {
+    int64_t want = (n4 + 255) / 256;
+    const int grid = static_cast<int>(want < max_grid ? want : max_grid);
+    if (grad_dtype == ZK_F32)
+      launch_vec<float>(param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_dtype, n4, s, grid, st);
+    else if (grad_dtype == ZK_BF16)
+      launch_vec<bf16>(param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_dtype, n4, s, grid, st);
+    else
+      launch_vec<f16>(param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_dtype, n4, s, grid, st);
+  }
+  const int64_t begin = n4 * 4;
+  if (begin < n) {
+    int64_t want = (n - begin + 255) / 256;
+    const int grid = static_cast<int>(want < max_grid ? want : max_grid);
+    hipLaunchKernelGGL(adamw_scalar, dim3(grid), dim3(256), 0, st, param, grad,
+                       grad_dtype, exp_avg, exp_avg_sq, param_lowp, lowp_dtype,
+                       begin, n, s);
+  }
+  return launch_status("zk_adamw_step");
+}

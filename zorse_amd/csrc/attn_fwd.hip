@@ -1,0 +1,388 @@
+// Flash-attention forward for gfx950 (bf16 / fp16 storage, fp32 softmax).
+//
+// Workgroup = 4 waves = 128 queries of one (batch, q-head); each wave owns 32
+// queries whose Q rows stay in registers for the whole kernel.  The kernel
+// streams 64-key tiles of K and V through LDS (K row-major, V transposed on
+// the LDS write) with the next tile's global loads in flight during the
+// current tile's math.
+//
+// Orientation: the score tile is computed transposed, S^T = K Q^T, with
+// v_mfma_f32_32x32x16 (A = K from LDS, B = Q from registers).  In the MFMA
+// result layout lane l holds query (l mod 32) and 16 keys, so the online
+// softmax row max / row sum are per-lane reductions plus one exchange between
+// the two lane halves, and the rescale of the output accumulator is a
+// per-lane scalar.  The output is also accumulated transposed,
+// O^T += V^T P^T: the probabilities go from the score accumulators straight
+// into the B operand (a fixed permutation of the 16 keys of each MFMA step,
+// matched by the order in which V^T is read), so P never touches LDS.
+//
+// Masking: causal (key <= query), sliding window (key > query - W) and the
+// ragged end of the key range; tiles entirely masked for a wave are skipped,
+// tiles entirely visible skip the per-element mask.  Causal blocks are
+// launched heaviest-first.
+#include <type_traits>
+
+#include "attn_common.h"
+
+namespace zk {
+
+template <typename T, int D>
+struct FwdCfg {
+  static constexpr int BM = 128;          // queries per workgroup
+  static constexpr int BN = 64;           // keys per tile
+  static constexpr int KP = D + 8;        // K row pitch in LDS (elements)
+  static constexpr int VP = BN + 4;       // V^T row pitch in LDS (elements)
+  static constexpr int KCH = BN * D / 8 / 256;         // 16-byte K chunks / thread
+  static constexpr int VPR = (BN / 2) * (D / 8) / 256; // key-pair V chunks / thread
+  static_assert(KCH >= 1 && VPR >= 1, "tile too small for 256 threads");
+};
+
+__device__ __forceinline__ float fast_exp2(float x) {
+  return __builtin_amdgcn_exp2f(x);
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
+  typedef FwdCfg<T, D> C;
+  typedef Mfma<T> M;
+  typedef typename M::vec8 V8;
+  constexpr int BM = C::BM, BN = C::BN, KP = C::KP, VP = C::VP;
+  __shared__ __attribute__((aligned(16))) T Ks[BN * KP];
+  __shared__ __attribute__((aligned(16))) T Vt[D * VP];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int64_t nbh = a.B * a.Hq;
+  const int64_t bid = blockIdx.x;
+  const int64_t qt = n_qt - 1 - bid / nbh;  // heaviest (last) q tiles first
+  const int64_t bh = bid % nbh;
+  const int64_t b = bh / a.Hq, hq = bh % a.Hq;
+  const int64_t hk = hq / (a.Hq / a.Hkv);
+  const int64_t q0 = qt * BM;
+  const int64_t qw0 = q0 + wave * 32;
+  const int64_t my_q = qw0 + l32;
+
+  const T* Qp = static_cast<const T*>(a.q) + b * a.q_sb + hq * a.q_sh;
+  const T* Kp = static_cast<const T*>(a.k) + b * a.k_sb + hk * a.k_sh;
+  const T* Vp = static_cast<const T*>(a.v) + b * a.v_sb + hk * a.v_sh;
+
+  // Q^T operand: lane holds Q[my_q][16 ks + 8 g .. +7].
+  V8 qreg[D / 16];
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) {
+    if (my_q < a.Sq)
+      qreg[ks] = *reinterpret_cast<const V8*>(Qp + my_q * a.q_ss + 16 * ks + 8 * g);
+    else
+      qreg[ks] = V8{};
+  }
+
+  int64_t kv_lo = 0, kv_hi = a.Skv;
+  if (a.causal && kv_hi > q0 + BM) kv_hi = q0 + BM;
+  if (a.window > 0 && q0 - a.window + 1 > kv_lo) kv_lo = q0 - a.window + 1;
+  const int64_t t_lo = kv_lo / BN;
+  const int64_t t_hi = kv_hi > kv_lo ? (kv_hi + BN - 1) / BN : t_lo;
+
+  uint4 kr[C::KCH];
+  uint4 vr[2 * C::VPR];
+  auto prefetch = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < C::KCH; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c / (D / 8), col = (c % (D / 8)) * 8;
+      const int64_t key = k0 + row;
+      kr[i] = key < a.Skv ? *reinterpret_cast<const uint4*>(Kp + key * a.k_ss + col)
+                          : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < C::VPR; ++i) {
+      const int c = tid + 256 * i;
+      const int kp = c % (BN / 2), dch = c / (BN / 2);
+      const int64_t key = k0 + 2 * kp;
+      vr[2 * i] = key < a.Skv
+                      ? *reinterpret_cast<const uint4*>(Vp + key * a.v_ss + dch * 8)
+                      : make_uint4(0, 0, 0, 0);
+      vr[2 * i + 1] =
+          key + 1 < a.Skv
+              ? *reinterpret_cast<const uint4*>(Vp + (key + 1) * a.v_ss + dch * 8)
+              : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store_lds = [&]() {
+#pragma unroll
+    for (int i = 0; i < C::KCH; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c / (D / 8), col = (c % (D / 8)) * 8;
+      *reinterpret_cast<uint4*>(&Ks[row * KP + col]) = kr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < C::VPR; ++i) {
+      const int c = tid + 256 * i;
+      const int kp = c % (BN / 2), dch = c / (BN / 2);
+      const uint16_t* e0 = reinterpret_cast<const uint16_t*>(&vr[2 * i]);
+      const uint16_t* e1 = reinterpret_cast<const uint16_t*>(&vr[2 * i + 1]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t packed = static_cast<uint32_t>(e0[e]) |
+                                (static_cast<uint32_t>(e1[e]) << 16);
+        *reinterpret_cast<uint32_t*>(&Vt[(dch * 8 + e) * VP + 2 * kp]) = packed;
+      }
+    }
+  };
+
+  f32x16 o[D / 32];
+#pragma unroll
+  for (int nt = 0; nt < D / 32; ++nt) o[nt] = f32x16{};
+  float m_i = -INFINITY, l_i = 0.f;
+  const float c2 = a.scale_log2;
+
+  if (t_lo < t_hi) prefetch(t_lo * BN);
+  for (int64_t t = t_lo; t < t_hi; ++t) {
+    const int64_t k0 = t * BN;
+    __syncthreads();
+    store_lds();
+    __syncthreads();
+    if (t + 1 < t_hi) prefetch(k0 + BN);
+
+    // wave-uniform tile classification
+    bool skip = false, need_mask = k0 + BN > a.Skv;
+    const int64_t qmin = qw0, qmax = qw0 + 31;
+    if (a.causal) {
+      if (k0 > qmax) skip = true;
+      if (k0 + BN - 1 > qmin) need_mask = true;
+    }
+    if (a.window > 0) {
+      if (k0 + BN - 1 <= qmin - a.window) skip = true;
+      if (k0 <= qmax - a.window) need_mask = true;
+    }
+    if (skip) continue;
+
+    // The tile body is instantiated with and without the element mask so
+    // that the masking writes sit in the same straight-line block as the MFMA
+    // chain producing the scores (no branch between the two).
+    auto tile = [&](auto mask_tag) {
+      constexpr bool kMask = decltype(mask_tag)::value;
+      // S^T = K Q^T : s[tt] covers keys k0 + 32 tt .. +31
+      f32x16 s[BN / 32];
+#pragma unroll
+      for (int tt = 0; tt < BN / 32; ++tt) {
+        s[tt] = f32x16{};
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ++ks) {
+          const V8 kv = *reinterpret_cast<const V8*>(
+              &Ks[(32 * tt + l32) * KP + 16 * ks + 8 * g]);
+          s[tt] = M::mma(kv, qreg[ks], s[tt]);
+        }
+      }
+      if (kMask) {
+#pragma unroll
+        for (int tt = 0; tt < BN / 32; ++tt)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int64_t key = k0 + 32 * tt + 8 * (j >> 2) + 4 * g + (j & 3);
+            if (!attn_visible(my_q, key, a.Skv, a.causal, a.window))
+              s[tt][j] = -INFINITY;
+          }
+      }
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int tt = 0; tt < BN / 32; ++tt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, s[tt][j]);
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      const float m_new = fmaxf(m_i, mloc);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = fast_exp2((m_i - m_use) * c2);
+      m_i = m_new;
+      const float mc = m_use * c2;
+
+      // P^T (packed per 16-key MFMA step) and row sums
+      V8 pb[BN / 16];
+      float lsum = 0.f;
+#pragma unroll
+      for (int tt = 0; tt < BN / 32; ++tt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float p = fast_exp2(fmaf(s[tt][j], c2, -mc));
+          lsum += p;
+          pb[2 * tt + (j >> 3)][j & 7] = static_cast<T>(p);
+        }
+      l_i = l_i * alpha + lsum;
+#pragma unroll
+      for (int nt = 0; nt < D / 32; ++nt) o[nt] *= alpha;
+
+      // O^T += V^T P^T
+#pragma unroll
+      for (int nt = 0; nt < D / 32; ++nt) {
+        const T* vrow = &Vt[(32 * nt + l32) * VP];
+#pragma unroll
+        for (int kk = 0; kk < BN / 16; ++kk) {
+          const int kb = 16 * kk + 4 * g;
+          const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + kb);
+          const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + kb + 8);
+          const u32x4 w = {lo[0], lo[1], hi[0], hi[1]};
+          o[nt] = M::mma(__builtin_bit_cast(V8, w), pb[kk], o[nt]);
+        }
+      }
+    };
+    if (need_mask)
+      tile(std::true_type{});
+    else
+      tile(std::false_type{});
+  }
+
+  const float l_tot = l_i + __shfl_xor(l_i, 32, 64);
+  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  if (my_q < a.Sq) {
+    T* Op = static_cast<T*>(a.out) + b * a.o_sb + hq * a.o_sh + my_q * a.o_ss;
+#pragma unroll
+    for (int nt = 0; nt < D / 32; ++nt)
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        const int d0 = 32 * nt + 8 * a4 + 4 * g;
+        typedef T T4 __attribute__((ext_vector_type(4)));
+        T4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = static_cast<T>(o[nt][4 * a4 + e] * inv);
+        *reinterpret_cast<T4*>(Op + d0) = w;
+      }
+    if (g == 0)
+      a.lse_out[(b * a.Hq + hq) * a.Sq + my_q] =
+          l_tot > 0.f ? m_i * a.scale + logf(l_tot) : -INFINITY;
+  }
+}
+
+// --------------------------------------------------------------------------
+// fp32 path: one thread per query row, online softmax over all keys with the
+// row kept in registers.  Used for fp32 layers (small shapes); no MFMA.
+template <int D>
+__global__ __launch_bounds__(64) void attn_fwd_f32_kernel(AttnArgs a) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+  const int64_t total = a.B * a.Hq * a.Sq;
+  if (row >= total) return;
+  const int64_t qi = row % a.Sq;
+  const int64_t bh = row / a.Sq;
+  const int64_t b = bh / a.Hq, hq = bh % a.Hq;
+  const int64_t hk = hq / (a.Hq / a.Hkv);
+  const float* Q = static_cast<const float*>(a.q) + b * a.q_sb + hq * a.q_sh + qi * a.q_ss;
+  const float* K = static_cast<const float*>(a.k) + b * a.k_sb + hk * a.k_sh;
+  const float* V = static_cast<const float*>(a.v) + b * a.v_sb + hk * a.v_sh;
+  float q[D], acc[D];
+  for (int e = 0; e < D; ++e) { q[e] = e < a.d ? Q[e] : 0.f; acc[e] = 0.f; }
+  float m = -INFINITY, l = 0.f;
+  for (int64_t j = 0; j < a.Skv; ++j) {
+    if (!attn_visible(qi, j, a.Skv, a.causal, a.window)) continue;
+    const float* kr = K + j * a.k_ss;
+    float s = 0.f;
+    for (int e = 0; e < a.d; ++e) s = fmaf(q[e], kr[e], s);
+    s *= a.scale;
+    const float m_new = fmaxf(m, s);
+    const float alpha = expf(m - m_new);
+    const float p = expf(s - m_new);
+    l = l * alpha + p;
+    const float* vr = V + j * a.v_ss;
+    for (int e = 0; e < a.d; ++e) acc[e] = fmaf(acc[e], alpha, p * vr[e]);
+    m = m_new;
+  }
+  float* O = static_cast<float*>(a.out) + b * a.o_sb + hq * a.o_sh + qi * a.o_ss;
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  for (int e = 0; e < a.d; ++e) O[e] = acc[e] * inv;
+  a.lse_out[(b * a.Hq + hq) * a.Sq + qi] = l > 0.f ? m + logf(l) : -INFINITY;
+}
+
+}  // namespace zk
+
+using namespace zk;
+
+namespace zk {
+// Validates a descriptor; shared by forward and backward entry points.
+int check_attn_desc(const zk_attn_desc* d, const char* who, bool bwd) {
+  ZK_REQUIRE(d != nullptr, ZK_EINVAL, "%s: null descriptor", who);
+  ZK_REQUIRE(d->dtype == ZK_BF16 || d->dtype == ZK_F16 || d->dtype == ZK_F32,
+             ZK_EDTYPE, "%s: bad dtype %d", who, d->dtype);
+  ZK_REQUIRE(d->B >= 0 && d->Sq >= 0 && d->Skv >= 0 && d->Hq > 0 && d->Hkv > 0,
+             ZK_EINVAL, "%s: bad shape", who);
+  ZK_REQUIRE(d->Hq % d->Hkv == 0, ZK_EINVAL,
+             "%s: Hq=%lld not a multiple of Hkv=%lld", who, (long long)d->Hq,
+             (long long)d->Hkv);
+  ZK_REQUIRE(d->window >= 0, ZK_EINVAL, "%s: negative window", who);
+  ZK_REQUIRE(!(d->causal || d->window > 0) || d->Sq == d->Skv, ZK_EUNSUPPORTED,
+             "%s: masked attention needs Sq == Skv (got %lld, %lld)", who,
+             (long long)d->Sq, (long long)d->Skv);
+  if (d->dtype == ZK_F32) {
+    ZK_REQUIRE(d->d > 0 && d->d <= 128, ZK_EUNSUPPORTED,
+               "%s: fp32 path supports head_dim <= 128 (got %lld)", who,
+               (long long)d->d);
+  } else {
+    ZK_REQUIRE(d->d == 64 || d->d == 128, ZK_EUNSUPPORTED,
+               "%s: head_dim must be 64 or 128 (got %lld)", who, (long long)d->d);
+    // 16-byte vector access along d and along rows
+    const int64_t strides[] = {d->q_sb, d->q_ss, d->q_sh, d->k_sb, d->k_ss,
+                               d->k_sh, d->v_sb, d->v_ss, d->v_sh, d->o_sb,
+                               d->o_ss, d->o_sh};
+    for (int64_t s : strides)
+      ZK_REQUIRE(s % 8 == 0, ZK_EALIGN,
+                 "%s: strides must be multiples of 8 elements (got %lld)", who,
+                 (long long)s);
+    if (bwd) {
+      const int64_t bs[] = {d->dq_sb, d->dq_ss, d->dq_sh, d->dk_sb, d->dk_ss,
+                            d->dk_sh, d->dv_sb, d->dv_ss, d->dv_sh};
+      for (int64_t s : bs)
+        ZK_REQUIRE(s % 8 == 0, ZK_EALIGN,
+                   "%s: grad strides must be multiples of 8 elements", who);
+    }
+  }
+  ZK_REQUIRE(d->B * d->Hq * ((d->Sq + 127) / 128) < 0x7fffffffLL, ZK_EINVAL,
+             "%s: grid too large", who);
+  return ZK_OK;
+}
+
+void fill_args(AttnArgs& a, const zk_attn_desc* d) {
+  a.B = d->B; a.Sq = d->Sq; a.Skv = d->Skv; a.Hq = d->Hq; a.Hkv = d->Hkv; a.d = d->d;
+  a.q_sb = d->q_sb; a.q_ss = d->q_ss; a.q_sh = d->q_sh;
+  a.k_sb = d->k_sb; a.k_ss = d->k_ss; a.k_sh = d->k_sh;
+  a.v_sb = d->v_sb; a.v_ss = d->v_ss; a.v_sh = d->v_sh;
+  a.o_sb = d->o_sb; a.o_ss = d->o_ss; a.o_sh = d->o_sh;
+  a.dq_sb = d->dq_sb; a.dq_ss = d->dq_ss; a.dq_sh = d->dq_sh;
+  a.dk_sb = d->dk_sb; a.dk_ss = d->dk_ss; a.dk_sh = d->dk_sh;
+  a.dv_sb = d->dv_sb; a.dv_ss = d->dv_ss; a.dv_sh = d->dv_sh;
+  a.scale = d->scale;
+  a.scale_log2 = d->scale * kLog2e;
+  a.causal = d->causal;
+  a.window = d->window;
+}
+}  // namespace zk
+
+extern "C" int zk_attn_fwd(const zk_attn_desc* desc, const void* q,
+                           const void* k, const void* v, void* o, float* lse,
+                           zk_stream_t stream) {
+  int rc = check_attn_desc(desc, "zk_attn_fwd", false);
+  if (rc != ZK_OK) return rc;
+  if (desc->B == 0 || desc->Sq == 0) return ZK_OK;
+  ZK_REQUIRE(q && k && v && o && lse, ZK_EINVAL, "zk_attn_fwd: null pointer");
+  AttnArgs a = {};
+  fill_args(a, desc);
+  a.q = q; a.k = k; a.v = v; a.out = o; a.lse_out = lse;
+  hipStream_t s = as_stream(stream);
+  if (desc->dtype == ZK_F32) {
+    const int64_t rows = desc->B * desc->Hq * desc->Sq;
+    const dim3 grid(static_cast<unsigned>((rows + 63) / 64));
+    if (desc->d <= 64)
+      hipLaunchKernelGGL(attn_fwd_f32_kernel<64>, grid, dim3(64), 0, s, a);
+    else
+      hipLaunchKernelGGL(attn_fwd_f32_kernel<128>, grid, dim3(64), 0, s, a);
+    return launch_status("zk_attn_fwd");
+  }
+  ZK_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(o, 16),
+             ZK_EALIGN, "zk_attn_fwd: q/k/v/o must be 16-byte aligned");
+  const int64_t n_qt = (desc->Sq + 127) / 128;
+  const dim3 grid(static_cast<unsigned>(n_qt * desc->B * desc->Hq));
+#define ZK_FWD(T, D) hipLaunchKernelGGL((attn_fwd_kernel<T, D>), grid, dim3(256), 0, s, a, n_qt)
+  if (desc->dtype == ZK_BF16) {
+    if (desc->d == 128) ZK_FWD(bf16, 128); else ZK_FWD(bf16, 64);
+  } else {
+    if (desc->d == 128) ZK_FWD(f16, 128); else ZK_FWD(f16, 64);
+  }
+#undef ZK_FWD
+  return launch_status("zk_attn_fwd");
+}

@@ -1,0 +1,365 @@
+// RMSNorm forward / backward for gfx950.
+//
+// One workgroup per row (forward) keeps the row in registers: NT threads x
+// MAXCH chunks of 8 elements (16-byte loads for 2-byte types), so x is read
+// once and y written once -- the HBM minimum.  The backward walks rows with a
+// grid of at most kBwdParts workgroups; each thread owns fixed columns, so the
+// weight gradient accumulates in registers and is written as one fp32 partial
+// row per workgroup, then reduced by a second kernel (deterministic, no
+// atomics).  Rows whose width is not a multiple of 8 (or misaligned buffers)
+// take the scalar kernels, which read the row twice.
+#include "vec.h"
+
+namespace zk {
+
+static constexpr int kBwdParts = 512;
+static constexpr int kMaxCh = 4;
+
+template <int NT>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (NT > 64) {
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < NT / 64; ++i) t += red[i];
+    __syncthreads();
+    return t;
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------- forward ---
+template <typename T, typename W, int NT>
+__global__ __launch_bounds__(NT) void rmsnorm_fwd_vec(
+    const T* __restrict__ x, const T* __restrict__ res, T* __restrict__ hout,
+    const W* __restrict__ w, T* __restrict__ y, float* __restrict__ rstd,
+    int64_t hidden, float eps) {
+  __shared__ float red[NT / 64];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * hidden;
+  const int nchunk = static_cast<int>(hidden / 8);
+  float v[kMaxCh][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < kMaxCh; ++c) {
+    const int ch = threadIdx.x + c * NT;
+    if (ch < nchunk) {
+      Vec8<T>::load(xr + ch * 8, v[c]);
+      if (res != nullptr) {
+        float r8[8];
+        Vec8<T>::load(res + row * hidden + ch * 8, r8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[c][i] = round_to<T>(v[c][i] + r8[i]);
+        Vec8<T>::store(hout + row * hidden + ch * 8, v[c]);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss = fmaf(v[c][i], v[c][i], ss);
+    }
+  }
+  ss = block_sum<NT>(ss, red);
+  const float r = 1.0f / sqrtf(ss / static_cast<float>(hidden) + eps);
+  if (threadIdx.x == 0) rstd[row] = r;
+#pragma unroll
+  for (int c = 0; c < kMaxCh; ++c) {
+    const int ch = threadIdx.x + c * NT;
+    if (ch < nchunk) {
+      float w8[8], o[8];
+      Vec8<W>::load(w + ch * 8, w8);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = w8[i] * round_to<T>(v[c][i] * r);
+      Vec8<T>::store(y + row * hidden + ch * 8, o);
+    }
+  }
+}
+
+// Scalar fallback: any width / alignment; dtypes by runtime code.
+__global__ __launch_bounds__(256) void rmsnorm_fwd_scalar(
+    const void* __restrict__ x, const void* __restrict__ res,
+    void* __restrict__ hout, const void* __restrict__ w, void* __restrict__ y,
+    float* __restrict__ rstd, int64_t hidden, float eps, int adt, int wdt) {
+  __shared__ float red[4];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * hidden;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < hidden; i += 256) {
+    float h = load_dt(x, base + i, adt);
+    if (res != nullptr) {
+      h = h + load_dt(res, base + i, adt);
+      store_dt(hout, base + i, adt, h);
+      h = load_dt(hout, base + i, adt);  // rounded value
+    }
+    ss = fmaf(h, h, ss);
+  }
+  ss = block_sum<256>(ss, red);
+  const float r = 1.0f / sqrtf(ss / static_cast<float>(hidden) + eps);
+  if (threadIdx.x == 0) rstd[blockIdx.x] = r;
+  const void* src = res != nullptr ? hout : x;
+  for (int64_t i = threadIdx.x; i < hidden; i += 256) {
+    const float h = load_dt(src, base + i, adt);
+    float xh = h * r;
+    if (adt != ZK_F32) xh = adt == ZK_BF16 ? round_to<bf16>(xh) : round_to<f16>(xh);
+    store_dt(y, base + i, adt, load_dt(w, i, wdt) * xh);
+  }
+}
+
+// --------------------------------------------------------------- backward ---
+template <typename T, typename W, int NT>
+__global__ __launch_bounds__(NT) void rmsnorm_bwd_vec(
+    const T* __restrict__ dy, const T* __restrict__ h, const W* __restrict__ w,
+    const float* __restrict__ rstd, const T* __restrict__ dres,
+    T* __restrict__ dx, float* __restrict__ part, int64_t rows,
+    int64_t hidden) {
+  __shared__ float red[NT / 64];
+  const int nchunk = static_cast<int>(hidden / 8);
+  float wv[kMaxCh][8], dw[kMaxCh][8];
+#pragma unroll
+  for (int c = 0; c < kMaxCh; ++c) {
+    const int ch = threadIdx.x + c * NT;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dw[c][i] = 0.f;
+    if (ch < nchunk) Vec8<W>::load(w + ch * 8, wv[c]);
+  }
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const float r = rstd[row];
+    float g[kMaxCh][8], xh[kMaxCh][8];
+    float dot = 0.f;
+#pragma unroll
+    for (int c = 0; c < kMaxCh; ++c) {
+      const int ch = threadIdx.x + c * NT;
+      if (ch < nchunk) {
+        float d8[8], h8[8];
+        Vec8<T>::load(dy + row * hidden + ch * 8, d8);
+        Vec8<T>::load(h + row * hidden + ch * 8, h8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          xh[c][i] = h8[i] * r;
+          g[c][i] = d8[i] * wv[c][i];
+          dot = fmaf(g[c][i], xh[c][i], dot);
+          dw[c][i] = fmaf(d8[i], round_to<T>(xh[c][i]), dw[c][i]);
+        }
+      }
+    }
+    dot = block_sum<NT>(dot, red);
+    const float mean = dot / static_cast<float>(hidden);
+#pragma unroll
+    for (int c = 0; c < kMaxCh; ++c) {
+      const int ch = threadIdx.x + c * NT;
+      if (ch < nchunk) {
+        float o[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = r * (g[c][i] - xh[c][i] * mean);
+        if (dres != nullptr) {
+          float r8[8];
+          Vec8<T>::load(dres + row * hidden + ch * 8, r8);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] += r8[i];
+        }
+        Vec8<T>::store(dx + row * hidden + ch * 8, o);
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < kMaxCh; ++c) {
+    const int ch = threadIdx.x + c * NT;
+    if (ch < nchunk)
+      Vec8<float>::store(part + static_cast<int64_t>(blockIdx.x) * hidden + ch * 8,
+                         dw[c]);
+  }
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_bwd_scalar(
+    const void* __restrict__ dy, const void* __restrict__ h,
+    const void* __restrict__ w, const float* __restrict__ rstd,
+    const void* __restrict__ dres, void* __restrict__ dx,
+    float* __restrict__ part, int64_t rows, int64_t hidden, int adt,
+    int wdt) {
+  __shared__ float red[4];
+  float* prow = part + static_cast<int64_t>(blockIdx.x) * hidden;
+  for (int64_t i = threadIdx.x; i < hidden; i += 256) prow[i] = 0.f;
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const int64_t base = row * hidden;
+    const float r = rstd[row];
+    float dot = 0.f;
+    for (int64_t i = threadIdx.x; i < hidden; i += 256) {
+      const float xh = load_dt(h, base + i, adt) * r;
+      const float d = load_dt(dy, base + i, adt);
+      dot = fmaf(d * load_dt(w, i, wdt), xh, dot);
+      float xr = xh;
+      if (adt != ZK_F32) xr = adt == ZK_BF16 ? round_to<bf16>(xh) : round_to<f16>(xh);
+      prow[i] = fmaf(d, xr, prow[i]);
+    }
+    dot = block_sum<256>(dot, red);
+    const float mean = dot / static_cast<float>(hidden);
+    for (int64_t i = threadIdx.x; i < hidden; i += 256) {
+      const float xh = load_dt(h, base + i, adt) * r;
+      const float g = load_dt(dy, base + i, adt) * load_dt(w, i, wdt);
+      float o = r * (g - xh * mean);
+      if (dres != nullptr) o += load_dt(dres, base + i, adt);
+      store_dt(dx, base + i, adt, o);
+    }
+  }
+}
+
+// dw[c] = sum_p part[p][c]  (optionally added to the existing dw).  A
+// workgroup owns 64 columns; its 4 waves stride over the partial rows and
+// meet in LDS.  nparts == 0 writes zeros (or leaves dw unchanged).
+__global__ __launch_bounds__(256) void rmsnorm_dw_reduce(
+    const float* __restrict__ part, int64_t nparts, int64_t hidden,
+    void* __restrict__ dw, int wdt, int accumulate) {
+  __shared__ float red[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+  float s = 0.f;
+  if (c < hidden)
+    for (int64_t p = wave; p < nparts; p += 4) s += part[p * hidden + c];
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && c < hidden) {
+    s = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+    if (accumulate) s += load_dt(dw, c, wdt);
+    store_dt(dw, c, wdt, s);
+  }
+}
+
+// ------------------------------------------------------------ dispatch ------
+static int pick_threads(int64_t hidden) {
+  const int64_t nchunk = hidden / 8;
+  if (nchunk > 128 * kMaxCh) return 256;
+  if (nchunk > 64 * kMaxCh) return 128;
+  return 64;
+}
+
+template <typename T, typename W>
+static void launch_fwd_vec(const void* x, const void* res, void* hout,
+                           const void* w, void* y, float* rstd, int64_t rows,
+                           int64_t hidden, float eps, hipStream_t s) {
+  const int nt = pick_threads(hidden);
+#define ZK_LAUNCH(NT)                                                       \
+  hipLaunchKernelGGL((rmsnorm_fwd_vec<T, W, NT>), dim3(rows), dim3(NT), 0, s, \
+                     (const T*)x, (const T*)res, (T*)hout, (const W*)w,     \
+                     (T*)y, rstd, hidden, eps)
+  if (nt == 256) ZK_LAUNCH(256);
+  else if (nt == 128) ZK_LAUNCH(128);
+  else ZK_LAUNCH(64);
+#undef ZK_LAUNCH
+}
+
+template <typename T, typename W>
+static void launch_bwd_vec(const void* dy, const void* h, const void* w,
+                           const float* rstd, const void* dres, void* dx,
+                           float* part, int64_t nparts, int64_t rows,
+                           int64_t hidden, hipStream_t s) {
+  const int nt = pick_threads(hidden);
+#define ZK_LAUNCH(NT)                                                          \
+  hipLaunchKernelGGL((rmsnorm_bwd_vec<T, W, NT>), dim3(nparts), dim3(NT), 0, s, \
+                     (const T*)dy, (const T*)h, (const W*)w, rstd,             \
+                     (const T*)dres, (T*)dx, part, rows, hidden)
+  if (nt == 256) ZK_LAUNCH(256);
+  else if (nt == 128) ZK_LAUNCH(128);
+  else ZK_LAUNCH(64);
+#undef ZK_LAUNCH
+}
+
+template <typename T>
+static bool dispatch_w_fwd(int wdt, const void* x, const void* res, void* hout,
+                           const void* w, void* y, float* rstd, int64_t rows,
+                           int64_t hidden, float eps, hipStream_t s) {
+  if (wdt == ZK_F32) launch_fwd_vec<T, float>(x, res, hout, w, y, rstd, rows, hidden, eps, s);
+  else if (wdt == ZK_BF16) launch_fwd_vec<T, bf16>(x, res, hout, w, y, rstd, rows, hidden, eps, s);
+  else launch_fwd_vec<T, f16>(x, res, hout, w, y, rstd, rows, hidden, eps, s);
+  return true;
+}
+
+template <typename T>
+static void dispatch_w_bwd(int wdt, const void* dy, const void* h,
+                           const void* w, const float* rstd, const void* dres,
+                           void* dx, float* part, int64_t nparts, int64_t rows,
+                           int64_t hidden, hipStream_t s) {
+  if (wdt == ZK_F32) launch_bwd_vec<T, float>(dy, h, w, rstd, dres, dx, part, nparts, rows, hidden, s);
+  else if (wdt == ZK_BF16) launch_bwd_vec<T, bf16>(dy, h, w, rstd, dres, dx, part, nparts, rows, hidden, s);
+  else launch_bwd_vec<T, f16>(dy, h, w, rstd, dres, dx, part, nparts, rows, hidden, s);
+}
+
+static bool vec_ok(int64_t hidden, int adt, int wdt,
+                   std::initializer_list<const void*> ptrs) {
+  if (hidden % 8 != 0 || hidden / 8 > 256 * kMaxCh) return false;
+  for (const void* p : ptrs)
+    if (p != nullptr && !aligned(p, 16)) return false;
+  (void)adt;
+  (void)wdt;
+  return true;
+}
+
+}  // namespace zk
+
+using namespace zk;
+
+extern "C" int zk_rmsnorm_fwd(const void* x, const void* residual, void* h_out,
+                              const void* w, void* y, float* rstd, int64_t rows,
+                              int64_t hidden, float eps, int act_dtype,
+                              int w_dtype, zk_stream_t stream) {
+  ZK_REQUIRE(valid_dtype(act_dtype) && valid_dtype(w_dtype), ZK_EDTYPE,
+             "zk_rmsnorm_fwd: bad dtype code (%d, %d)", act_dtype, w_dtype);
+  ZK_REQUIRE(rows >= 0 && hidden > 0, ZK_EINVAL,
+             "zk_rmsnorm_fwd: bad shape rows=%lld hidden=%lld",
+             (long long)rows, (long long)hidden);
+  ZK_REQUIRE(x && w && y && rstd, ZK_EINVAL, "zk_rmsnorm_fwd: null pointer");
+  ZK_REQUIRE(residual == nullptr || h_out != nullptr, ZK_EINVAL,
+             "zk_rmsnorm_fwd: residual given without h_out");
+  ZK_REQUIRE(rows <= 0x7fffffff, ZK_EINVAL, "zk_rmsnorm_fwd: too many rows");
+  if (rows == 0) return ZK_OK;
+  hipStream_t s = as_stream(stream);
+  if (vec_ok(hidden, act_dtype, w_dtype, {x, residual, h_out, w, y})) {
+    if (act_dtype == ZK_BF16) dispatch_w_fwd<bf16>(w_dtype, x, residual, h_out, w, y, rstd, rows, hidden, eps, s);
+    else if (act_dtype == ZK_F16) dispatch_w_fwd<f16>(w_dtype, x, residual, h_out, w, y, rstd, rows, hidden, eps, s);
+    else dispatch_w_fwd<float>(w_dtype, x, residual, h_out, w, y, rstd, rows, hidden, eps, s);
+  } else {
+    hipLaunchKernelGGL(rmsnorm_fwd_scalar, dim3(rows), dim3(256), 0, s, x,
+                       residual, h_out, w, y, rstd, hidden, eps, act_dtype,
+                       w_dtype);
+  }
+  return launch_status("zk_rmsnorm_fwd");
+}
+
+extern "C" int64_t zk_rmsnorm_bwd_workspace(int64_t rows, int64_t hidden) {
+  if (rows <= 0 || hidden <= 0) return 0;
+  const int64_t parts = rows < kBwdParts ? rows : kBwdParts;
+  return parts * hidden;
+}
+
+extern "C" int zk_rmsnorm_bwd(const void* dy, const void* h, const void* w,
+                              const float* rstd, const void* dres, void* dx,
+                              void* dw, int accumulate, float* workspace,
+                              int64_t workspace_elems, int64_t rows,
+                              int64_t hidden, int act_dtype, int w_dtype,
+                              zk_stream_t stream) {
+  ZK_REQUIRE(valid_dtype(act_dtype) && valid_dtype(w_dtype), ZK_EDTYPE,
+             "zk_rmsnorm_bwd: bad dtype code (%d, %d)", act_dtype, w_dtype);
+  ZK_REQUIRE(rows >= 0 && hidden > 0, ZK_EINVAL,
+             "zk_rmsnorm_bwd: bad shape rows=%lld hidden=%lld",
+             (long long)rows, (long long)hidden);
+  ZK_REQUIRE(dy && h && w && rstd && dx && dw, ZK_EINVAL,
+             "zk_rmsnorm_bwd: null pointer");
+  const int64_t need = zk_rmsnorm_bwd_workspace(rows, hidden);
+  ZK_REQUIRE(workspace_elems >= need && (need == 0 || workspace != nullptr),
+             ZK_EWORKSPACE, "zk_rmsnorm_bwd: workspace %lld < %lld floats",
+             (long long)workspace_elems, (long long)need);
+  hipStream_t s = as_stream(stream);
+  const int64_t parts = rows == 0 ? 0 : need / hidden;
+  if (rows == 0) {
+    // nothing to differentiate; the reduce below writes dw = 0 (or keeps it)
+  } else if (vec_ok(hidden, act_dtype, w_dtype, {dy, h, w, dres, dx, workspace})) {
+    if (act_dtype == ZK_BF16) dispatch_w_bwd<bf16>(w_dtype, dy, h, w, rstd, dres, dx, workspace, parts, rows, hidden, s);
+    else if (act_dtype == ZK_F16) dispatch_w_bwd<f16>(w_dtype, dy, h, w, rstd, dres, dx, workspace, parts, rows, hidden, s);
+    else dispatch_w_bwd<float>(w_dtype, dy, h, w, rstd, dres, dx, workspace, parts, rows, hidden, s);
+  } else {
+    hipLaunchKernelGGL(rmsnorm_bwd_scalar, dim3(parts), dim3(256), 0, s, dy, h,
+                       w, rstd, dres, dx, workspace, rows, hidden, act_dtype,
+                       w_dtype);
+  }
+  hipLaunchKernelGGL(rmsnorm_dw_reduce, dim3((hidden + 63) / 64), dim3(256),
+                     0, s, workspace, parts, hidden, dw, w_dtype, accumulate);
+  return launch_status("zk_rmsnorm_bwd");
+}

@@ -1,0 +1,138 @@
+// Rotary position embedding, applied in place to Q and K.
+//
+// One thread rotates 4 pairs of one (batch, position, head) row: for the
+// half-split pairing it reads elements i..i+3 and i+d/2..i+d/2+3, for the
+// interleaved pairing the 8 consecutive elements 2i..2i+7.  cos/sin come
+// from fp32 tables [n_pos, d/2] built by the caller with the reference's
+// own formula, so the kernel only does the rotation arithmetic:
+//   half-split (HF rotate_half, per-op rounding in the storage type):
+//     y1 = r(r(x1 c) + r(-x2 s))      y2 = r(r(x2 c) + r(x1 s))
+//   interleaved (complex product in fp32, one rounding):
+//     y1 = r(x1 c - x2 s)             y2 = r(x1 s + x2 c)
+// The inverse (backward) applies the transpose rotation with the same
+// rounding structure as autograd of those expressions.
+#include "zk_common.h"
+
+namespace zk {
+
+template <typename T, int kPairing, bool kInverse>
+__device__ __forceinline__ void rotate_pair(float x1, float x2, float c,
+                                            float s, float& y1, float& y2) {
+  if (kPairing == ZK_ROPE_HALF) {
+    if (!kInverse) {
+      y1 = round_to<T>(round_to<T>(x1 * c) + round_to<T>(-x2 * s));
+      y2 = round_to<T>(round_to<T>(x2 * c) + round_to<T>(x1 * s));
+    } else {
+      // d/dx of the forward: dx1 = dy1 c + dy2 s, dx2 = dy2 c - dy1 s
+      y1 = round_to<T>(round_to<T>(x1 * c) + round_to<T>(x2 * s));
+      y2 = round_to<T>(round_to<T>(x2 * c) - round_to<T>(x1 * s));
+    }
+  } else {
+    if (!kInverse) {
+      y1 = x1 * c - x2 * s;
+      y2 = x1 * s + x2 * c;
+    } else {
+      y1 = x1 * c + x2 * s;
+      y2 = x2 * c - x1 * s;
+    }
+  }
+}
+
+template <typename T, int kPairing, bool kInverse>
+__global__ __launch_bounds__(256) void rope_kernel(
+    T* __restrict__ q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+    T* __restrict__ k, int64_t k_sb, int64_t k_ss, int64_t k_sh, int64_t B,
+    int64_t S, int64_t Hq, int64_t Hkv, int64_t d,
+    const float* __restrict__ cosT, const float* __restrict__ sinT,
+    int64_t n_pos, const int64_t* __restrict__ positions) {
+  const int64_t half = d / 2;
+  const int64_t nq = (half + 3) / 4;  // quads of pairs per row
+  const int64_t H = Hq + (k != nullptr ? Hkv : 0);
+  const int64_t total = B * S * H * nq;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       t < total; t += stride) {
+    int64_t r = t;
+    const int64_t quad = r % nq; r /= nq;
+    const int64_t h = r % H; r /= H;
+    const int64_t s = r % S;
+    const int64_t b = r / S;
+    T* row = h < Hq ? q + b * q_sb + s * q_ss + h * q_sh
+                    : k + b * k_sb + s * k_ss + (h - Hq) * k_sh;
+    int64_t pos = positions != nullptr ? positions[s] : s;
+    if (pos < 0) pos = 0;
+    if (pos >= n_pos) pos = n_pos - 1;
+    const float* crow = cosT + pos * half;
+    const float* srow = sinT + pos * half;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t i = quad * 4 + j;
+      if (i < half) {
+        const int64_t i1 = kPairing == ZK_ROPE_HALF ? i : 2 * i;
+        const int64_t i2 = kPairing == ZK_ROPE_HALF ? i + half : 2 * i + 1;
+        float y1, y2;
+        rotate_pair<T, kPairing, kInverse>(to_f32(row[i1]), to_f32(row[i2]),
+                                           crow[i], srow[i], y1, y2);
+        row[i1] = from_f32<T>(y1);
+        row[i2] = from_f32<T>(y2);
+      }
+    }
+  }
+}
+
+template <typename T>
+static void launch_rope(int pairing, int inverse, void* q, int64_t q_sb,
+                        int64_t q_ss, int64_t q_sh, void* k, int64_t k_sb,
+                        int64_t k_ss, int64_t k_sh, int64_t B, int64_t S,
+                        int64_t Hq, int64_t Hkv, int64_t d, const float* c,
+                        const float* sn, int64_t n_pos, const int64_t* pos,
+                        hipStream_t st) {
+  const int64_t H = Hq + (k != nullptr ? Hkv : 0);
+  const int64_t total = B * S * H * ((d / 2 + 3) / 4);
+  int64_t grid = (total + 255) / 256;
+  const int64_t cap = static_cast<int64_t>(device_cus()) * 16;
+  if (grid > cap) grid = cap;
+  if (grid < 1) grid = 1;
+#define ZK_ROPE(P, I)                                                          \
+  hipLaunchKernelGGL((rope_kernel<T, P, I>), dim3(grid), dim3(256), 0, st,     \
+                     (T*)q, q_sb, q_ss, q_sh, (T*)k, k_sb, k_ss, k_sh, B, S, Hq, \
+                     Hkv, d, c, sn, n_pos, pos)
+  if (pairing == ZK_ROPE_HALF) {
+    if (inverse) ZK_ROPE(ZK_ROPE_HALF, true); else ZK_ROPE(ZK_ROPE_HALF, false);
+  } else {
+    if (inverse) ZK_ROPE(ZK_ROPE_INTERLEAVED, true); else ZK_ROPE(ZK_ROPE_INTERLEAVED, false);
+  }
+#undef ZK_ROPE
+}
+
+}  // namespace zk
+
+using namespace zk;
+
+extern "C" int zk_rope(void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                       void* k, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                       int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t d,
+                       const float* cos, const float* sin, int64_t n_pos,
+                       const int64_t* positions, int pairing, int inverse,
+                       int dtype, zk_stream_t stream) {
+  ZK_REQUIRE(valid_dtype(dtype), ZK_EDTYPE, "zk_rope: bad dtype %d", dtype);
+  ZK_REQUIRE(pairing == ZK_ROPE_HALF || pairing == ZK_ROPE_INTERLEAVED,
+             ZK_EINVAL, "zk_rope: bad pairing %d", pairing);
+  ZK_REQUIRE(B >= 0 && S >= 0 && Hq >= 0 && Hkv >= 0 && d > 0 && d % 2 == 0,
+             ZK_EINVAL, "zk_rope: bad shape (d must be even, got %lld)",
+             (long long)d);
+  ZK_REQUIRE(q && cos && sin, ZK_EINVAL, "zk_rope: null pointer");
+  ZK_REQUIRE(positions != nullptr || n_pos >= S, ZK_EINVAL,
+             "zk_rope: table has %lld positions < S=%lld", (long long)n_pos,
+             (long long)S);
+  ZK_REQUIRE(n_pos > 0, ZK_EINVAL, "zk_rope: empty table");
+  if (B == 0 || S == 0 || Hq + Hkv == 0) return ZK_OK;
+  hipStream_t st = as_stream(stream);
+  if (dtype == ZK_BF16)
+    launch_rope<bf16>(pairing, inverse, q, q_sb, q_ss, q_sh, k, k_sb, k_ss, k_sh, B, S, Hq, Hkv, d, cos, sin, n_pos, positions, st);
+  else if (dtype == ZK_F16)
+    launch_rope<f16>(pairing, inverse, q, q_sb, q_ss, q_sh, k, k_sb, k_ss, k_sh, B, S, Hq, Hkv, d, cos, sin, n_pos, positions, st);
+  else
+    launch_rope<float>(pairing, inverse, q, q_sb, q_ss, q_sh, k, k_sb, k_ss, k_sh, B, S, Hq, Hkv, d, cos, sin, n_pos, positions, st);
+  return launch_status("zk_rope");
+}

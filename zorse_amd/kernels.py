@@ -1,0 +1,317 @@
+"""Tensor-level wrappers of the C ABI.
+
+Each wrapper validates device / dtype / layout in Python (so bad input is a
+``ValueError`` before anything is enqueued), allocates outputs and workspaces
+with torch's caching allocator, and enqueues the kernel on torch's current
+stream.  The C side re-validates and reports through ``zk_last_error``.
+Nothing here falls back to another implementation: without the library or a
+GPU tensor these functions raise.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _abi
+from ._abi import check, dtype_code, lib, ptr, stream_handle
+
+_LOWP = (torch.bfloat16, torch.float16)
+
+
+def _require_gpu(*tensors: torch.Tensor | None) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("zorse_amd kernels need GPU tensors (got a CPU tensor)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} vs {t.device}")
+    if dev is None:
+        raise ValueError("no tensor given")
+    return dev
+
+
+def _require_contig(name: str, t: torch.Tensor) -> None:
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+# --------------------------------------------------------------- RMSNorm ---
+
+def rmsnorm_fwd(x: torch.Tensor, weight: torch.Tensor, eps: float,
+                residual: torch.Tensor | None = None):
+    """y = w * round(h * rsqrt(mean(h^2) + eps)), h = x (+ residual).
+
+    Returns (y, rstd, h); h is x itself when no residual is given."""
+    dev = _require_gpu(x, weight, residual)
+    if x.dtype not in (torch.float32, *_LOWP):
+        raise ValueError(f"unsupported activation dtype {x.dtype}")
+    hidden = x.shape[-1]
+    if weight.shape != (hidden,):
+        raise ValueError(f"weight shape {tuple(weight.shape)} != ({hidden},)")
+    _require_contig("x", x)
+    _require_contig("weight", weight)
+    rows = x.numel() // hidden if hidden else 0
+    y = torch.empty_like(x)
+    rstd = torch.empty(x.shape[:-1], device=dev, dtype=torch.float32)
+    h = x
+    if residual is not None:
+        if residual.shape != x.shape or residual.dtype != x.dtype:
+            raise ValueError("residual must match x in shape and dtype")
+        _require_contig("residual", residual)
+        h = torch.empty_like(x)
+    check(lib().zk_rmsnorm_fwd(ptr(x), ptr(residual), ptr(h) if residual is not None else None,
+                               ptr(weight), ptr(y), ptr(rstd), rows, hidden, float(eps),
+                               dtype_code(x.dtype), dtype_code(weight.dtype),
+                               stream_handle(dev)), "zk_rmsnorm_fwd")
+    return y, rstd, h
+
+
+def rmsnorm_bwd(dy: torch.Tensor, h: torch.Tensor, weight: torch.Tensor,
+                rstd: torch.Tensor, dres: torch.Tensor | None = None,
+                dw: torch.Tensor | None = None, accumulate: bool = False,
+                dw_dtype: torch.dtype | None = None):
+    """Returns (dx, dw).  dx includes dres when given; dw is written (or
+    accumulated into) ``dw`` if supplied, else a new tensor of ``dw_dtype``
+    (default: weight dtype)."""
+    dev = _require_gpu(dy, h, weight, rstd, dres, dw)
+    hidden = h.shape[-1]
+    for name, t in (("dy", dy), ("h", h), ("rstd", rstd), ("weight", weight)):
+        _require_contig(name, t)
+    if dy.shape != h.shape or dy.dtype != h.dtype:
+        raise ValueError("dy must match h in shape and dtype")
+    rows = h.numel() // hidden if hidden else 0
+    if rstd.numel() != rows or rstd.dtype != torch.float32:
+        raise ValueError("rstd must be fp32 with one value per row")
+    if dres is not None:
+        if dres.shape != h.shape or dres.dtype != h.dtype:
+            raise ValueError("dres must match h")
+        _require_contig("dres", dres)
+    if dw is None:
+        dw = torch.empty(hidden, device=dev, dtype=dw_dtype or weight.dtype)
+        accumulate = False
+    elif dw.shape != (hidden,) or not dw.is_contiguous():
+        raise ValueError("dw must be a contiguous [hidden] tensor")
+    dx = torch.empty_like(h)
+    ws_elems = lib().zk_rmsnorm_bwd_workspace(rows, hidden)
+    ws = torch.empty(max(ws_elems, 1), device=dev, dtype=torch.float32)
+    check(lib().zk_rmsnorm_bwd(ptr(dy), ptr(h), ptr(weight), ptr(rstd), ptr(dres), ptr(dx),
+                               ptr(dw), int(accumulate), ptr(ws), ws.numel(), rows, hidden,
+                               dtype_code(h.dtype), dtype_code(weight.dtype),
+                               stream_handle(dev)), "zk_rmsnorm_bwd")
+    return dx, dw
+
+
+# ----------------------------------------------------------------- SwiGLU --
+
+def _row_view_check(name: str, t: torch.Tensor) -> int:
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a 2-D row-major view (unit column stride)")
+    return t.stride(0)
+
+
+def swiglu_fwd(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None):
+    """z = round(round(silu(g)) * u) for 2-D views gate/up sharing a row stride."""
+    dev = _require_gpu(gate, up, out)
+    if gate.shape != up.shape or gate.dtype != up.dtype:
+        raise ValueError("gate and up must match")
+    ld = _row_view_check("gate", gate)
+    if _row_view_check("up", up) != ld:
+        raise ValueError("gate and up must share a row stride")
+    rows, cols = gate.shape
+    if out is None:
+        out = torch.empty(rows, cols, device=dev, dtype=gate.dtype)
+    ldz = _row_view_check("out", out)
+    check(lib().zk_swiglu_fwd(ptr(gate), ptr(up), ld, ptr(out), ldz, rows, cols,
+                              dtype_code(gate.dtype), stream_handle(dev)), "zk_swiglu_fwd")
+    return out
+
+
+def swiglu_bwd(dz: torch.Tensor, gate: torch.Tensor, up: torch.Tensor,
+               dgate: torch.Tensor, dup: torch.Tensor) -> None:
+    """Writes dgate / dup (2-D views sharing a row stride)."""
+    dev = _require_gpu(dz, gate, up, dgate, dup)
+    ld_in = _row_view_check("gate", gate)
+    if _row_view_check("up", up) != ld_in:
+        raise ValueError("gate and up must share a row stride")
+    ld_out = _row_view_check("dgate", dgate)
+    if _row_view_check("dup", dup) != ld_out:
+        raise ValueError("dgate and dup must share a row stride")
+    ld_dz = _row_view_check("dz", dz)
+    rows, cols = gate.shape
+    for t in (dz, up, dgate, dup):
+        if t.shape != (rows, cols) or t.dtype != gate.dtype:
+            raise ValueError("swiglu_bwd operands must match gate")
+    check(lib().zk_swiglu_bwd(ptr(dz), ld_dz, ptr(gate), ptr(up), ld_in, ptr(dgate),
+                              ptr(dup), ld_out, rows, cols, dtype_code(gate.dtype),
+                              stream_handle(dev)), "zk_swiglu_bwd")
+
+
+# ------------------------------------------------------------------- RoPE --
+
+def rope_(q: torch.Tensor, k: torch.Tensor | None, cos: torch.Tensor, sin: torch.Tensor,
+          positions: torch.Tensor | None = None, interleaved: bool = False,
+          inverse: bool = False) -> None:
+    """Rotate q [B,S,Hq,d] and k [B,S,Hkv,d] in place (unit stride along d).
+    cos / sin: fp32 [n_pos, d/2] tables."""
+    dev = _require_gpu(q, k, cos, sin, positions)
+    if q.dim() != 4 or q.stride(3) != 1:
+        raise ValueError("q must be [B,S,H,d] with unit stride along d")
+    B, S, Hq, d = q.shape
+    if k is not None:
+        if k.dim() != 4 or k.stride(3) != 1 or k.shape[0] != B or k.shape[1] != S \
+                or k.shape[3] != d or k.dtype != q.dtype:
+            raise ValueError("k must be [B,S,Hkv,d] matching q")
+        Hkv = k.shape[2]
+        ks = k.stride()
+    else:
+        Hkv, ks = 0, (0, 0, 0, 1)
+    if d % 2:
+        raise ValueError("head_dim must be even")
+    for name, t in (("cos", cos), ("sin", sin)):
+        if t.dtype != torch.float32 or t.dim() != 2 or t.shape[1] != d // 2 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous fp32 [n_pos, {d // 2}] table")
+    if cos.shape != sin.shape:
+        raise ValueError("cos and sin tables differ in shape")
+    n_pos = cos.shape[0]
+    if positions is not None:
+        if positions.dtype != torch.int64 or positions.numel() != S or not positions.is_contiguous():
+            raise ValueError("positions must be a contiguous int64 [S] tensor")
+    elif n_pos < S:
+        raise ValueError(f"table holds {n_pos} positions < S={S}")
+    qs = q.stride()
+    check(lib().zk_rope(ptr(q), qs[0], qs[1], qs[2], ptr(k), ks[0], ks[1], ks[2], B, S, Hq,
+                        Hkv, d, ptr(cos), ptr(sin), n_pos, ptr(positions),
+                        _abi.ZK_ROPE_INTERLEAVED if interleaved else _abi.ZK_ROPE_HALF,
+                        int(inverse), dtype_code(q.dtype), stream_handle(dev)), "zk_rope")
+
+
+# -------------------------------------------------------------- Attention --
+
+def _attn_desc(q, k, v, o, scale, causal, window, dq=None, dk=None, dv=None):
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be [B, S, H, d]")
+    B, Sq, Hq, d = q.shape
+    Bk, Skv, Hkv, dk_ = k.shape
+    if Bk != B or dk_ != d or v.shape != k.shape:
+        raise ValueError(f"shape mismatch q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
+    if Hq % Hkv:
+        raise ValueError(f"Hq={Hq} must be a multiple of Hkv={Hkv}")
+    for name, t in (("q", q), ("k", k), ("v", v), ("o", o), ("dq", dq), ("dk", dk), ("dv", dv)):
+        if t is not None and t.stride(3) != 1:
+            raise ValueError(f"{name} must have unit stride along head_dim")
+        if t is not None and t.dtype != q.dtype:
+            raise ValueError(f"{name} dtype {t.dtype} != q dtype {q.dtype}")
+    if (causal or window) and Sq != Skv:
+        raise ValueError("causal / windowed attention needs Sq == Skv")
+    desc = _abi.AttnDesc()
+    desc.B, desc.Sq, desc.Skv, desc.Hq, desc.Hkv, desc.d = B, Sq, Skv, Hq, Hkv, d
+    desc.q_sb, desc.q_ss, desc.q_sh = q.stride(0), q.stride(1), q.stride(2)
+    desc.k_sb, desc.k_ss, desc.k_sh = k.stride(0), k.stride(1), k.stride(2)
+    desc.v_sb, desc.v_ss, desc.v_sh = v.stride(0), v.stride(1), v.stride(2)
+    if o is not None:
+        desc.o_sb, desc.o_ss, desc.o_sh = o.stride(0), o.stride(1), o.stride(2)
+    for pre, t in (("dq", dq), ("dk", dk), ("dv", dv)):
+        if t is not None:
+            setattr(desc, pre + "_sb", t.stride(0))
+            setattr(desc, pre + "_ss", t.stride(1))
+            setattr(desc, pre + "_sh", t.stride(2))
+    desc.scale = float(scale)
+    desc.causal = int(bool(causal))
+    desc.window = int(window or 0)
+    desc.dtype = dtype_code(q.dtype)
+    return desc
+
+
+def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool = True,
+             window: int = 0, scale: float | None = None, out: torch.Tensor | None = None):
+    """Flash attention forward on [B,S,H,d] views.  Returns (o, lse) with o
+    [B,Sq,Hq,d] (contiguous unless ``out`` is given) and lse fp32 [B,Hq,Sq]."""
+    dev = _require_gpu(q, k, v, out)
+    B, Sq, Hq, d = q.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if out is None:
+        out = torch.empty(B, Sq, Hq, d, device=dev, dtype=q.dtype)
+    elif out.shape != (B, Sq, Hq, d):
+        raise ValueError("out has the wrong shape")
+    desc = _attn_desc(q, k, v, out, scale, causal, window)
+    lse = torch.empty(B, Hq, Sq, device=dev, dtype=torch.float32)
+    check(lib().zk_attn_fwd(desc, ptr(q), ptr(k), ptr(v), ptr(out), ptr(lse),
+                            stream_handle(dev)), "zk_attn_fwd")
+    return out, lse
+
+
+def attn_bwd(q, k, v, o, do, lse, *, causal: bool = True, window: int = 0,
+             scale: float | None = None, dq=None, dk=None, dv=None):
+    """Flash attention backward.  Returns (dq, dk, dv); outputs may be given
+    as (strided) views, e.g. slices of one fused [T, (Hq+2Hkv) d] buffer."""
+    dev = _require_gpu(q, k, v, o, do, lse, dq, dk, dv)
+    d = q.shape[3]
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if do.shape != o.shape or do.stride() != o.stride():
+        raise ValueError("dO must have the same shape and strides as O")
+    if lse.dtype != torch.float32 or lse.shape != (q.shape[0], q.shape[2], q.shape[1]) \
+            or not lse.is_contiguous():
+        raise ValueError("lse must be contiguous fp32 [B, Hq, Sq]")
+    dq = torch.empty_like(q, memory_format=torch.contiguous_format) if dq is None else dq
+    dk = torch.empty_like(k, memory_format=torch.contiguous_format) if dk is None else dk
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format) if dv is None else dv
+    if dq.shape != q.shape or dk.shape != k.shape or dv.shape != v.shape:
+        raise ValueError("gradient buffers have the wrong shape")
+    desc = _attn_desc(q, k, v, o, scale, causal, window, dq, dk, dv)
+    nbytes = lib().zk_attn_bwd_workspace(desc)
+    ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
+    check(lib().zk_attn_bwd(desc, ptr(q), ptr(k), ptr(v), ptr(o), ptr(do), ptr(lse),
+                            ptr(dq), ptr(dk), ptr(dv), ptr(ws), nbytes,
+                            stream_handle(dev)), "zk_attn_bwd")
+    return dq, dk, dv
+
+
+# ------------------------------------------------------------------ AdamW --
+
+def adamw_step(param: torch.Tensor, grad: torch.Tensor, exp_avg: torch.Tensor,
+               exp_avg_sq: torch.Tensor, *, lr: float, beta1: float, beta2: float,
+               eps: float, weight_decay: float, step: int,
+               lowp_out: torch.Tensor | None = None) -> None:
+    """One fused AdamW update of a flat fp32 shard (in place)."""
+    dev = _require_gpu(param, grad, exp_avg, exp_avg_sq, lowp_out)
+    n = param.numel()
+    for name, t in (("param", param), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq)):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != n:
+            raise ValueError(f"{name} must be contiguous fp32 with {n} elements")
+    if grad.numel() != n or not grad.is_contiguous():
+        raise ValueError("grad must be contiguous with the same number of elements")
+    if lowp_out is not None and (lowp_out.numel() != n or not lowp_out.is_contiguous()):
+        raise ValueError("lowp_out must be contiguous with the same number of elements")
+    check(lib().zk_adamw_step(ptr(param), ptr(grad), dtype_code(grad.dtype), ptr(exp_avg),
+                              ptr(exp_avg_sq), ptr(lowp_out),
+                              dtype_code(lowp_out.dtype) if lowp_out is not None else 0,
+                              n, float(lr), float(beta1), float(beta2), float(eps),
+                              float(weight_decay), int(step), stream_handle(dev)),
+          "zk_adamw_step")
+
+
+def cast_(src: torch.Tensor, dst: torch.Tensor, accumulate: bool = False) -> torch.Tensor:
+    """dst = round(src) (or dst = round(dst + src)); contiguous, same numel."""
+    dev = _require_gpu(src, dst)
+    if src.numel() != dst.numel() or not src.is_contiguous() or not dst.is_contiguous():
+        raise ValueError("cast_ needs contiguous tensors of equal size")
+    check(lib().zk_cast(ptr(src), dtype_code(src.dtype), ptr(dst), dtype_code(dst.dtype),
+                        src.numel(), int(accumulate), stream_handle(dev)), "zk_cast")
+    return dst
+
+
+def device_info(device: int = 0) -> dict:
+    import ctypes
+    arch = ctypes.create_string_buffer(64)
+    cus, clk, mem = ctypes.c_int(), ctypes.c_int(), ctypes.c_int64()
+    check(lib().zk_device_info(device, arch, 64, ctypes.byref(cus), ctypes.byref(clk),
+                               ctypes.byref(mem)), "zk_device_info")
+    return {"arch": arch.value.decode(), "num_cus": cus.value,
+            "max_clock_khz": clk.value, "hbm_bytes": mem.value}
