@@ -1,0 +1,261 @@
+"""Benchmark of the decoder-layer hot path on one MI355X.
+
+Workload: a Llama-2-7B-shaped pipeline stage of 8
+decoder layers (hidden 4096, 32 heads x 128, FFN 11008, RoPE theta 1e4),
+micro-batch 1, seq 4096, bf16 compute with fp32 master weights; one step =
+forward through the 8 layers, backward, and the fused AdamW (lr 1e-4, betas
+0.9 / 0.95, wd 0.1) applied to each layer's flat shard inside the backward
+on the optimizer stream, as the reference's --optimizer_in_backwards path
+does.  Inputs are synthetic (seeded N(0,1) activations and upstream grads,
+N(0, 0.02) weights) and resident in HBM before the timed region.
+
+value = decoder-layer fwd+bwd tokens/s = layers * B * S / (time per stage
+step), the per-layer throughput the reference's profiler reports
+(data/model_latencies.json).  The JSON line also carries the attention
+kernels' TFLOP/s against the MFMA peak, the HBM-bound kernels' GB/s, and the
+CPU oracle timed on a bounded sample.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+MFMA_BF16_PEAK_TFLOPS = 2516.6   # MI355X dense bf16 (256 CU x 4096 FLOP/clk x 2.4 GHz)
+HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
+H100_FP16_LAYER_TOKS = 221_477   # data/model_latencies.json:7551, 7B layer seq 4096 fp16
+
+
+def _events_time(fn, iters: int, warm: int = 2) -> float:
+    """Average milliseconds per call of ``fn`` between HIP events recorded on
+    torch's current stream (the stream every kernel here is launched on)."""
+    for _ in range(warm):
+        fn()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(iters):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def build_stage(n_layers, dev, seed=3):
+    from zorse_amd import llama_simple as L
+    cfg = L.llama_config(hidden_size=4096, num_attention_heads=32, intermediate_size=11008,
+                         rope_theta=1e4, max_position_embeddings=4096)
+    g = torch.Generator().manual_seed(seed)
+    layers = []
+    for i in range(n_layers):
+        with torch.device("meta"):
+            layer = L.LlamaDecoderLayer(cfg, i, torch.bfloat16, param_dtype=torch.bfloat16)
+        layer.flat_param = torch.nn.Parameter(
+            torch.empty(layer.spec.numel, dtype=torch.bfloat16, device=dev))
+        # N(0, 0.02) linear weights drawn on the device from a seeded generator
+        gd = torch.Generator(device=dev).manual_seed(seed * 1000 + i)
+        with torch.no_grad():
+            layer.flat_param.normal_(0.0, 0.02, generator=gd)
+            layer.param_view("ln1").fill_(1.0)
+            layer.param_view("ln2").fill_(1.0)
+        layers.append(layer)
+    return cfg, layers, g
+
+
+def measure_kernels(dev, spec, S):
+    """Live HIP-event timings of the hand-written kernels at the stage's
+    shapes.  HBM-bound kernels rotate through enough buffers that the working
+    set exceeds the 256 MB Infinity Cache."""
+    from zorse_amd import flops
+    from zorse_amd import kernels as K
+    torch.manual_seed(0)
+    B, H, d, h = 1, spec.heads, spec.head_dim, spec.hidden
+    q = torch.randn(B, S, H, d, device=dev, dtype=torch.bfloat16)
+    k = torch.randn(B, S, H, d, device=dev, dtype=torch.bfloat16)
+    v = torch.randn(B, S, H, d, device=dev, dtype=torch.bfloat16)
+    do = torch.randn(B, S, H, d, device=dev, dtype=torch.bfloat16)
+    o, lse = K.attn_fwd(q, k, v)
+    t_fwd = _events_time(lambda: K.attn_fwd(q, k, v, out=o), 20)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    t_bwd = _events_time(lambda: K.attn_bwd(q, k, v, o, do, lse, dq=dq, dk=dk, dv=dv), 10)
+    f_fwd = flops.attn_fwd_flops(B, H, d, S, S, True, 0)
+    f_bwd = flops.attn_bwd_flops(B, H, d, S, S, True, 0)
+    del q, k, v, do, o, dq, dk, dv
+
+    T = B * S
+    nbuf = 8
+    xs = [torch.randn(T, h, device=dev, dtype=torch.bfloat16) for _ in range(nbuf)]
+    w = torch.ones(h, device=dev, dtype=torch.bfloat16)
+    ys = [torch.empty_like(x) for x in xs]
+    rs = [torch.empty(T, device=dev, dtype=torch.float32) for _ in xs]
+    it = [0]
+
+    def rms_fwd():
+        i = it[0] % nbuf
+        it[0] += 1
+        K.rmsnorm_fwd(xs[i], w, 1e-6, out=(ys[i], rs[i]))
+    t_rms = _events_time(rms_fwd, 4 * nbuf, warm=nbuf)
+    dxs = ys
+    ws = torch.empty(K.rmsnorm_bwd_workspace_elems(T, h), device=dev, dtype=torch.float32)
+    dw = torch.empty(h, device=dev, dtype=torch.bfloat16)
+
+    def rms_bwd():
+        i = it[0] % nbuf
+        it[0] += 1
+        j = (i + 1) % nbuf
+        K.rmsnorm_bwd(xs[j], xs[i], w, rs[i], dw=dw, out=dxs[(i + 2) % nbuf], workspace=ws)
+    t_rms_b = _events_time(rms_bwd, 4 * nbuf, warm=nbuf)
+    del xs, ys, rs, ws
+
+    n = spec.numel
+    p = torch.randn(n, device=dev)
+    m = torch.zeros(n, device=dev)
+    vv = torch.zeros(n, device=dev)
+    gr = torch.randn(n, device=dev, dtype=torch.bfloat16)
+    lowp = torch.empty(n, device=dev, dtype=torch.bfloat16)
+    step = [0]
+
+    def adam():
+        step[0] += 1
+        K.adamw_step(p, gr, m, vv, lr=1e-4, beta1=0.9, beta2=0.95, eps=1e-8,
+                     weight_decay=0.1, step=step[0], lowp_out=lowp)
+    t_adam = _events_time(adam, 5)
+    del p, m, vv, gr, lowp
+
+    def rf(name, bound, achieved, peak, unit, ms, work):
+        return {"kernel": name, "bound": bound, "achieved": round(achieved, 1),
+                "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
+                "avg_ms": round(ms, 4), "work_per_launch": work}
+
+    out = {
+        "attn_fwd": rf("attn_fwd_kernel<bf16,128>", "mfma", f_fwd / t_fwd / 1e9,
+                       MFMA_BF16_PEAK_TFLOPS, "TFLOP/s", t_fwd, f_fwd),
+        "attn_bwd": rf("zk_attn_bwd (prep + attn_bwd_kernel<bf16,128> + dq store)", "mfma",
+                       f_bwd / t_bwd / 1e9, MFMA_BF16_PEAK_TFLOPS, "TFLOP/s", t_bwd, f_bwd),
+        "rmsnorm_fwd": rf("rmsnorm_fwd_vec<bf16,bf16,128>", "hbm",
+                          flops.rmsnorm_fwd_bytes(T, h) / t_rms / 1e6, HBM_PEAK_GBS, "GB/s",
+                          t_rms, flops.rmsnorm_fwd_bytes(T, h)),
+        "rmsnorm_bwd": rf("rmsnorm_bwd_vec<bf16,bf16,128> + dw reduce", "hbm",
+                          flops.rmsnorm_bwd_bytes(T, h) / t_rms_b / 1e6, HBM_PEAK_GBS, "GB/s",
+                          t_rms_b, flops.rmsnorm_bwd_bytes(T, h)),
+        "adamw": rf("adamw_vec4<bf16,bf16,true>", "hbm",
+                    flops.adamw_bytes(n, 2, True) / t_adam / 1e6, HBM_PEAK_GBS, "GB/s",
+                    t_adam, flops.adamw_bytes(n, 2, True)),
+    }
+    return out
+
+
+def cpu_baseline(spec, S, seed=3):
+    """The CPU oracle (plain PyTorch, fp32) timed on one layer's fwd+bwd at the
+    stage's shape -- a bounded sample (1 of the 8 layers, 1 iteration after a
+    short warm-up) of the same workload, on the host's cores."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import decoder as O
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    shape = O.LayerShape(hidden=spec.hidden, heads=spec.heads, kv_heads=spec.kv_heads,
+                         head_dim=spec.head_dim, ffn=spec.ffn, theta=spec.rope_theta)
+    g = torch.Generator().manual_seed(seed)
+    p = O.init_params(shape, g)
+    warm_x = torch.randn(1, 128, spec.hidden, generator=g)
+    O.layer_fwd_bwd(warm_x, p, shape, torch.randn_like(warm_x))
+    x = torch.randn(1, S, spec.hidden, generator=g)
+    dout = torch.randn(1, S, spec.hidden, generator=g)
+    t0 = time.perf_counter()
+    O.layer_fwd_bwd(x, p, shape, dout)
+    dt = time.perf_counter() - t0
+    return {"value": round(S / dt, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle (plain PyTorch fp32) fwd+bwd of 1 of the 8 layers at seq {S}, "
+                      f"1 timed iteration ({dt:.2f} s) on {threads} host threads",
+            "seconds": round(dt, 2)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=8)
+    ap.add_argument("--seq", type=int, default=4096)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(collectives and sharding are out of scope); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    from zorse_amd import flops
+    from zorse_amd.stage import StageRunner
+
+    S, B = args.seq, 1
+    cfg, layers, g = build_stage(args.layers, dev)
+    spec = layers[0].spec
+    runner = StageRunner(layers, lr=1e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+    x = torch.randn(B, S, spec.hidden, generator=g).to(torch.bfloat16).to(dev)
+    dout = torch.randn(B, S, spec.hidden, generator=g).to(torch.bfloat16).to(dev)
+    x.requires_grad_(False)
+
+    for i in range(args.warmup):
+        runner.step(x, dout)
+        print(f"warmup step {i + 1}/{args.warmup} done", file=sys.stderr, flush=True)
+    runner.wait_optimizer()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        runner.step(x, dout)
+    runner.wait_optimizer()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_step = 1e3 * elapsed / args.steps
+    print(f"timed {args.steps} steps: {ms_step:.2f} ms/step", file=sys.stderr, flush=True)
+    layer_toks = args.layers * B * S / (ms_step / 1e3)
+    layer_tflops = flops.layer_fwd_bwd_flops(spec, B, S) * args.layers / (ms_step / 1e3) / 1e12
+    del runner, layers, x, dout
+    torch.cuda.empty_cache()
+
+    kern = measure_kernels(dev, spec, S)
+    print("kernel timings done", file=sys.stderr, flush=True)
+    cpu = None if args.no_cpu else cpu_baseline(spec, S)
+    a = kern["attn_fwd"]
+    line = {
+        "metric": "decoder-layer fwd+bwd tokens/s at 1 GPU; attention TFLOP/s vs MFMA peak",
+        "value": round(layer_toks, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(layer_toks / H100_FP16_LAYER_TOKS, 3),
+        "vs_baseline_ref": "H100-NVL fp16 7B layer seq 4096 mb 1, 221,477 tok/s/layer "
+                           "(data/model_latencies.json:7551; other GPU and dtype, no AdamW)",
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations / grads, N(0,0.02) weights)",
+        "config": {"workload": "llama2-7b-shaped pipeline stage fwd+bwd + per-layer AdamW in "
+                               "backward (BASELINE configs[3])",
+                   "layers": args.layers, "hidden": spec.hidden, "heads": spec.heads,
+                   "head_dim": spec.head_dim, "ffn": spec.ffn, "micro_batch": B, "seq_len": S,
+                   "global_batch": B, "parallelism": "none (1 GPU)",
+                   "stage_tokens_per_s": round(B * S / (ms_step / 1e3), 1),
+                   "layer_fwd_bwd_tflops": round(layer_tflops, 1)},
+        "roofline": {"bound": "mfma", "achieved": a["achieved"], "peak": a["peak"],
+                     "unit": "TFLOP/s", "frac": a["frac"], "traffic": None,
+                     "kernel": a["kernel"], "avg_ms": a["avg_ms"]},
+        "kernels": kern,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,171 @@
+"""CPU checks of the C-ABI boundary and host logic (no kernel launches).
+
+* libzorse_amd.so loads and exports every entry point include/zorse_amd.h
+  declares, with the ctypes table matching the header;
+* the library's own argument validation rejects bad input with the
+  documented status codes and messages (these return before any HIP call);
+* the Python wrappers reject CPU tensors and bad shapes with ValueError;
+* the drop-in modules keep the reference's names and parameter counts.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "zorse_amd.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(zk_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from zorse_amd import _abi
+    if not os.path.exists(_abi.LIB_PATH):
+        pytest.fail("libzorse_amd.so is not built: run python -m zorse_amd.build")
+    return _abi.lib()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from zorse_amd import _abi
+    declared = _declared()
+    assert declared, "no entry points parsed from the header"
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in zorse_amd.h but not exported"
+    assert sorted(_abi.SIGNATURES) == declared
+
+
+def test_abi_version_and_error_text(lib):
+    assert lib.zk_abi_version() >= 1
+    rc = lib.zk_rmsnorm_fwd(None, None, None, None, None, None, 4, 8, 1e-6, 7, 0, None)
+    assert rc == -2  # ZK_EDTYPE
+    assert b"dtype" in lib.zk_last_error()
+
+
+def test_validation_codes(lib):
+    from zorse_amd import _abi
+    # null pointers
+    assert lib.zk_rmsnorm_fwd(None, None, None, None, None, None, 4, 8, 1e-6, 2, 0, None) == -1
+    # residual without h_out
+    p = ctypes.c_void_p(16)
+    assert lib.zk_rmsnorm_fwd(p, p, None, p, p, p, 4, 8, 1e-6, 2, 0, None) == -1
+    # workspace too small
+    assert lib.zk_rmsnorm_bwd(p, p, p, p, None, p, p, 0, p, 1, 64, 128, 2, 0, None) == -5
+    # AdamW: step 0 and bad betas
+    assert lib.zk_adamw_step(p, p, 0, p, p, None, 0, 8, 1e-3, 0.9, 0.999, 1e-8, 0.0, 0, None) == -1
+    assert lib.zk_adamw_step(p, p, 0, p, p, None, 0, 8, 1e-3, 1.0, 0.999, 1e-8, 0.0, 1, None) == -1
+    # attention: head_dim 96 unsupported on the MFMA path; Hq not multiple of Hkv
+    d = _abi.AttnDesc(B=1, Sq=8, Skv=8, Hq=4, Hkv=4, d=96, scale=0.1, causal=1, window=0,
+                      dtype=_abi.ZK_BF16)
+    for f in ("q", "k", "v", "o"):
+        setattr(d, f + "_sb", 8 * 4 * 96); setattr(d, f + "_ss", 4 * 96); setattr(d, f + "_sh", 96)
+    assert lib.zk_attn_fwd(ctypes.byref(d), p, p, p, p, p, None) == -4
+    d.d, d.Hkv = 128, 3
+    assert lib.zk_attn_fwd(ctypes.byref(d), p, p, p, p, p, None) == -1
+    d.Hkv, d.Sq = 4, 9
+    assert lib.zk_attn_fwd(ctypes.byref(d), p, p, p, p, p, None) == -4  # causal, Sq != Skv
+    # swiglu bad ld, rope odd head dim, cast bad dtype
+    assert lib.zk_swiglu_fwd(p, p, 4, p, 8, 2, 8, 2, None) == -1
+    assert lib.zk_rope(p, 0, 0, 0, None, 0, 0, 0, 1, 1, 1, 0, 7, p, p, 1, None, 0, 0, 2, None) == -1
+    assert lib.zk_cast(p, 5, p, 0, 8, 0, None) == -2
+
+
+def test_wrappers_reject_cpu_tensors():
+    from zorse_amd import kernels as K
+    x = torch.zeros(4, 8)
+    with pytest.raises(ValueError):
+        K.rmsnorm_fwd(x, torch.ones(8), 1e-6)
+    with pytest.raises(ValueError):
+        K.attn_fwd(torch.zeros(1, 8, 2, 64), torch.zeros(1, 8, 2, 64), torch.zeros(1, 8, 2, 64))
+    with pytest.raises(ValueError):
+        K.adamw_step(torch.zeros(8), torch.zeros(8), torch.zeros(8), torch.zeros(8), lr=1e-3,
+                     beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0, step=1)
+
+
+def test_dropin_names_and_counts():
+    from zorse_amd import llama_simple
+    from oracle import decoder as O
+    cfg = llama_simple.llama_config(hidden_size=64, intermediate_size=96, num_attention_heads=4,
+                                    num_key_value_heads=2)
+    layer = llama_simple.LlamaDecoderLayer(cfg, 0)
+    params = list(layer.parameters())
+    assert len(params) == 1 and params[0] is layer.flat_param
+    shape = O.LayerShape(hidden=64, heads=4, kv_heads=2, head_dim=16, ffn=96)
+    assert layer.flat_param.numel() == O.flat_numel(shape)
+    assert layer.self_attn.q_proj.weight.shape == (64, 64)
+    assert layer.self_attn.k_proj.weight.shape == (32, 64)
+    assert layer.mlp.down_proj.weight.shape == (64, 96)
+    assert torch.equal(layer.input_layernorm.weight, torch.ones(64))
+    # views alias the flat parameter in registration order
+    names = [n for n, _ in layer.orig_named_parameters()]
+    assert names[0] == "self_attn.q_proj.weight" and names[-1] == "post_attention_layernorm.weight"
+    flat = torch.cat([t.reshape(-1) for _, t in layer.orig_named_parameters()])
+    assert torch.equal(flat, layer.flat_param.detach())
+    with torch.no_grad():
+        layer.self_attn.v_proj.weight.fill_(3.0)
+    a, b = layer._offsets["v"]
+    assert torch.all(layer.flat_param[a:b] == 3.0)
+    # the 7B and tiny layers hold the reference's per-layer parameter counts
+    # (data/model_stats.json:92,104), counted without allocating weights
+    for name, numel in (("deepspeedllama_7b", 202_383_360), ("deepspeedllama_tiny", 51_384_320)):
+        hidden, inter, _, heads = llama_simple.MODEL_SHAPES[name]
+        spec = llama_simple.spec_from_config(llama_simple.llama_config(
+            hidden_size=hidden, intermediate_size=inter, num_attention_heads=heads))
+        assert spec.numel == numel
+
+
+def test_get_model_structure():
+    from zorse_amd import llama_simple
+    with torch.device("meta"):
+        model = llama_simple.get_model("deepspeedllama_7b", vocab_size=128, seq_length=64,
+                                       layers=2, insert_noop=True)
+    assert model._hidden_size == 4096
+    assert len(model.layers) == 4  # Block, NoOp, Block, NoOp
+    blk = model.layers[0]
+    assert isinstance(blk.block, llama_simple.LlamaDecoderLayer)
+    assert blk.block.flat_param.numel() == 202_383_360
+    assert blk.block.spec.window == 0
+    parts = model.join_layers()
+    assert parts[0] is model.embed_tokens and parts[-1] is model.output_layer
+
+
+def test_mistral_defaults():
+    from zorse_amd import mistral_simple
+    with torch.device("meta"):
+        model = mistral_simple.get_model("deepspeedmistral_toy", vocab_size=128, seq_length=64,
+                                         layers=1)
+    spec = model.layers[0].block.spec
+    assert (spec.heads, spec.kv_heads, spec.head_dim, spec.ffn) == (32, 8, 128, 14336)
+    assert spec.window == 4096 and spec.causal
+    assert model._hidden_size == 4096
+    assert model.layers[0].block.flat_param.numel() == 218_112_000
+
+
+def test_fused_adamw_validation():
+    from zorse_amd.optim import FusedAdam, FusedAdamW
+    p = torch.nn.Parameter(torch.zeros(4))
+    with pytest.raises(ValueError):
+        FusedAdamW([p], betas=(1.0, 0.9))
+    with pytest.raises(ValueError):
+        FusedAdam([p], weight_decay=0.1)
+    opt = FusedAdamW([p], lr=1e-4, weight_decay=0.1)
+    assert opt.param_groups[0]["weight_decay"] == 0.1
+
+
+def test_flop_and_byte_counts_match_survey_table():
+    from zorse_amd import flops
+    # attention fwd FLOPs (4 B Hq d P)
+    assert round(flops.attn_fwd_flops(8, 32, 128, 2048, 2048, True, 0) / 1e9, 1) == 275.0
+    assert round(flops.attn_fwd_flops(1, 32, 128, 4096, 4096, True, 0) / 1e9, 1) == 137.5
+    assert round(flops.attn_fwd_flops(1, 32, 128, 8192, 8192, True, 4096) / 1e9, 1) == 412.4
+    # GEMM work of one 7B layer fwd+bwd (with attention): 5.455 TF
+    from zorse_amd.layer import LayerSpec
+    spec = LayerSpec(hidden=4096, heads=32, kv_heads=32, head_dim=128, ffn=11008)
+    assert round(flops.layer_fwd_bwd_flops(spec, 1, 4096) / 1e12, 3) == 5.455
+    assert flops.adamw_bytes(202_383_360, 4, False) == 28 * 202_383_360

@@ -1,0 +1,308 @@
+"""GPU parity of each kernel against the CPU oracle, through the C ABI.
+
+Inputs are drawn on the CPU from seeded generators, rounded to the storage
+dtype and copied to the GPU; the oracle runs in fp64 on the same rounded
+values.  Shapes cover the vector and scalar code paths, ragged sizes, GQA,
+causal / sliding-window / unmasked attention and both RoPE pairings.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import decoder as O
+from tests._tol import assert_close
+
+pytestmark = pytest.mark.gpu
+
+LOWP = (torch.bfloat16, torch.float16)
+ALL = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def _rand(shape, dtype, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (scale * torch.randn(shape, generator=g)).to(dtype)
+
+
+# ---------------------------------------------------------------- RMSNorm --
+
+RMS_SHAPES = [(1, 256), (37, 2048), (64, 4096), (3, 100), (5, 8200), (300, 688)]
+
+
+@pytest.mark.parametrize("rows,hidden", RMS_SHAPES)
+@pytest.mark.parametrize("dtype", ALL)
+def test_rmsnorm_fwd_bwd(dev, rows, hidden, dtype):
+    from zorse_amd import kernels as K
+    print(f"rmsnorm rows={rows} hidden={hidden} {dtype}", flush=True)
+    x = _rand((rows, hidden), dtype, 1)
+    res = _rand((rows, hidden), dtype, 2)
+    w = (1 + 0.1 * torch.randn(hidden, generator=torch.Generator().manual_seed(3))).to(dtype)
+    dy = _rand((rows, hidden), dtype, 4)
+    for with_res in (False, True):
+        y, rstd, h = K.rmsnorm_fwd(x.to(dev), w.to(dev), 1e-6,
+                                   residual=res.to(dev) if with_res else None)
+        href = (x.double() + res.double()).to(dtype) if with_res else x
+        if with_res:
+            assert torch.equal(h.cpu(), href)   # rounded residual sum: bit-exact
+        ref = O.rmsnorm(href.double(), w.double(), 1e-6)
+        assert_close(y, ref, dtype, "y")
+        assert_close(rstd, O.rmsnorm_rstd(href.double(), 1e-6), torch.float32, "rstd")
+        dres = _rand((rows, hidden), dtype, 5) if with_res else None
+        dx, dw = K.rmsnorm_bwd(dy.to(dev), h, w.to(dev), rstd,
+                               dres=dres.to(dev) if with_res else None)
+        rdx, rdw = O.rmsnorm_bwd(dy.double(), href.double(), w.double(), 1e-6)
+        if with_res:
+            rdx = rdx + dres.double()
+        assert_close(dx, rdx, dtype, "dx")
+        assert_close(dw, rdw, dtype, "dw")
+
+
+def test_rmsnorm_dw_accumulate_and_fp32_weight(dev):
+    from zorse_amd import kernels as K
+    x = _rand((33, 512), torch.bfloat16, 6).to(dev)
+    w = torch.ones(512, dtype=torch.float32, device=dev)
+    y, rstd, _ = K.rmsnorm_fwd(x, w, 1e-6)
+    dy = _rand((33, 512), torch.bfloat16, 7).to(dev)
+    _, dw1 = K.rmsnorm_bwd(dy, x, w, rstd)
+    acc = dw1.clone()
+    K.rmsnorm_bwd(dy, x, w, rstd, dw=acc, accumulate=True)
+    assert torch.allclose(acc, 2 * dw1, rtol=1e-6, atol=1e-6)
+    assert dw1.dtype == torch.float32
+
+
+# ----------------------------------------------------------------- SwiGLU --
+
+@pytest.mark.parametrize("rows,cols", [(64, 688), (128, 1024), (7, 13)])
+@pytest.mark.parametrize("dtype", ALL)
+def test_swiglu_fwd_bwd(dev, rows, cols, dtype):
+    from zorse_amd import kernels as K
+    print(f"swiglu rows={rows} cols={cols} {dtype}", flush=True)
+    gu = _rand((rows, 2 * cols), dtype, 8, 2.0)
+    dz = _rand((rows, cols), dtype, 9)
+    gu_d = gu.to(dev)
+    g, u = gu_d[:, :cols], gu_d[:, cols:]
+    z = K.swiglu_fwd(g, u)
+    gr, ur = gu[:, :cols].double(), gu[:, cols:].double()
+    assert_close(z, O.swiglu(gr, ur), dtype, "z")
+    dgu = torch.empty_like(gu_d)
+    K.swiglu_bwd(dz.to(dev), g, u, dgu[:, :cols], dgu[:, cols:])
+    rdg, rdu = O.swiglu_bwd(dz.double(), gr, ur)
+    assert_close(dgu[:, :cols], rdg, dtype, "dg")
+    assert_close(dgu[:, cols:], rdu, dtype, "du")
+
+
+# ------------------------------------------------------------------- RoPE --
+
+@pytest.mark.parametrize("d,theta", [(64, 5e5), (128, 1e4), (128, 1e6)])
+@pytest.mark.parametrize("dtype", ALL)
+def test_rope_half(dev, d, theta, dtype):
+    from zorse_amd import kernels as K
+    from zorse_amd.functional import rope_tables
+    B, S, Hq, Hkv = 2, 77, 4, 2
+    q = _rand((B, S, Hq, d), dtype, 10)
+    k = _rand((B, S, Hkv, d), dtype, 11)
+    cos, sin = rope_tables(S, d, theta, dtype, dev)
+    qd, kd = q.to(dev), k.to(dev)
+    K.rope_(qd, kd, cos, sin)
+    c, s = O.rope_cos_sin(S, d, theta, dtype)
+    rq, rk = O.apply_rope_half(q, k, c, s)   # the reference's op sequence in dtype
+    if dtype in LOWP:
+        assert torch.equal(qd.cpu(), rq) and torch.equal(kd.cpu(), rk)
+    else:
+        assert_close(qd, rq, dtype, "q")
+        assert_close(kd, rk, dtype, "k")
+    # inverse == gradient of the rotation (fp64 autograd on the oracle)
+    gq = _rand((B, S, Hq, d), dtype, 12)
+    gk = _rand((B, S, Hkv, d), dtype, 13)
+    qa = q.double().requires_grad_(True)
+    ka = k.double().requires_grad_(True)
+    c64, s64 = c.double(), s.double()
+    oq, ok = O.apply_rope_half(qa, ka, c64, s64)
+    torch.autograd.backward([oq, ok], [gq.double(), gk.double()])
+    gqd, gkd = gq.to(dev), gk.to(dev)
+    K.rope_(gqd, gkd, cos, sin, inverse=True)
+    assert_close(gqd, qa.grad, dtype, "dq")
+    assert_close(gkd, ka.grad, dtype, "dk")
+
+
+@pytest.mark.parametrize("dtype", ALL)
+def test_rope_interleaved(dev, dtype):
+    from zorse_amd import kernels as K
+    from zorse_amd.functional import rope_tables
+    B, S, H, d = 1, 50, 3, 64
+    q = _rand((B, S, H, d), dtype, 14)
+    k = _rand((B, S, 1, d), dtype, 15)
+    cos, sin = rope_tables(S, d, 1e4, dtype, dev, interleaved=True)
+    qd, kd = q.to(dev), k.to(dev)
+    K.rope_(qd, kd, cos, sin, interleaved=True)
+    rq, rk = O.apply_rope_interleaved(q.double(), k.double(), O.rope_freqs_cis(d, S, 1e4))
+    assert_close(qd, rq, dtype, "q")
+    assert_close(kd, rk, dtype, "k")
+    K.rope_(qd, kd, cos, sin, interleaved=True, inverse=True)
+    assert_close(qd, q.double(), dtype, "inverse(q)")
+
+
+# -------------------------------------------------------------- attention --
+
+ATTN_CASES = [
+    # B, S, Hq, Hkv, d, causal, window, dtype
+    (2, 128, 4, 4, 64, True, 0, torch.bfloat16),
+    (1, 200, 8, 2, 128, True, 0, torch.float16),
+    (1, 256, 4, 1, 128, True, 64, torch.bfloat16),
+    (1, 333, 2, 2, 64, True, 100, torch.float16),
+    (2, 64, 2, 2, 64, False, 0, torch.bfloat16),
+    (1, 1, 2, 2, 128, True, 0, torch.bfloat16),
+    (1, 130, 4, 2, 128, True, 1, torch.bfloat16),
+    (1, 50, 2, 1, 16, True, 0, torch.float32),
+    (1, 90, 4, 2, 64, True, 30, torch.float32),
+]
+
+
+def _ids(c):
+    return "B{}S{}H{}x{}d{}{}w{}{}".format(c[0], c[1], c[2], c[3], c[4], "c" if c[5] else "n",
+                                          c[6], str(c[7]).split(".")[-1])
+
+
+@pytest.mark.parametrize("case", ATTN_CASES, ids=[_ids(c) for c in ATTN_CASES])
+def test_attention_fwd_bwd(dev, case):
+    from zorse_amd import kernels as K
+    B, S, Hq, Hkv, d, causal, window, dtype = case
+    print(f"attention {_ids(case)}", flush=True)
+    q = _rand((B, S, Hq, d), dtype, 20)
+    k = _rand((B, S, Hkv, d), dtype, 21)
+    v = _rand((B, S, Hkv, d), dtype, 22)
+    do = _rand((B, S, Hq, d), dtype, 23)
+    o, lse = K.attn_fwd(q.to(dev), k.to(dev), v.to(dev), causal=causal, window=window)
+    ro, rlse = O.attention(q.double(), k.double(), v.double(), causal, window)
+    assert_close(o, ro, dtype, "o")
+    assert_close(lse, rlse, torch.float32 if dtype == torch.float32 else dtype, "lse")
+    dq, dk, dv = K.attn_bwd(q.to(dev), k.to(dev), v.to(dev), o, do.to(dev), lse,
+                            causal=causal, window=window)
+    rdq, rdk, rdv = O.attention_bwd(q.double(), k.double(), v.double(), do.double(),
+                                    causal, window)
+    assert_close(dq, rdq, dtype, "dq")
+    assert_close(dk, rdk, dtype, "dk")
+    assert_close(dv, rdv, dtype, "dv")
+
+
+def test_attention_strided_qkv_views(dev):
+    """q / k / v as column slices of one [T, (Hq + 2 Hkv) d] projection output
+    and gradients written into the matching slices (the fused-layer layout)."""
+    from zorse_amd import kernels as K
+    B, S, Hq, Hkv, d = 1, 192, 4, 2, 128
+    dtype = torch.bfloat16
+    qkv = _rand((B * S, (Hq + 2 * Hkv) * d), dtype, 30).to(dev)
+    q = qkv[:, :Hq * d].view(B, S, Hq, d)
+    k = qkv[:, Hq * d:(Hq + Hkv) * d].view(B, S, Hkv, d)
+    v = qkv[:, (Hq + Hkv) * d:].view(B, S, Hkv, d)
+    o, lse = K.attn_fwd(q, k, v)
+    ro, _ = O.attention(q.cpu().double(), k.cpu().double(), v.cpu().double())
+    assert_close(o, ro, dtype, "o")
+    do = _rand((B, S, Hq, d), dtype, 31).to(dev)
+    dqkv = torch.full_like(qkv, float("nan"))
+    dq = dqkv[:, :Hq * d].view(B, S, Hq, d)
+    dk = dqkv[:, Hq * d:(Hq + Hkv) * d].view(B, S, Hkv, d)
+    dv = dqkv[:, (Hq + Hkv) * d:].view(B, S, Hkv, d)
+    K.attn_bwd(q, k, v, o, do, lse, dq=dq, dk=dk, dv=dv)
+    rdq, rdk, rdv = O.attention_bwd(q.cpu().double(), k.cpu().double(), v.cpu().double(),
+                                    do.cpu().double())
+    assert_close(dq, rdq, dtype, "dq")
+    assert_close(dk, rdk, dtype, "dk")
+    assert_close(dv, rdv, dtype, "dv")
+
+
+@pytest.mark.parametrize("dtype", ALL)
+def test_flash_attention_autograd_with_rope(dev, dtype):
+    from zorse_amd.functional import flash_attention
+    B, S, Hq, Hkv, d, theta = 1, 96, 4, 2, 64, 1e4
+    q = _rand((B, S, Hq, d), dtype, 40)
+    k = _rand((B, S, Hkv, d), dtype, 41)
+    v = _rand((B, S, Hkv, d), dtype, 42)
+    do = _rand((B, S, Hq, d), dtype, 43)
+    qd, kd, vd = (t.to(dev).requires_grad_(True) for t in (q, k, v))
+    out = flash_attention(qd, kd, vd, causal=True, rope_theta=theta)
+    out.backward(do.to(dev))
+    qa, ka, va = (t.double().requires_grad_(True) for t in (q, k, v))
+    c, s = O.rope_cos_sin(S, d, theta, dtype)
+    rq, rk = O.apply_rope_half(qa, ka, c.double(), s.double())
+    ro, _ = O.attention(rq, rk, va)
+    ro.backward(do.double())
+    assert_close(out, ro, dtype, "o")
+    assert_close(qd.grad, qa.grad, dtype, "dq")
+    assert_close(kd.grad, ka.grad, dtype, "dk")
+    assert_close(vd.grad, va.grad, dtype, "dv")
+
+
+# ------------------------------------------------------------------ AdamW --
+
+@pytest.mark.parametrize("gdt", ALL)
+@pytest.mark.parametrize("n", [1_000_003, 4096, 5])
+def test_adamw_kernel_vs_oracle(dev, gdt, n):
+    from zorse_amd import kernels as K
+    g = torch.Generator().manual_seed(50)
+    p0 = torch.randn(n, generator=g)
+    m0 = 0.01 * torch.randn(n, generator=g)
+    v0 = 0.001 * torch.rand(n, generator=g)
+    p, m, v = p0.to(dev), m0.to(dev), v0.to(dev)
+    lowp = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    rp, rm, rv = p0.double(), m0.double(), v0.double()
+    for t in range(3, 6):
+        gr = torch.randn(n, generator=g).to(gdt)
+        K.adamw_step(p, gr.to(dev), m, v, lr=1e-4, beta1=0.9, beta2=0.95, eps=1e-8,
+                     weight_decay=0.1, step=t, lowp_out=lowp)
+        O.adamw_step(rp, gr.double(), rm, rv, t, 1e-4, 0.9, 0.95, 1e-8, 0.1)
+    assert_close(p, rp, torch.float32, "p")
+    assert_close(m, rm, torch.float32, "m")
+    assert_close(v, rv, torch.float32, "v")
+    assert torch.equal(lowp.cpu(), p.cpu().to(torch.bfloat16))
+
+
+def test_fused_adamw_matches_torch_adamw_and_adam(dev):
+    from zorse_amd.optim import FusedAdam, FusedAdamW
+    g = torch.Generator().manual_seed(51)
+    p0 = torch.randn(10_007, generator=g)
+    grads = [torch.randn(10_007, generator=g) for _ in range(4)]
+    for wd, ours_cls, ref_cls in ((0.1, FusedAdamW, torch.optim.AdamW),
+                                  (0.0, FusedAdam, torch.optim.Adam)):
+        a = torch.nn.Parameter(p0.clone().to(dev))
+        b = torch.nn.Parameter(p0.clone().double())
+        kw = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8)
+        oa = ours_cls([a], weight_decay=wd, **kw) if wd else ours_cls([a], **kw)
+        ob = ref_cls([b], weight_decay=wd, foreach=False, **kw)
+        for gr in grads:
+            a.grad = gr.to(dev)
+            b.grad = gr.double()
+            oa.step()
+            ob.step()
+        assert_close(a, b.detach(), torch.float32, f"{ours_cls.__name__}")
+
+
+def test_fused_adamw_mixed_precision_master(dev):
+    """bf16 parameter + bf16 grad: fp32 master, m, v updated and the rounded
+    parameter written back in the same pass."""
+    from zorse_amd.optim import FusedAdamW
+    g = torch.Generator().manual_seed(52)
+    p32 = torch.randn(4099, generator=g)
+    p = torch.nn.Parameter(p32.to(torch.bfloat16).to(dev))
+    opt = FusedAdamW([p], lr=1e-2, betas=(0.9, 0.95), weight_decay=0.1)
+    rp = p32.to(torch.bfloat16).double()
+    rm, rv = torch.zeros_like(rp), torch.zeros_like(rp)
+    for t in range(1, 4):
+        gr = torch.randn(4099, generator=g).to(torch.bfloat16)
+        p.grad = gr.to(dev)
+        opt.step()
+        O.adamw_step(rp, gr.double(), rm, rv, t, 1e-2, 0.9, 0.95, 1e-8, 0.1)
+    master = opt.master_param(p)
+    assert master.dtype == torch.float32
+    assert_close(master, rp, torch.float32, "master")
+    assert torch.equal(p.detach().cpu(), master.cpu().to(torch.bfloat16))
+
+
+def test_cast(dev):
+    from zorse_amd import kernels as K
+    x = _rand((1001,), torch.float32, 60).to(dev)
+    y = torch.zeros(1001, dtype=torch.bfloat16, device=dev)
+    K.cast_(x, y)
+    assert torch.equal(y, x.to(torch.bfloat16))
+    K.cast_(x, y, accumulate=True)
+    assert torch.equal(y, (x.to(torch.bfloat16).float() + x).to(torch.bfloat16))

@@ -43,10 +43,11 @@ def _require_contig(name: str, t: torch.Tensor) -> None:
 # --------------------------------------------------------------- RMSNorm ---
 
 def rmsnorm_fwd(x: torch.Tensor, weight: torch.Tensor, eps: float,
-                residual: torch.Tensor | None = None):
+                residual: torch.Tensor | None = None, out=None):
     """y = w * round(h * rsqrt(mean(h^2) + eps)), h = x (+ residual).
 
-    Returns (y, rstd, h); h is x itself when no residual is given."""
+    Returns (y, rstd, h); h is x itself when no residual is given.  ``out``
+    may supply preallocated (y, rstd) or (y, rstd, h)."""
     dev = _require_gpu(x, weight, residual)
     if x.dtype not in (torch.float32, *_LOWP):
         raise ValueError(f"unsupported activation dtype {x.dtype}")
@@ -56,14 +57,21 @@ def rmsnorm_fwd(x: torch.Tensor, weight: torch.Tensor, eps: float,
     _require_contig("x", x)
     _require_contig("weight", weight)
     rows = x.numel() // hidden if hidden else 0
-    y = torch.empty_like(x)
-    rstd = torch.empty(x.shape[:-1], device=dev, dtype=torch.float32)
+    if out is not None:
+        y, rstd = out[0], out[1]
+        if y.shape != x.shape or y.dtype != x.dtype or not y.is_contiguous():
+            raise ValueError("out y must match x")
+        if rstd.numel() != rows or rstd.dtype != torch.float32 or not rstd.is_contiguous():
+            raise ValueError("out rstd must be contiguous fp32 with one value per row")
+    else:
+        y = torch.empty_like(x)
+        rstd = torch.empty(x.shape[:-1], device=dev, dtype=torch.float32)
     h = x
     if residual is not None:
         if residual.shape != x.shape or residual.dtype != x.dtype:
             raise ValueError("residual must match x in shape and dtype")
         _require_contig("residual", residual)
-        h = torch.empty_like(x)
+        h = out[2] if out is not None and len(out) > 2 else torch.empty_like(x)
     check(lib().zk_rmsnorm_fwd(ptr(x), ptr(residual), ptr(h) if residual is not None else None,
                                ptr(weight), ptr(y), ptr(rstd), rows, hidden, float(eps),
                                dtype_code(x.dtype), dtype_code(weight.dtype),
@@ -71,13 +79,19 @@ def rmsnorm_fwd(x: torch.Tensor, weight: torch.Tensor, eps: float,
     return y, rstd, h
 
 
+def rmsnorm_bwd_workspace_elems(rows: int, hidden: int) -> int:
+    """fp32 elements of scratch zk_rmsnorm_bwd needs (the dw partial rows)."""
+    return max(int(lib().zk_rmsnorm_bwd_workspace(rows, hidden)), 1)
+
+
 def rmsnorm_bwd(dy: torch.Tensor, h: torch.Tensor, weight: torch.Tensor,
                 rstd: torch.Tensor, dres: torch.Tensor | None = None,
                 dw: torch.Tensor | None = None, accumulate: bool = False,
-                dw_dtype: torch.dtype | None = None):
+                dw_dtype: torch.dtype | None = None, out: torch.Tensor | None = None,
+                workspace: torch.Tensor | None = None):
     """Returns (dx, dw).  dx includes dres when given; dw is written (or
     accumulated into) ``dw`` if supplied, else a new tensor of ``dw_dtype``
-    (default: weight dtype)."""
+    (default: weight dtype).  ``out`` / ``workspace`` may be preallocated."""
     dev = _require_gpu(dy, h, weight, rstd, dres, dw)
     hidden = h.shape[-1]
     for name, t in (("dy", dy), ("h", h), ("rstd", rstd), ("weight", weight)):
@@ -96,9 +110,20 @@ def rmsnorm_bwd(dy: torch.Tensor, h: torch.Tensor, weight: torch.Tensor,
         accumulate = False
     elif dw.shape != (hidden,) or not dw.is_contiguous():
         raise ValueError("dw must be a contiguous [hidden] tensor")
-    dx = torch.empty_like(h)
-    ws_elems = lib().zk_rmsnorm_bwd_workspace(rows, hidden)
-    ws = torch.empty(max(ws_elems, 1), device=dev, dtype=torch.float32)
+    if out is not None:
+        if out.shape != h.shape or out.dtype != h.dtype or not out.is_contiguous():
+            raise ValueError("out must match h")
+        dx = out
+    else:
+        dx = torch.empty_like(h)
+    ws_elems = rmsnorm_bwd_workspace_elems(rows, hidden)
+    if workspace is not None:
+        if workspace.dtype != torch.float32 or workspace.numel() < ws_elems or \
+                not workspace.is_contiguous():
+            raise ValueError(f"workspace must be contiguous fp32 with >= {ws_elems} elements")
+        ws = workspace
+    else:
+        ws = torch.empty(ws_elems, device=dev, dtype=torch.float32)
     check(lib().zk_rmsnorm_bwd(ptr(dy), ptr(h), ptr(weight), ptr(rstd), ptr(dres), ptr(dx),
                                ptr(dw), int(accumulate), ptr(ws), ws.numel(), rows, hidden,
                                dtype_code(h.dtype), dtype_code(weight.dtype),

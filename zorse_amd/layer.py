@@ -1,0 +1,197 @@
+"""Fused decoder-layer forward / backward over one flat parameter buffer.
+
+One autograd node per layer: the whole of LlamaDecoderLayer.forward
+(models/llama_simple.py:456-479) -- RMSNorm, the q|k|v projection as ONE GEMM,
+RoPE, flash attention (GQA, causal / sliding window), o_proj with the residual
+add folded into the GEMM (addmm), RMSNorm, gate|up as ONE GEMM, SwiGLU, down
+with the residual folded in -- and its backward, which writes every weight
+gradient straight into one flat gradient buffer laid out like the flat
+parameter (q, k, v, o, gate, up, down, ln1, ln2 -- the registration order the
+reference's FSDP flat parameter uses, zorse_utils/pipeline.py:120-148).
+
+Because q, k, v (and gate, up) are adjacent in that order, the fused
+projection weights are plain views of the flat buffer, and their gradients
+are single GEMMs into adjacent slices: no concatenation, no gradient copies.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import kernels as K
+from .functional import rope_tables
+
+PARAM_ORDER = ("q", "k", "v", "o", "gate", "up", "down", "ln1", "ln2")
+
+
+@dataclass(frozen=True)
+class LayerSpec:
+    hidden: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    ffn: int
+    eps: float = 1e-6
+    rope_theta: float = 1e4
+    causal: bool = True
+    window: int = 0
+    interleaved_rope: bool = False
+
+    def __post_init__(self):
+        if self.heads % self.kv_heads:
+            raise ValueError(f"heads={self.heads} not a multiple of kv_heads={self.kv_heads}")
+        if self.head_dim % 2:
+            raise ValueError("head_dim must be even")
+
+    @property
+    def q_dim(self) -> int:
+        return self.heads * self.head_dim
+
+    @property
+    def kv_dim(self) -> int:
+        return self.kv_heads * self.head_dim
+
+    @property
+    def qkv_dim(self) -> int:
+        return self.q_dim + 2 * self.kv_dim
+
+    def shapes(self) -> dict[str, tuple[int, ...]]:
+        h, F = self.hidden, self.ffn
+        return {"q": (self.q_dim, h), "k": (self.kv_dim, h), "v": (self.kv_dim, h),
+                "o": (h, self.q_dim), "gate": (F, h), "up": (F, h), "down": (h, F),
+                "ln1": (h,), "ln2": (h,)}
+
+    def offsets(self) -> dict[str, tuple[int, int]]:
+        out, off = {}, 0
+        for k, shp in self.shapes().items():
+            n = math.prod(shp)
+            out[k] = (off, off + n)
+            off += n
+        return out
+
+    @property
+    def numel(self) -> int:
+        return sum(math.prod(s) for s in self.shapes().values())
+
+
+class FlatViews:
+    """Named views of a flat buffer laid out as LayerSpec.offsets()."""
+
+    def __init__(self, spec: LayerSpec, flat: torch.Tensor):
+        o = spec.offsets()
+        h, F = spec.hidden, spec.ffn
+
+        def v(a, b, shp):
+            return flat[a:b].view(shp)
+
+        self.qkv = v(o["q"][0], o["v"][1], (spec.qkv_dim, h))
+        self.o = v(*o["o"], (h, spec.q_dim))
+        self.gu = v(o["gate"][0], o["up"][1], (2 * F, h))
+        self.down = v(*o["down"], (h, F))
+        self.ln1 = flat[o["ln1"][0]:o["ln1"][1]]
+        self.ln2 = flat[o["ln2"][0]:o["ln2"][1]]
+
+
+def _mm(a, b, out=None):
+    return torch.mm(a, b) if out is None else torch.mm(a, b, out=out)
+
+
+def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec):
+    """Forward on compute-dtype tensors; returns (out, saved tuple)."""
+    B, S, h = x.shape
+    T = B * S
+    d, Hq, Hkv = spec.head_dim, spec.heads, spec.kv_heads
+    x2 = x.reshape(T, h)
+    n1, rstd1, _ = K.rmsnorm_fwd(x2, w.ln1, spec.eps)
+    qkv = _mm(n1, w.qkv.t())                         # [T, (Hq + 2 Hkv) d]
+    q = qkv[:, :spec.q_dim].view(B, S, Hq, d)
+    k = qkv[:, spec.q_dim:spec.q_dim + spec.kv_dim].view(B, S, Hkv, d)
+    v = qkv[:, spec.q_dim + spec.kv_dim:].view(B, S, Hkv, d)
+    cos, sin = rope_tables(S, d, spec.rope_theta, x.dtype, x.device, spec.interleaved_rope)
+    K.rope_(q, k, cos, sin, interleaved=spec.interleaved_rope)
+    o, lse = K.attn_fwd(q, k, v, causal=spec.causal, window=spec.window)
+    o2 = o.view(T, spec.q_dim)
+    hdn = torch.addmm(x2, o2, w.o.t())               # residual + o_proj(attn)
+    n2, rstd2, _ = K.rmsnorm_fwd(hdn, w.ln2, spec.eps)
+    gu = _mm(n2, w.gu.t())                           # [T, 2F] = gate | up
+    F = spec.ffn
+    z = K.swiglu_fwd(gu[:, :F], gu[:, F:])
+    out = torch.addmm(hdn, z, w.down.t())            # residual + down(z)
+    saved = (x2, n1, rstd1, qkv, o2, lse, hdn, n2, rstd2, gu, z)
+    return out.view(B, S, h), saved
+
+
+def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
+                   grad_flat: torch.Tensor) -> torch.Tensor:
+    """Backward of layer_forward; writes weight grads into ``grad_flat``
+    (compute dtype, flat layout) and returns dx."""
+    x2, n1, rstd1, qkv, o2, lse, hdn, n2, rstd2, gu, z = saved
+    T, h = x2.shape
+    B = dout.shape[0]
+    S = T // B
+    d, Hq, Hkv, F = spec.head_dim, spec.heads, spec.kv_heads, spec.ffn
+    g = FlatViews(spec, grad_flat)
+    dout2 = dout.reshape(T, h)
+
+    # MLP: out = hdn + z W_down^T
+    dz = _mm(dout2, w.down)                          # [T, F]
+    _mm(dout2.t(), z, out=g.down)
+    dgu = torch.empty_like(gu)
+    K.swiglu_bwd(dz, gu[:, :F], gu[:, F:], dgu[:, :F], dgu[:, F:])
+    del dz
+    dn2 = _mm(dgu, w.gu)                             # [T, h]
+    _mm(dgu.t(), n2, out=g.gu)
+    del dgu
+    dh, _ = K.rmsnorm_bwd(dn2, hdn, w.ln2, rstd2, dres=dout2, dw=g.ln2)
+    del dn2
+
+    # attention: hdn = x + o W_o^T
+    do2 = _mm(dh, w.o)                               # [T, Hq d]
+    _mm(dh.t(), o2, out=g.o)
+    q = qkv[:, :spec.q_dim].view(B, S, Hq, d)
+    k = qkv[:, spec.q_dim:spec.q_dim + spec.kv_dim].view(B, S, Hkv, d)
+    v = qkv[:, spec.q_dim + spec.kv_dim:].view(B, S, Hkv, d)
+    dqkv = torch.empty_like(qkv)
+    dq = dqkv[:, :spec.q_dim].view(B, S, Hq, d)
+    dk = dqkv[:, spec.q_dim:spec.q_dim + spec.kv_dim].view(B, S, Hkv, d)
+    dv = dqkv[:, spec.q_dim + spec.kv_dim:].view(B, S, Hkv, d)
+    K.attn_bwd(q, k, v, o2.view(B, S, Hq, d), do2.view(B, S, Hq, d), lse,
+               causal=spec.causal, window=spec.window, dq=dq, dk=dk, dv=dv)
+    del do2
+    cos, sin = rope_tables(S, d, spec.rope_theta, dout.dtype, dout.device, spec.interleaved_rope)
+    K.rope_(dq, dk, cos, sin, interleaved=spec.interleaved_rope, inverse=True)
+    dn1 = _mm(dqkv, w.qkv)                           # [T, h]
+    _mm(dqkv.t(), n1, out=g.qkv)
+    del dqkv
+    dx, _ = K.rmsnorm_bwd(dn1, x2, w.ln1, rstd1, dres=dh, dw=g.ln1)
+    return dx.view(B, S, h)
+
+
+class DecoderLayerFunction(torch.autograd.Function):
+    """autograd node of one decoder layer: inputs (x, flat_param)."""
+
+    @staticmethod
+    def forward(ctx, x, flat_param, spec, weights_lowp):
+        w_flat = weights_lowp if weights_lowp is not None else flat_param
+        w = FlatViews(spec, w_flat)
+        with torch.autocast("cuda", enabled=False):
+            out, saved = layer_forward(x.contiguous(), w, spec)
+        ctx.spec = spec
+        ctx.param_dtype = flat_param.dtype
+        ctx.save_for_backward(w_flat, *saved)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        w_flat, *saved = ctx.saved_tensors
+        spec = ctx.spec
+        w = FlatViews(spec, w_flat)
+        dout = dout.to(w_flat.dtype).contiguous()
+        grad_flat = torch.empty(spec.numel, device=dout.device, dtype=w_flat.dtype)
+        with torch.autocast("cuda", enabled=False):
+            dx = layer_backward(dout, saved, w, spec, grad_flat)
+        if ctx.param_dtype != grad_flat.dtype:
+            grad_flat = grad_flat.to(ctx.param_dtype)
+        return dx, grad_flat, None, None

@@ -1,0 +1,103 @@
+"""One-GPU pipeline-stage runner: the per-layer call order of the reference's
+stage executor with the optimizer stepped inside the backward.
+
+Reference behaviour reproduced (single GPU, no communication):
+  * forward: each layer called in order on the micro-batch
+    (zorse_utils/pipeline_schedule_v2.py:138-155, ``_forward_layer``);
+  * backward: ``out.backward(grad)``, and as soon as a layer's flat gradient
+    is complete its optimizer steps on a dedicated optimizer stream that first
+    waits for the compute stream (utils/patch.py:76-154, the
+    ``--optimizer_in_backwards`` path built at zorse_utils/pipeline.py:
+    150-181), then the gradient is released;
+  * ``recompute=True`` re-runs each layer's forward inside the backward, as
+    ``_backward_layer`` does (zorse_utils/pipeline_schedule_v2.py:157-200).
+
+All streams are created at the default priority.
+"""
+from __future__ import annotations
+
+from typing import Sequence
+
+import torch
+import torch.nn as nn
+
+from .optim import FusedAdamW
+
+
+class StageRunner:
+    def __init__(self, layers: Sequence[nn.Module], lr=1e-4, betas=(0.9, 0.95), eps=1e-8,
+                 weight_decay=0.1, optimizer_in_backwards=True, recompute=False):
+        self.layers = list(layers)
+        self.optimizer_in_backwards = optimizer_in_backwards
+        self.recompute = recompute
+        self.optimizers = []
+        self._hooks = []
+        dev = next(self.layers[0].parameters()).device
+        self.optimizer_stream = torch.cuda.Stream(device=dev) if dev.type == "cuda" else None
+        for layer in self.layers:
+            params = [p for p in layer.parameters() if p.requires_grad]
+            opt = FusedAdamW(params, lr=lr, betas=betas, eps=eps, weight_decay=weight_decay)
+            self.optimizers.append(opt)
+            if optimizer_in_backwards:
+                for p in params:
+                    self._hooks.append(p.register_post_accumulate_grad_hook(
+                        self._make_hook(opt)))
+
+    def _make_hook(self, opt: FusedAdamW):
+        def hook(p: torch.Tensor):
+            self._step_on_side_stream(opt, p)
+        return hook
+
+    def _step_on_side_stream(self, opt: FusedAdamW, p: torch.Tensor):
+        cur = torch.cuda.current_stream(p.device)
+        side = self.optimizer_stream
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            grad = p.grad
+            opt.step()
+            grad.record_stream(side)
+            p.grad = None
+
+    def wait_optimizer(self):
+        """Make the compute stream wait for every optimizer step enqueued so
+        far (call before the next forward touches the parameters)."""
+        if self.optimizer_stream is not None:
+            torch.cuda.current_stream(self.optimizer_stream.device).wait_stream(
+                self.optimizer_stream)
+
+    def forward(self, x: torch.Tensor):
+        self.wait_optimizer()
+        if self.recompute:
+            self._inputs = []
+            with torch.no_grad():
+                for layer in self.layers:
+                    self._inputs.append(x)
+                    x = layer(x)
+            return x
+        for layer in self.layers:
+            x = layer(x)
+        return x
+
+    def backward(self, out: torch.Tensor, grad: torch.Tensor):
+        if not self.recompute:
+            out.backward(grad)
+        else:
+            g = grad
+            for layer, x in zip(reversed(self.layers), reversed(self._inputs)):
+                xr = x.detach().requires_grad_(True)
+                y = layer(xr)
+                y.backward(g)
+                g = xr.grad
+            self._inputs = []
+        if not self.optimizer_in_backwards:
+            for opt in self.optimizers:
+                opt.step()
+                opt.zero_grad(set_to_none=True)
+
+    def step(self, x: torch.Tensor, grad: torch.Tensor):
+        """One stage step: forward, backward, per-layer AdamW."""
+        out = self.forward(x)
+        if self.recompute:
+            out = out.detach()
+        self.backward(out, grad)
+        return out
