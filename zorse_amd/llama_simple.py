@@ -150,8 +150,9 @@ class LlamaDecoderLayer(nn.Module):
     """LlamaDecoderLayer (models/llama_simple.py:391-487) over one flat
     parameter.  ``dtype`` is accepted for signature compatibility (the
     reference uses it only to pick the attention class); parameters are
-    created in ``param_dtype`` (fp32, the nn.Linear default) unless
-    ``to_mixed_precision`` switches them."""
+    created in ``param_dtype``: fp32 (the nn.Linear default) for the
+    profiler's autocast protocol, or bf16 / fp16 for the pipeline's mixed
+    precision, where the optimizer keeps the fp32 master."""
 
     def __init__(self, config, layer_idx: int, dtype=torch.float32, *,
                  sliding_window=None, device=None, param_dtype=torch.float32,

@@ -24,6 +24,12 @@ import torch.nn as nn
 from .optim import FusedAdamW
 
 
+def _call(layer: nn.Module, x: torch.Tensor) -> torch.Tensor:
+    """Blocks return a tensor, bare decoder layers a tuple (hidden, ...)."""
+    y = layer(x)
+    return y[0] if isinstance(y, tuple) else y
+
+
 class StageRunner:
     def __init__(self, layers: Sequence[nn.Module], lr=1e-4, betas=(0.9, 0.95), eps=1e-8,
                  weight_decay=0.1, optimizer_in_backwards=True, recompute=False):
@@ -72,10 +78,10 @@ class StageRunner:
             with torch.no_grad():
                 for layer in self.layers:
                     self._inputs.append(x)
-                    x = layer(x)
+                    x = _call(layer, x)
             return x
         for layer in self.layers:
-            x = layer(x)
+            x = _call(layer, x)
         return x
 
     def backward(self, out: torch.Tensor, grad: torch.Tensor):
@@ -85,7 +91,7 @@ class StageRunner:
             g = grad
             for layer, x in zip(reversed(self.layers), reversed(self._inputs)):
                 xr = x.detach().requires_grad_(True)
-                y = layer(xr)
+                y = _call(layer, xr)
                 y.backward(g)
                 g = xr.grad
             self._inputs = []
