@@ -1,25 +1,30 @@
-// Flash-attention backward for gfx950 (bf16 / fp16 storage).
+// Flash-attention backward for gfx950 (bf16 / fp16 storage), atomic-free.
 //
-// Three kernels:
-//  1. attn_bwd_prep: delta[b,h,i] = sum_d dO[i,d] * O[i,d] (fp32) and zeroes
-//     the fp32 dQ accumulator rows it visits (no memset node, so the whole
-//     backward can be captured in a graph).
-//  2. attn_bwd_kernel: KV-stationary.  A workgroup owns 128 keys of one
-//     (batch, kv-head) -- 32 keys per wave, with that wave's K and V rows held
-//     in registers as MFMA operands -- and loops over every 32-query block of
-//     every q-head in the GQA group (the group reduction of dK / dV happens in
-//     registers, repeat_kv is never materialised).  Per query block:
-//       S   = Q K^T          (A = Q from LDS, B = K from registers)
-//       P   = exp2(S*scale*log2e - lse*log2e), masked
-//       dP  = dO V^T         (A = dO from LDS, B = V from registers)
-//       dS  = P (dP - delta)
-//       dV^T += dO^T P,  dK^T += Q^T dS   (P / dS feed the B operand straight
-//                          from the score accumulators; Q^T / dO^T from LDS)
-//       dQ  += dS K          (dS and the workgroup's K^T through LDS),
-//                          added into the fp32 accumulator with hardware
-//                          fp32 atomics, one row-contiguous store per lane.
-//     dK and dV are written once at the end (scaled), rounded to storage type.
-//  3. attn_bwd_dq_store: dq = round(dq_acc).
+// Three kernels, all on the caller's stream:
+//  1. attn_bwd_prep: delta[b,h,i] = sum_d dO[i,d] * O[i,d] (fp32).
+//  2. attn_bwd_dkdv: KV-stationary.  A workgroup owns 128 keys of one
+//     (batch, kv-head) -- 32 keys per wave, that wave's K and V rows held in
+//     registers as MFMA B operands -- and loops over 64-query blocks of every
+//     q-head in the GQA group (the group reduction of dK / dV happens in the
+//     accumulators; repeat_kv is never materialised).  Per block:
+//       S  = Q K^T,  dP = dO V^T      (A = Q / dO rows from LDS)
+//       P  = exp2(S scale log2e - lse log2e),  dS = P (dP - delta)
+//       dV^T += dO^T P,  dK^T += Q^T dS
+//     with dO^T / Q^T read transposed straight from the row-major LDS tiles
+//     (ds_read_tr16_b64) and P / dS fed from the score accumulators as the B
+//     operand (a fixed query permutation, matched by the transposed reads).
+//  3. attn_bwd_dq: Q-stationary (the forward's structure).  A workgroup owns
+//     128 queries of one (batch, q-head), 32 per wave with Q and dO rows in
+//     registers, and streams 64-key tiles of K and V through LDS:
+//       S^T = K Q^T,  dP^T = V dO^T,  dS^T = P^T (dP^T - delta),
+//       dQ^T += K^T dS^T              (K^T read transposed from LDS)
+//     Each lane owns one query, so lse and delta are per-lane scalars.
+// dQ is produced by its own pass instead of fp32 atomics into a shared
+// accumulator: S and dP are recomputed there (4 of the 14 d-length products
+// per pair), which costs less than device-scope atomic traffic and keeps the
+// result deterministic.
+#include <type_traits>
+
 #include "attn_common.h"
 
 namespace zk {
@@ -28,7 +33,9 @@ int check_attn_desc(const zk_attn_desc* d, const char* who, bool bwd);
 void fill_args(AttnArgs& a, const zk_attn_desc* d);
 
 // ----------------------------------------------------------------- prep ----
-// 8 lanes per (b, q, h) row; each lane covers d/8 elements.
+// 8 lanes per (b, q, h) row; each lane covers d/8 elements.  Writes
+// delta = rowsum(dO o O) and lse2 = lse * log2(e) (+inf for an empty row, so
+// that exp2(s - lse2) = 0), both fp32 [B, Hq, Sq].
 template <typename T>
 __global__ __launch_bounds__(256) void attn_bwd_prep(AttnArgs a) {
   const int64_t rows = a.B * a.Sq * a.Hq;
@@ -44,71 +51,44 @@ __global__ __launch_bounds__(256) void attn_bwd_prep(AttnArgs a) {
     b = bq / a.Sq;
     const T* Or = static_cast<const T*>(a.o) + b * a.o_sb + q * a.o_ss + h * a.o_sh;
     const T* Dr = static_cast<const T*>(a.dout) + b * a.o_sb + q * a.o_ss + h * a.o_sh;
-    float* acc_row = a.dq_acc + row * a.d;
-    for (int64_t e = sub; e < a.d; e += 8) {
-      acc = fmaf(to_f32(Or[e]), to_f32(Dr[e]), acc);
-      acc_row[e] = 0.f;
-    }
+    for (int64_t e = sub; e < a.d; e += 8) acc = fmaf(to_f32(Or[e]), to_f32(Dr[e]), acc);
   }
   acc += __shfl_xor(acc, 1, 64);
   acc += __shfl_xor(acc, 2, 64);
   acc += __shfl_xor(acc, 4, 64);
-  if (row < rows && sub == 0) a.delta[(b * a.Hq + h) * a.Sq + q] = acc;
-}
-
-// ------------------------------------------------------------ dq store -----
-template <typename T>
-__global__ __launch_bounds__(256) void attn_bwd_dq_store(AttnArgs a) {
-  const int64_t total = a.B * a.Sq * a.Hq * a.d;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-       i < total; i += stride) {
-    const int64_t e = i % a.d;
-    int64_t r = i / a.d;
-    const int64_t h = r % a.Hq; r /= a.Hq;
-    const int64_t q = r % a.Sq;
-    const int64_t b = r / a.Sq;
-    T* dq = static_cast<T*>(a.dq);
-    dq[b * a.dq_sb + q * a.dq_ss + h * a.dq_sh + e] = from_f32<T>(a.dq_acc[i]);
+  if (row < rows && sub == 0) {
+    const int64_t i = (b * a.Hq + h) * a.Sq + q;
+    a.delta[i] = acc;
+    const float l = a.lse[i];
+    a.lse2[i] = l == -INFINITY ? INFINITY : l * kLog2e;
   }
 }
 
-// -------------------------------------------------------------- main -------
+// ------------------------------------------------------------- dK / dV -----
 template <int D>
-struct BwdCfg {
-  static constexpr int BK = 128;       // keys per workgroup (32 per wave)
-  static constexpr int MQ = 32;        // queries per iteration
-  static constexpr int QP = D + 8;     // row-major Q / dO pitch (elements)
-  static constexpr int TP = MQ + 4;    // transposed Q^T / dO^T pitch
-  static constexpr int SP = BK + 8;    // dS pitch
-  static constexpr int NSL = D / 32;   // d slices of 32 for dQ
-  static constexpr int KSPLIT = 4 / NSL;            // key groups for dQ
-  static constexpr int KGK = BK / KSPLIT;           // keys per dQ group
-  static constexpr int UNITS = (MQ / 2) * (D / 8);  // (row pair, 8-col chunk)
-  static_assert(NSL * KSPLIT == 4, "d must be 64 or 128");
-  static_assert(UNITS <= 256, "tile too large");
+struct DkdvCfg {
+  static constexpr int BK = 128;              // keys per workgroup (32 per wave)
+  static constexpr int MQ = 64;               // queries per block
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_bwd_kernel(AttnArgs a, int64_t n_kt) {
-  typedef BwdCfg<D> C;
+__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
+  typedef DkdvCfg<D> C;
   typedef Mfma<T> M;
   typedef typename M::vec8 V8;
-  constexpr int BK = C::BK, MQ = C::MQ, QP = C::QP, TP = C::TP, SP = C::SP;
-  __shared__ __attribute__((aligned(16))) T Qs[MQ * QP];
-  __shared__ __attribute__((aligned(16))) T dOs[MQ * QP];
-  __shared__ __attribute__((aligned(16))) T Qt[D * TP];
-  __shared__ __attribute__((aligned(16))) T dOt[D * TP];
-  __shared__ __attribute__((aligned(16))) T dSs[MQ * SP];
-  __shared__ __attribute__((aligned(16))) T Kt[D * SP];
-  __shared__ __attribute__((aligned(16))) float lse2s[MQ];
-  __shared__ __attribute__((aligned(16))) float dels[MQ];
+  constexpr int BK = C::BK, MQ = C::MQ;
+  // Q / dO tiles double-buffered (swizzled rows); each wave keeps its own copy
+  // of the block's lse2 / delta vectors so every wave issues the same loads.
+  __shared__ __attribute__((aligned(16))) T Qs[2][MQ * D];
+  __shared__ __attribute__((aligned(16))) T dOs[2][MQ * D];
+  __shared__ __attribute__((aligned(16))) float lse2s[2][4][MQ];
+  __shared__ __attribute__((aligned(16))) float dels[2][4][MQ];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, g = lane >> 5;
   const int64_t nbh = a.B * a.Hkv;
   const int64_t bid = blockIdx.x;
-  const int64_t kt = bid / nbh;  // low key tiles carry the most causal work
+  const int64_t kt = bid / nbh;  // low key tiles carry the most causal work: first
   const int64_t bh = bid % nbh;
   const int64_t b = bh / a.Hkv, hk = bh % a.Hkv;
   const int64_t n_rep = a.Hq / a.Hkv;
@@ -116,11 +96,13 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(AttnArgs a, int64_t n_kt)
   const int64_t kw0 = k0 + 32 * wave;
   const int64_t my_key = kw0 + l32;
   const float c2 = a.scale_log2;
+  const int ik = static_cast<int>(my_key), Sq32 = static_cast<int>(a.Sq),
+            Skv32 = static_cast<int>(a.Skv), W32 = static_cast<int>(a.window);
 
   const T* Kp = static_cast<const T*>(a.k) + b * a.k_sb + hk * a.k_sh;
   const T* Vp = static_cast<const T*>(a.v) + b * a.v_sb + hk * a.v_sh;
 
-  // B operands for S = Q K^T and dP = dO V^T: lane holds row my_key.
+  // B operands of S = Q K^T and dP = dO V^T: lane holds row my_key.
   V8 kreg[D / 16], vreg[D / 16];
 #pragma unroll
   for (int ks = 0; ks < D / 16; ++ks) {
@@ -132,25 +114,6 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(AttnArgs a, int64_t n_kt)
       vreg[ks] = V8{};
     }
   }
-  // B operand for dQ = dS K, read from Kt[dsl + l32][kbase + 16 kk + 8 g ..]:
-  // K^T of the workgroup's keys, written once (key pairs packed per 32-bit).
-  const int dsl = 32 * (wave % C::NSL);
-  const int kbase = C::KGK * (wave / C::NSL);
-  for (int u = tid; u < (BK / 2) * (D / 8); u += 256) {
-    const int kp = u % (BK / 2), dch = u / (BK / 2);
-    const int64_t key = k0 + 2 * kp;
-    const uint4 r0 = key < a.Skv ? *reinterpret_cast<const uint4*>(Kp + key * a.k_ss + dch * 8)
-                                 : make_uint4(0, 0, 0, 0);
-    const uint4 r1 = key + 1 < a.Skv
-                         ? *reinterpret_cast<const uint4*>(Kp + (key + 1) * a.k_ss + dch * 8)
-                         : make_uint4(0, 0, 0, 0);
-    const uint16_t* e0 = reinterpret_cast<const uint16_t*>(&r0);
-    const uint16_t* e1 = reinterpret_cast<const uint16_t*>(&r1);
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      *reinterpret_cast<uint32_t*>(&Kt[(dch * 8 + e) * SP + 2 * kp]) =
-          static_cast<uint32_t>(e0[e]) | (static_cast<uint32_t>(e1[e]) << 16);
-  }
 
   f32x16 dk[D / 32], dv[D / 32];
 #pragma unroll
@@ -159,7 +122,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(AttnArgs a, int64_t n_kt)
     dv[nt] = f32x16{};
   }
 
-  // query range that can see keys [k0, k0 + BK)
+  // queries that can see keys [k0, k0 + BK)
   int64_t q_lo = 0, q_hi = a.Sq;
   if (a.causal) q_lo = k0;
   if (a.window > 0 && k0 + BK - 1 + a.window < q_hi) q_hi = k0 + BK - 1 + a.window;
@@ -168,77 +131,36 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(AttnArgs a, int64_t n_kt)
   const int64_t nqb = qb_hi - qb_lo;
   const int64_t n_iter = nqb * n_rep;
 
-  // staging registers for the next (head, query block)
-  uint4 qr[2], dr[2];
-  float lse_r = 0.f, del_r = 0.f;
-  const bool loader = tid < C::UNITS;
-  const int up = tid % (MQ / 2), udch = tid / (MQ / 2);
-  auto prefetch = [&](int64_t it) {
+  constexpr int NL = 2 * tile_load_insts<D, MQ>() + 2;
+  auto issue = [&](int64_t it, int st) {
     const int64_t hq = hk * n_rep + it / nqb;
     const int64_t qb0 = (qb_lo + it % nqb) * MQ;
-    if (loader) {
-      const T* Qp = static_cast<const T*>(a.q) + b * a.q_sb + hq * a.q_sh;
-      const T* Dp = static_cast<const T*>(a.dout) + b * a.o_sb + hq * a.o_sh;
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int64_t qi = qb0 + 2 * up + r;
-        if (qi < a.Sq) {
-          qr[r] = *reinterpret_cast<const uint4*>(Qp + qi * a.q_ss + udch * 8);
-          dr[r] = *reinterpret_cast<const uint4*>(Dp + qi * a.o_ss + udch * 8);
-        } else {
-          qr[r] = make_uint4(0, 0, 0, 0);
-          dr[r] = make_uint4(0, 0, 0, 0);
-        }
-      }
-    }
-    if (tid < MQ) {
-      const int64_t qi = qb0 + tid;
-      if (qi < a.Sq) {
-        const float l = a.lse[(b * a.Hq + hq) * a.Sq + qi];
-        lse_r = l == -INFINITY ? INFINITY : l * kLog2e;
-        del_r = a.delta[(b * a.Hq + hq) * a.Sq + qi];
-      } else {
-        lse_r = INFINITY;  // P = 0 for rows past the end
-        del_r = 0.f;
-      }
-    }
-  };
-  auto store_lds = [&]() {
-    if (loader) {
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        *reinterpret_cast<uint4*>(&Qs[(2 * up + r) * QP + udch * 8]) = qr[r];
-        *reinterpret_cast<uint4*>(&dOs[(2 * up + r) * QP + udch * 8]) = dr[r];
-      }
-      const uint16_t* q0e = reinterpret_cast<const uint16_t*>(&qr[0]);
-      const uint16_t* q1e = reinterpret_cast<const uint16_t*>(&qr[1]);
-      const uint16_t* d0e = reinterpret_cast<const uint16_t*>(&dr[0]);
-      const uint16_t* d1e = reinterpret_cast<const uint16_t*>(&dr[1]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int row = udch * 8 + e;
-        *reinterpret_cast<uint32_t*>(&Qt[row * TP + 2 * up]) =
-            static_cast<uint32_t>(q0e[e]) | (static_cast<uint32_t>(q1e[e]) << 16);
-        *reinterpret_cast<uint32_t*>(&dOt[row * TP + 2 * up]) =
-            static_cast<uint32_t>(d0e[e]) | (static_cast<uint32_t>(d1e[e]) << 16);
-      }
-    }
-    if (tid < MQ) {
-      lse2s[tid] = lse_r;
-      dels[tid] = del_r;
-    }
+    const T* Qp = static_cast<const T*>(a.q) + b * a.q_sb + hq * a.q_sh;
+    const T* Dp = static_cast<const T*>(a.dout) + b * a.o_sb + hq * a.o_sh;
+    tile_load_async<T, D, MQ>(Qs[st], Qp, a.q_ss, qb0, a.Sq);
+    tile_load_async<T, D, MQ>(dOs[st], Dp, a.o_ss, qb0, a.Sq);
+    int64_t qi = qb0 + lane;
+    if (qi > a.Sq - 1) qi = a.Sq - 1;
+    const int64_t ri = (b * a.Hq + hq) * a.Sq + qi;
+    __builtin_amdgcn_global_load_lds((gmem_void*)(a.lse2 + ri), (lds_void*)&lse2s[st][wave][0], 4, 0, 0);
+    __builtin_amdgcn_global_load_lds((gmem_void*)(a.delta + ri), (lds_void*)&dels[st][wave][0], 4, 0, 0);
   };
 
-  if (n_iter > 0) prefetch(0);
-  for (int64_t it = 0; it < n_iter; ++it) {
-    const int64_t hq = hk * n_rep + it / nqb;
+  // One pipeline step on LDS stage ST (compile-time: immediate LDS offsets).
+  auto step = [&](auto stage_tag, int64_t it) {
+    constexpr int st = decltype(stage_tag)::value;
     const int64_t qb0 = (qb_lo + it % nqb) * MQ;
+    __syncthreads();  // every wave is done with the other stage
+    if (it + 1 < n_iter) {
+      issue(it + 1, st ^ 1);
+      wait_vmcnt<NL>();
+    } else {
+      wait_vmcnt<0>();
+    }
     __syncthreads();
-    store_lds();
-    __syncthreads();
-    if (it + 1 < n_iter) prefetch(it + 1);
 
-    bool skip = false, need_mask = kw0 + 31 >= a.Skv;
+    // wave-uniform classification of this (query block, 32 keys) tile
+    bool skip = false, need_mask = kw0 + 31 >= a.Skv || qb0 + MQ > a.Sq;
     if (a.causal) {
       if (kw0 > qb0 + MQ - 1) skip = true;
       if (kw0 + 31 > qb0) need_mask = true;
@@ -247,81 +169,70 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(AttnArgs a, int64_t n_kt)
       if (kw0 + 31 <= qb0 - a.window) skip = true;
       if (kw0 <= qb0 + MQ - 1 - a.window) need_mask = true;
     }
+    if (skip) return;
+    const T* Qt = Qs[st];
+    const T* dOt = dOs[st];
+    const float* l2v = lse2s[st][wave];
+    const float* dlv = dels[st][wave];
 
-    if (!skip) {
-      // S = Q K^T and dP = dO V^T (rows = queries, cols = this wave's keys)
-      f32x16 s = f32x16{}, dp = f32x16{};
+    f32x16 s[2], dp[2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      s[mb] = f32x16{};
+      dp[mb] = f32x16{};
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
-        const V8 qa = *reinterpret_cast<const V8*>(&Qs[l32 * QP + 16 * ks + 8 * g]);
-        s = M::mma(qa, kreg[ks], s);
-        const V8 da = *reinterpret_cast<const V8*>(&dOs[l32 * QP + 16 * ks + 8 * g]);
-        dp = M::mma(da, vreg[ks], dp);
+        const V8 qa = *reinterpret_cast<const V8*>(&Qt[tile_off<D>(32 * mb + l32, 16 * ks + 8 * g)]);
+        s[mb] = M::mma(qa, kreg[ks], s[mb]);
+        const V8 da = *reinterpret_cast<const V8*>(&dOt[tile_off<D>(32 * mb + l32, 16 * ks + 8 * g)]);
+        dp[mb] = M::mma(da, vreg[ks], dp[mb]);
       }
-      V8 pb[2], sb[2];
+    }
+    // P and dS; element j of block mb is query 32 mb + 8 (j/4) + 4 g + j%4
+    V8 pb[4], sb[4];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int a4 = 0; a4 < 4; ++a4) {
-        const float4 l4 = *reinterpret_cast<const float4*>(&lse2s[8 * a4 + 4 * g]);
-        const float4 d4 = *reinterpret_cast<const float4*>(&dels[8 * a4 + 4 * g]);
+        const int r0 = 32 * mb + 8 * a4 + 4 * g;
+        const float4 l4 = *reinterpret_cast<const float4*>(&l2v[r0]);
+        const float4 d4 = *reinterpret_cast<const float4*>(&dlv[r0]);
         const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
         const float dl[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int j = 4 * a4 + e;
-          float p = __builtin_amdgcn_exp2f(fmaf(s[j], c2, -lv[e]));
-          if (need_mask) {
-            const int64_t qi = qb0 + 8 * a4 + 4 * g + e;
-            if (!attn_visible(qi, my_key, a.Skv, a.causal, a.window)) p = 0.f;
-          }
-          const float ds = p * (dp[j] - dl[e]);
-          pb[j >> 3][j & 7] = static_cast<T>(p);
-          sb[j >> 3][j & 7] = static_cast<T>(ds);
-          dSs[(8 * a4 + 4 * g + e) * SP + 32 * wave + l32] = static_cast<T>(ds);
+          float p = __builtin_amdgcn_exp2f(fmaf(s[mb][j], c2, -lv[e]));
+          if (need_mask && !visible32(static_cast<int>(qb0) + r0 + e, ik, Sq32, Skv32,
+                                      a.causal, W32))
+            p = 0.f;
+          const float ds = p * (dp[mb][j] - dl[e]);
+          pb[2 * mb + (j >> 3)][j & 7] = static_cast<T>(p);
+          sb[2 * mb + (j >> 3)][j & 7] = static_cast<T>(ds);
         }
       }
-      // dV^T += dO^T P ; dK^T += Q^T dS
+    // dV^T += dO^T P ; dK^T += Q^T dS.  Step kk covers queries 16 kk + perm:
+    // lane half g holds queries 16 kk + 4 g + 0..3 and 16 kk + 8 + 4 g + 0..3.
+#pragma unroll
+    for (int kk = 0; kk < MQ / 16; ++kk) {
+      const int klo = 16 * kk + 4 * g, khi = 16 * kk + 8 + 4 * g;
 #pragma unroll
       for (int nt = 0; nt < D / 32; ++nt) {
-        const T* drow = &dOt[(32 * nt + l32) * TP];
-        const T* qrow = &Qt[(32 * nt + l32) * TP];
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const int qb = 16 * kk + 4 * g;
-          const u32x2 dlo = *reinterpret_cast<const u32x2*>(drow + qb);
-          const u32x2 dhi = *reinterpret_cast<const u32x2*>(drow + qb + 8);
-          const u32x4 dw = {dlo[0], dlo[1], dhi[0], dhi[1]};
-          dv[nt] = M::mma(__builtin_bit_cast(V8, dw), pb[kk], dv[nt]);
-          const u32x2 qlo = *reinterpret_cast<const u32x2*>(qrow + qb);
-          const u32x2 qhi = *reinterpret_cast<const u32x2*>(qrow + qb + 8);
-          const u32x4 qw = {qlo[0], qlo[1], qhi[0], qhi[1]};
-          dk[nt] = M::mma(__builtin_bit_cast(V8, qw), sb[kk], dk[nt]);
-        }
+        const V8 dA = lds_tr_operand<T, D>(dOt, 32 * nt, klo, khi);
+        dv[nt] = M::mma(dA, pb[kk], dv[nt]);
+        const V8 qA = lds_tr_operand<T, D>(Qt, 32 * nt, klo, khi);
+        dk[nt] = M::mma(qA, sb[kk], dk[nt]);
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-        dSs[(8 * (j >> 2) + 4 * g + (j & 3)) * SP + 32 * wave + l32] = static_cast<T>(0.f);
     }
-    __syncthreads();
+  };
 
-    // dQ[:, dsl..dsl+31] += dS[:, kbase..kbase+KGK) K[kbase.., dsl..]
-    f32x16 dq = f32x16{};
-#pragma unroll
-    for (int kk = 0; kk < C::KGK / 16; ++kk) {
-      const V8 sa = *reinterpret_cast<const V8*>(&dSs[l32 * SP + kbase + 16 * kk + 8 * g]);
-      const V8 kb = *reinterpret_cast<const V8*>(&Kt[(dsl + l32) * SP + kbase + 16 * kk + 8 * g]);
-      dq = M::mma(sa, kb, dq);
-    }
-    float* accp = a.dq_acc + ((b * a.Sq + qb0) * a.Hq + hq) * D + dsl + l32;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int qrow = 8 * (j >> 2) + 4 * g + (j & 3);
-      if (qb0 + qrow < a.Sq)
-        unsafeAtomicAdd(accp + static_cast<int64_t>(qrow) * a.Hq * D, dq[j] * a.scale);
-    }
+  if (n_iter > 0) issue(0, 0);
+  for (int64_t it = 0; it < n_iter; it += 2) {
+    step(std::integral_constant<int, 0>{}, it);
+    if (it + 1 < n_iter) step(std::integral_constant<int, 1>{}, it + 1);
   }
 
-  // dK = scale * (Q^T dS)^T, dV = (dO^T P)^T : lane holds key my_key and
+  // dK = scale (Q^T dS)^T, dV = (dO^T P)^T: lane holds key my_key and
   // d rows 32 nt + 8 a4 + 4 g + 0..3 (4 consecutive elements).
   if (my_key < a.Skv) {
     typedef T T4 __attribute__((ext_vector_type(4)));
@@ -340,6 +251,163 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(AttnArgs a, int64_t n_kt)
         }
         *reinterpret_cast<T4*>(dkp + d0) = wk;
         *reinterpret_cast<T4*>(dvp + d0) = wv;
+      }
+  }
+}
+
+// ------------------------------------------------------------------ dQ -----
+template <int D>
+struct DqCfg {
+  static constexpr int BM = 128;              // queries per workgroup (32 per wave)
+  static constexpr int BN = 64;               // keys per tile
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(256, 1) void attn_bwd_dq(AttnArgs a, int64_t n_qt) {
+  typedef DqCfg<D> C;
+  typedef Mfma<T> M;
+  typedef typename M::vec8 V8;
+  constexpr int BM = C::BM, BN = C::BN;
+  __shared__ __attribute__((aligned(16))) T Ks[2][BN * D];  // swizzled rows
+  __shared__ __attribute__((aligned(16))) T Vs[2][BN * D];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int64_t nbh = a.B * a.Hq;
+  const int64_t bid = blockIdx.x;
+  const int64_t qt = n_qt - 1 - bid / nbh;  // heaviest (last) query tiles first
+  const int64_t bh = bid % nbh;
+  const int64_t b = bh / a.Hq, hq = bh % a.Hq;
+  const int64_t hk = hq / (a.Hq / a.Hkv);
+  const int64_t q0 = qt * BM;
+  const int64_t qw0 = q0 + 32 * wave;
+  const int64_t my_q = qw0 + l32;
+  const float c2 = a.scale_log2;
+  const int iq = static_cast<int>(my_q), Sq32 = static_cast<int>(a.Sq),
+            Skv32 = static_cast<int>(a.Skv), W32 = static_cast<int>(a.window);
+
+  const T* Qp = static_cast<const T*>(a.q) + b * a.q_sb + hq * a.q_sh;
+  const T* Dp = static_cast<const T*>(a.dout) + b * a.o_sb + hq * a.o_sh;
+  const T* Kp = static_cast<const T*>(a.k) + b * a.k_sb + hk * a.k_sh;
+  const T* Vp = static_cast<const T*>(a.v) + b * a.v_sb + hk * a.v_sh;
+
+  // B operands of S^T = K Q^T and dP^T = V dO^T: lane holds query my_q.
+  V8 qreg[D / 16], dreg[D / 16];
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) {
+    if (my_q < a.Sq) {
+      qreg[ks] = *reinterpret_cast<const V8*>(Qp + my_q * a.q_ss + 16 * ks + 8 * g);
+      dreg[ks] = *reinterpret_cast<const V8*>(Dp + my_q * a.o_ss + 16 * ks + 8 * g);
+    } else {
+      qreg[ks] = V8{};
+      dreg[ks] = V8{};
+    }
+  }
+  float lse2 = INFINITY, del = 0.f;
+  if (my_q < a.Sq) {
+    lse2 = a.lse2[(b * a.Hq + hq) * a.Sq + my_q];
+    del = a.delta[(b * a.Hq + hq) * a.Sq + my_q];
+  }
+
+  int64_t kv_lo = 0, kv_hi = a.Skv;
+  if (a.causal && kv_hi > q0 + BM) kv_hi = q0 + BM;
+  if (a.window > 0 && q0 - a.window + 1 > kv_lo) kv_lo = q0 - a.window + 1;
+  const int64_t t_lo = kv_lo / BN;
+  const int64_t t_hi = kv_hi > kv_lo ? (kv_hi + BN - 1) / BN : t_lo;
+
+  constexpr int NL = 2 * tile_load_insts<D, BN>();
+  auto issue = [&](int64_t kb0, int st) {
+    tile_load_async<T, D, BN>(Ks[st], Kp, a.k_ss, kb0, a.Skv);
+    tile_load_async<T, D, BN>(Vs[st], Vp, a.v_ss, kb0, a.Skv);
+  };
+
+  f32x16 dq[D / 32];
+#pragma unroll
+  for (int nt = 0; nt < D / 32; ++nt) dq[nt] = f32x16{};
+
+  // One pipeline step on LDS stage ST (compile-time: immediate LDS offsets).
+  auto step = [&](auto stage_tag, int64_t t) {
+    constexpr int st = decltype(stage_tag)::value;
+    const int64_t kb0 = t * BN;
+    __syncthreads();
+    if (t + 1 < t_hi) {
+      issue(kb0 + BN, st ^ 1);
+      wait_vmcnt<NL>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    __syncthreads();
+
+    bool skip = false, need_mask = kb0 + BN > a.Skv || qw0 + 31 >= a.Sq;
+    if (a.causal) {
+      if (kb0 > qw0 + 31) skip = true;
+      if (kb0 + BN - 1 > qw0) need_mask = true;
+    }
+    if (a.window > 0) {
+      if (kb0 + BN - 1 <= qw0 - a.window) skip = true;
+      if (kb0 <= qw0 + 31 - a.window) need_mask = true;
+    }
+    if (skip) return;
+    const T* Kt = Ks[st];
+    const T* Vt = Vs[st];
+
+    // S^T and dP^T: block tt covers keys kb0 + 32 tt .. +31
+    f32x16 s[BN / 32], dp[BN / 32];
+#pragma unroll
+    for (int tt = 0; tt < BN / 32; ++tt) {
+      s[tt] = f32x16{};
+      dp[tt] = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks) {
+        const V8 kA = *reinterpret_cast<const V8*>(&Kt[tile_off<D>(32 * tt + l32, 16 * ks + 8 * g)]);
+        s[tt] = M::mma(kA, qreg[ks], s[tt]);
+        const V8 vA = *reinterpret_cast<const V8*>(&Vt[tile_off<D>(32 * tt + l32, 16 * ks + 8 * g)]);
+        dp[tt] = M::mma(vA, dreg[ks], dp[tt]);
+      }
+    }
+    // dS^T, packed per 16-key MFMA step (key = kb0 + 32 tt + 8 (j/4) + 4 g + j%4)
+    V8 sb[BN / 16];
+#pragma unroll
+    for (int tt = 0; tt < BN / 32; ++tt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float p = __builtin_amdgcn_exp2f(fmaf(s[tt][j], c2, -lse2));
+        if (need_mask) {
+          const int key = static_cast<int>(kb0) + 32 * tt + 8 * (j >> 2) + 4 * g + (j & 3);
+          if (!visible32(iq, key, Sq32, Skv32, a.causal, W32)) p = 0.f;
+        }
+        sb[2 * tt + (j >> 3)][j & 7] = static_cast<T>(p * (dp[tt][j] - del));
+      }
+    // dQ^T += K^T dS^T  (K^T read transposed from the row-major K tile)
+#pragma unroll
+    for (int kk = 0; kk < BN / 16; ++kk) {
+      const int klo = 16 * kk + 4 * g, khi = 16 * kk + 8 + 4 * g;
+#pragma unroll
+      for (int nt = 0; nt < D / 32; ++nt) {
+        const V8 kA = lds_tr_operand<T, D>(Kt, 32 * nt, klo, khi);
+        dq[nt] = M::mma(kA, sb[kk], dq[nt]);
+      }
+    }
+  };
+
+  if (t_lo < t_hi) issue(t_lo * BN, 0);
+  for (int64_t t = t_lo; t < t_hi; t += 2) {
+    step(std::integral_constant<int, 0>{}, t);
+    if (t + 1 < t_hi) step(std::integral_constant<int, 1>{}, t + 1);
+  }
+
+  if (my_q < a.Sq) {
+    typedef T T4 __attribute__((ext_vector_type(4)));
+    T* dqp = static_cast<T*>(a.dq) + b * a.dq_sb + hq * a.dq_sh + my_q * a.dq_ss;
+#pragma unroll
+    for (int nt = 0; nt < D / 32; ++nt)
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        const int d0 = 32 * nt + 8 * a4 + 4 * g;
+        T4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = static_cast<T>(dq[nt][4 * a4 + e] * a.scale);
+        *reinterpret_cast<T4*>(dqp + d0) = w;
       }
   }
 }
@@ -422,9 +490,8 @@ using namespace zk;
 
 extern "C" int64_t zk_attn_bwd_workspace(const zk_attn_desc* desc) {
   if (desc == nullptr) return 0;
-  const int64_t acc = desc->B * desc->Sq * desc->Hq * desc->d;  // fp32 dQ
-  const int64_t del = desc->B * desc->Hq * desc->Sq;            // fp32 delta
-  return (acc + del) * 4 + 256;
+  const int64_t rows = desc->B * desc->Hq * desc->Sq;  // fp32 delta and lse2
+  return 2 * rows * 4 + 512;
 }
 
 extern "C" int zk_attn_bwd(const zk_attn_desc* desc, const void* q,
@@ -446,8 +513,8 @@ extern "C" int zk_attn_bwd(const zk_attn_desc* desc, const void* q,
   a.q = q; a.k = k; a.v = v; a.o = o; a.dout = dout; a.lse = lse;
   a.dq = dq; a.dk = dk; a.dv = dv;
   const uintptr_t base = (reinterpret_cast<uintptr_t>(workspace) + 255) & ~uintptr_t(255);
-  a.dq_acc = reinterpret_cast<float*>(base);
-  a.delta = a.dq_acc + desc->B * desc->Sq * desc->Hq * desc->d;
+  a.delta = reinterpret_cast<float*>(base);
+  a.lse2 = a.delta + ((desc->B * desc->Hq * desc->Sq + 63) & ~int64_t(63));
   hipStream_t s = as_stream(stream);
 
   const int64_t rows = desc->B * desc->Sq * desc->Hq;
@@ -466,18 +533,17 @@ extern "C" int zk_attn_bwd(const zk_attn_desc* desc, const void* q,
     return launch_status("zk_attn_bwd");
   }
   ZK_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(o, 16) &&
-                 aligned(dout, 16) && aligned(dk, 8) && aligned(dv, 8),
+                 aligned(dout, 16) && aligned(dq, 8) && aligned(dk, 8) && aligned(dv, 8),
              ZK_EALIGN, "zk_attn_bwd: tensors must be 16-byte aligned");
-  const int64_t n_kt = (desc->Skv + 127) / 128;
-  const dim3 grid(static_cast<unsigned>(n_kt * desc->B * desc->Hkv));
-  int64_t sgrid = (rows * desc->d + 255) / 256;
-  const int64_t cap = static_cast<int64_t>(device_cus()) * 16;
-  if (sgrid > cap) sgrid = cap;
-#define ZK_BWD(T, D)                                                              \
-  do {                                                                            \
-    if (rows > 0) hipLaunchKernelGGL(attn_bwd_prep<T>, pgrid, dim3(256), 0, s, a); \
-    if (n_kt > 0) hipLaunchKernelGGL((attn_bwd_kernel<T, D>), grid, dim3(256), 0, s, a, n_kt); \
-    if (rows > 0) hipLaunchKernelGGL(attn_bwd_dq_store<T>, dim3(sgrid), dim3(256), 0, s, a); \
+  const int64_t n_kt = (desc->Skv + DkdvCfg<128>::BK - 1) / DkdvCfg<128>::BK;
+  const int64_t n_qt = (desc->Sq + DqCfg<128>::BM - 1) / DqCfg<128>::BM;
+  const dim3 kgrid(static_cast<unsigned>(n_kt * desc->B * desc->Hkv));
+  const dim3 qgrid(static_cast<unsigned>(n_qt * desc->B * desc->Hq));
+#define ZK_BWD(T, D)                                                                  \
+  do {                                                                                \
+    if (rows > 0) hipLaunchKernelGGL(attn_bwd_prep<T>, pgrid, dim3(256), 0, s, a);    \
+    if (n_kt > 0) hipLaunchKernelGGL((attn_bwd_dkdv<T, D>), kgrid, dim3(256), 0, s, a); \
+    if (n_qt > 0) hipLaunchKernelGGL((attn_bwd_dq<T, D>), qgrid, dim3(256), 0, s, a, n_qt); \
   } while (0)
   if (desc->dtype == ZK_BF16) {
     if (desc->d == 128) ZK_BWD(bf16, 128); else ZK_BWD(bf16, 64);

@@ -21,6 +21,7 @@ struct AttnArgs {
   void* dv;
   float* dq_acc;  // backward workspace: fp32 [B, Sq, Hq, d]
   float* delta;   // backward workspace: fp32 [B, Hq, Sq]
+  float* lse2;    // backward workspace: lse * log2(e), fp32 [B, Hq, Sq]
   int64_t B, Sq, Skv, Hq, Hkv, d;
   int64_t q_sb, q_ss, q_sh;
   int64_t k_sb, k_ss, k_sh;
@@ -63,6 +64,109 @@ __device__ __forceinline__ bool attn_visible(int64_t qi, int64_t kj,
   if (causal && kj > qi) return false;
   if (window > 0 && kj <= qi - window) return false;
   return true;
+}
+
+}  // namespace zk
+
+namespace zk {
+
+// ---------------------------------------------------------------------------
+// LDS tiles of D-element rows (D = 64 or 128, 2-byte elements), unpadded,
+// with the 16-byte chunks of row r XOR-swizzled by sw(r) so that both access
+// patterns the kernels use are free of bank conflicts:
+//  * row reads (ds_read_b128): 16 lanes read one logical chunk of 16
+//    consecutive rows -- sw(r) is a bijection on each run of 16 rows (per
+//    row parity for D = 64, where two rows share a 256-byte bank row);
+//  * transposed reads (ds_read_tr16_b64): a 32-lane half reads 4 consecutive
+//    chunks of 4 consecutive rows -- sw maps those 4 rows to 4 disjoint
+//    4-chunk groups.
+template <int D>
+__device__ __forceinline__ int tile_sw(int r) {
+  if (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+  return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+}
+// Element offset of (row, col) in a swizzled tile; col % 8 is kept.
+template <int D>
+__device__ __forceinline__ int tile_off(int r, int col) {
+  return r * D + ((((col >> 3) ^ tile_sw<D>(r))) << 3) + (col & 7);
+}
+
+// ---------------------------------------------------------------------------
+// Transposed MFMA operand from a row-major swizzled LDS tile (gfx950
+// ds_read_tr16_b64).
+//
+// The tile X holds X[r][c] at tile_off<D>(r, c).  The 32x32x16 MFMA A operand
+// wants, in lane l, the 8 elements X^T[i][k] = X[k][i] with i = col0 + l % 32
+// and k = klo + 0..3 (first half), k = khi + 0..3 (second half), where klo /
+// khi may differ between the lane halves l < 32 and l >= 32.
+// ds_read_tr16_b64 delivers, to lane i of a 16-lane group, element (i & 3) of
+// the 8-byte chunks addressed by lanes (i >> 2) + 4e of that group
+// (e = 0..3), so lane q of group G supplies the address of
+// X[k0 + (q >> 2)][col0 + 16 (G & 1) + 4 (q & 3)].  The same layout serves a
+// B operand whose columns are X's columns.
+template <typename T, int D>
+__device__ __forceinline__ typename Mfma<T>::vec8 lds_tr_operand(const T* tile, int col0,
+                                                                 int klo, int khi) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const int lane = threadIdx.x & 63;
+  const int q = lane & 15, G = lane >> 4;
+  const int col = col0 + 16 * (G & 1) + 4 * (q & 3);
+  const T* p0 = tile + tile_off<D>(klo + (q >> 2), col);
+  const T* p1 = tile + tile_off<D>(khi + (q >> 2), col);
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1));
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x8 w = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  return __builtin_bit_cast(typename Mfma<T>::vec8, w);
+}
+
+// ---------------------------------------------------------------------------
+// Asynchronous tile loads: global memory -> LDS without staging registers
+// (gfx950 global_load_lds_dwordx4).  One wave instruction writes 64
+// consecutive 16-byte LDS chunks (LDS address = wave-uniform base + 16 lane);
+// each lane picks the global chunk that belongs at its LDS position, which is
+// how the XOR swizzle of tile_off is applied.  Rows at or past `nrows` are
+// clamped to the last row so that every lane reads valid, finite data (the
+// kernels mask those rows).  Completion is tracked by the wave's vmcnt.
+typedef __attribute__((address_space(1))) void gmem_void;
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <typename T, int D, int ROWS>
+__device__ __forceinline__ void tile_load_async(T* tile, const T* gbase, int64_t ld,
+                                                int64_t g0, int64_t nrows) {
+  constexpr int CH = ROWS * D / 8;
+  static_assert(CH % 256 == 0, "tile must be a multiple of 256 chunks");
+  const int tid = threadIdx.x;
+  const int wave_chunk0 = tid & ~63;
+#pragma unroll
+  for (int i = 0; i < CH / 256; ++i) {
+    const int p = i * 256 + tid;
+    const int row = p / (D / 8);
+    const int c = (p % (D / 8)) ^ tile_sw<D>(row);
+    int64_t gr = g0 + row;
+    if (gr > nrows - 1) gr = nrows - 1;
+    const T* src = gbase + gr * ld + c * 8;
+    T* dst = tile + (i * 256 + wave_chunk0) * 8;
+    __builtin_amdgcn_global_load_lds((gmem_void*)src, (lds_void*)dst, 16, 0, 0);
+  }
+}
+
+// Number of vector-memory instructions tile_load_async issues per wave.
+template <int D, int ROWS>
+constexpr int tile_load_insts() { return ROWS * D / 8 / 256; }
+
+// s_waitcnt vmcnt(N) (expcnt / lgkmcnt left unconstrained), gfx9 encoding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt out of range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// True when key kj is visible from query qi (32-bit positions).
+__device__ __forceinline__ bool visible32(int qi, int kj, int Sq, int Skv, int causal,
+                                          int window) {
+  return qi < Sq && kj < Skv && (!causal || kj <= qi) && (window <= 0 || kj > qi - window);
 }
 
 }  // namespace zk

@@ -2,19 +2,25 @@
 //
 // Workgroup = 4 waves = 128 queries of one (batch, q-head); each wave owns 32
 // queries whose Q rows stay in registers for the whole kernel.  The kernel
-// streams 64-key tiles of K and V through LDS (K row-major, V transposed on
-// the LDS write) with the next tile's global loads in flight during the
-// current tile's math.
+// streams 64-key tiles of K and V through LDS (row-major, XOR-swizzled
+// 16-byte chunks, see tile_off) with the next tile's global loads in flight
+// during the current tile's math.
 //
 // Orientation: the score tile is computed transposed, S^T = K Q^T, with
-// v_mfma_f32_32x32x16 (A = K from LDS, B = Q from registers).  In the MFMA
-// result layout lane l holds query (l mod 32) and 16 keys, so the online
+// v_mfma_f32_32x32x16 (A = K rows from LDS, B = Q from registers).  In the
+// MFMA result layout lane l holds query (l mod 32) and 16 keys, so the online
 // softmax row max / row sum are per-lane reductions plus one exchange between
 // the two lane halves, and the rescale of the output accumulator is a
 // per-lane scalar.  The output is also accumulated transposed,
 // O^T += V^T P^T: the probabilities go from the score accumulators straight
-// into the B operand (a fixed permutation of the 16 keys of each MFMA step,
-// matched by the order in which V^T is read), so P never touches LDS.
+// into the B operand (a fixed permutation of the 16 keys of each MFMA step)
+// and V^T is read with the LDS transpose read in the matching order, so P
+// never touches LDS and V is never transposed in memory.
+//
+// The running maximum is only moved (and O, l rescaled) when some lane's new
+// maximum exceeds it by more than 2^8 in the exp2 domain: until then the
+// probabilities are bounded by 256, which fp32 sums and bf16 / fp16 P hold
+// exactly as well, and the result is the same after the final 1 / l.
 //
 // Masking: causal (key <= query), sliding window (key > query - W) and the
 // ragged end of the key range; tiles entirely masked for a wave are skipped,
@@ -28,18 +34,18 @@ namespace zk {
 
 template <typename T, int D>
 struct FwdCfg {
-  static constexpr int BM = 128;          // queries per workgroup
-  static constexpr int BN = 64;           // keys per tile
-  static constexpr int KP = D + 8;        // K row pitch in LDS (elements)
-  static constexpr int VP = BN + 4;       // V^T row pitch in LDS (elements)
-  static constexpr int KCH = BN * D / 8 / 256;         // 16-byte K chunks / thread
-  static constexpr int VPR = (BN / 2) * (D / 8) / 256; // key-pair V chunks / thread
-  static_assert(KCH >= 1 && VPR >= 1, "tile too small for 256 threads");
+  static constexpr int BM = 128;                   // queries per workgroup
+  static constexpr int BN = 64;                    // keys per tile
+  static constexpr int CPT = BN * D / 8 / 256;     // 16-byte chunks / thread / tile
+  static_assert(CPT >= 1, "tile too small for 256 threads");
 };
 
 __device__ __forceinline__ float fast_exp2(float x) {
   return __builtin_amdgcn_exp2f(x);
 }
+
+// log2-domain growth of the running maximum tolerated before rescaling
+static constexpr float kRescaleThreshold = 8.0f;
 
 template <typename T, int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
@@ -47,9 +53,9 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
   typedef FwdCfg<T, D> C;
   typedef Mfma<T> M;
   typedef typename M::vec8 V8;
-  constexpr int BM = C::BM, BN = C::BN, KP = C::KP, VP = C::VP;
-  __shared__ __attribute__((aligned(16))) T Ks[BN * KP];
-  __shared__ __attribute__((aligned(16))) T Vt[D * VP];
+  constexpr int BM = C::BM, BN = C::BN;
+  __shared__ __attribute__((aligned(16))) T Ks[2][BN * D];
+  __shared__ __attribute__((aligned(16))) T Vs[2][BN * D];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, g = lane >> 5;
@@ -83,66 +89,36 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
   const int64_t t_lo = kv_lo / BN;
   const int64_t t_hi = kv_hi > kv_lo ? (kv_hi + BN - 1) / BN : t_lo;
 
-  uint4 kr[C::KCH];
-  uint4 vr[2 * C::VPR];
-  auto prefetch = [&](int64_t k0) {
-#pragma unroll
-    for (int i = 0; i < C::KCH; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c / (D / 8), col = (c % (D / 8)) * 8;
-      const int64_t key = k0 + row;
-      kr[i] = key < a.Skv ? *reinterpret_cast<const uint4*>(Kp + key * a.k_ss + col)
-                          : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < C::VPR; ++i) {
-      const int c = tid + 256 * i;
-      const int kp = c % (BN / 2), dch = c / (BN / 2);
-      const int64_t key = k0 + 2 * kp;
-      vr[2 * i] = key < a.Skv
-                      ? *reinterpret_cast<const uint4*>(Vp + key * a.v_ss + dch * 8)
-                      : make_uint4(0, 0, 0, 0);
-      vr[2 * i + 1] =
-          key + 1 < a.Skv
-              ? *reinterpret_cast<const uint4*>(Vp + (key + 1) * a.v_ss + dch * 8)
-              : make_uint4(0, 0, 0, 0);
-    }
-  };
-  auto store_lds = [&]() {
-#pragma unroll
-    for (int i = 0; i < C::KCH; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c / (D / 8), col = (c % (D / 8)) * 8;
-      *reinterpret_cast<uint4*>(&Ks[row * KP + col]) = kr[i];
-    }
-#pragma unroll
-    for (int i = 0; i < C::VPR; ++i) {
-      const int c = tid + 256 * i;
-      const int kp = c % (BN / 2), dch = c / (BN / 2);
-      const uint16_t* e0 = reinterpret_cast<const uint16_t*>(&vr[2 * i]);
-      const uint16_t* e1 = reinterpret_cast<const uint16_t*>(&vr[2 * i + 1]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t packed = static_cast<uint32_t>(e0[e]) |
-                                (static_cast<uint32_t>(e1[e]) << 16);
-        *reinterpret_cast<uint32_t*>(&Vt[(dch * 8 + e) * VP + 2 * kp]) = packed;
-      }
-    }
+  // K / V tiles double-buffered in LDS, loaded asynchronously one tile ahead
+  constexpr int NL = 2 * tile_load_insts<D, BN>();
+  auto issue = [&](int64_t k0, int st) {
+    tile_load_async<T, D, BN>(Ks[st], Kp, a.k_ss, k0, a.Skv);
+    tile_load_async<T, D, BN>(Vs[st], Vp, a.v_ss, k0, a.Skv);
   };
 
   f32x16 o[D / 32];
 #pragma unroll
   for (int nt = 0; nt < D / 32; ++nt) o[nt] = f32x16{};
-  float m_i = -INFINITY, l_i = 0.f;
+  float m_ref = -INFINITY, l_i = 0.f;
   const float c2 = a.scale_log2;
+  const int iq = static_cast<int>(my_q), Sq32 = static_cast<int>(a.Sq),
+            Skv32 = static_cast<int>(a.Skv), W32 = static_cast<int>(a.window);
 
-  if (t_lo < t_hi) prefetch(t_lo * BN);
-  for (int64_t t = t_lo; t < t_hi; ++t) {
+  // One pipeline step on LDS stage ST (a compile-time constant, so every LDS
+  // address is a per-lane base plus an immediate offset).
+  auto step = [&](auto stage_tag, int64_t t) {
+    constexpr int st = decltype(stage_tag)::value;
     const int64_t k0 = t * BN;
-    __syncthreads();
-    store_lds();
-    __syncthreads();
-    if (t + 1 < t_hi) prefetch(k0 + BN);
+    __syncthreads();  // every wave is done with the other stage
+    if (t + 1 < t_hi) {
+      issue(k0 + BN, st ^ 1);
+      wait_vmcnt<NL>();  // this wave's loads of tile t have landed
+    } else {
+      wait_vmcnt<0>();
+    }
+    __syncthreads();  // ... and every other wave's
+    const T* Kt = Ks[st];
+    const T* Vt = Vs[st];
 
     // wave-uniform tile classification
     bool skip = false, need_mask = k0 + BN > a.Skv;
@@ -155,7 +131,7 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
       if (k0 + BN - 1 <= qmin - a.window) skip = true;
       if (k0 <= qmax - a.window) need_mask = true;
     }
-    if (skip) continue;
+    if (skip) return;
 
     // The tile body is instantiated with and without the element mask so
     // that the masking writes sit in the same straight-line block as the MFMA
@@ -169,8 +145,7 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
         s[tt] = f32x16{};
 #pragma unroll
         for (int ks = 0; ks < D / 16; ++ks) {
-          const V8 kv = *reinterpret_cast<const V8*>(
-              &Ks[(32 * tt + l32) * KP + 16 * ks + 8 * g]);
+          const V8 kv = *reinterpret_cast<const V8*>(&Kt[tile_off<D>(32 * tt + l32, 16 * ks + 8 * g)]);
           s[tt] = M::mma(kv, qreg[ks], s[tt]);
         }
       }
@@ -179,9 +154,8 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
         for (int tt = 0; tt < BN / 32; ++tt)
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
-            const int64_t key = k0 + 32 * tt + 8 * (j >> 2) + 4 * g + (j & 3);
-            if (!attn_visible(my_q, key, a.Skv, a.causal, a.window))
-              s[tt][j] = -INFINITY;
+            const int key = static_cast<int>(k0) + 32 * tt + 8 * (j >> 2) + 4 * g + (j & 3);
+            if (!visible32(iq, key, Sq32, Skv32, a.causal, W32)) s[tt][j] = -INFINITY;
           }
       }
       float mloc = -INFINITY;
@@ -190,11 +164,17 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, s[tt][j]);
       mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-      const float m_new = fmaxf(m_i, mloc);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = fast_exp2((m_i - m_use) * c2);
-      m_i = m_new;
-      const float mc = m_use * c2;
+      // move the reference maximum only when it has grown past the threshold
+      const bool grow = (mloc - m_ref) * c2 > kRescaleThreshold;
+      if (__any(grow)) {
+        const float m_new = fmaxf(m_ref, mloc);
+        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2((m_ref - m_new) * c2);
+        m_ref = m_new;
+        l_i *= alpha;
+#pragma unroll
+        for (int nt = 0; nt < D / 32; ++nt) o[nt] *= alpha;
+      }
+      const float mc = m_ref == -INFINITY ? 0.f : m_ref * c2;
 
       // P^T (packed per 16-key MFMA step) and row sums
       V8 pb[BN / 16];
@@ -207,21 +187,16 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
           lsum += p;
           pb[2 * tt + (j >> 3)][j & 7] = static_cast<T>(p);
         }
-      l_i = l_i * alpha + lsum;
-#pragma unroll
-      for (int nt = 0; nt < D / 32; ++nt) o[nt] *= alpha;
+      l_i += lsum;
 
-      // O^T += V^T P^T
+      // O^T += V^T P^T (V^T read transposed from the row-major V tile)
 #pragma unroll
-      for (int nt = 0; nt < D / 32; ++nt) {
-        const T* vrow = &Vt[(32 * nt + l32) * VP];
+      for (int kk = 0; kk < BN / 16; ++kk) {
+        const int klo = 16 * kk + 4 * g, khi = 16 * kk + 8 + 4 * g;
 #pragma unroll
-        for (int kk = 0; kk < BN / 16; ++kk) {
-          const int kb = 16 * kk + 4 * g;
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + kb);
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + kb + 8);
-          const u32x4 w = {lo[0], lo[1], hi[0], hi[1]};
-          o[nt] = M::mma(__builtin_bit_cast(V8, w), pb[kk], o[nt]);
+        for (int nt = 0; nt < D / 32; ++nt) {
+          const V8 vA = lds_tr_operand<T, D>(Vt, 32 * nt, klo, khi);
+          o[nt] = M::mma(vA, pb[kk], o[nt]);
         }
       }
     };
@@ -229,6 +204,12 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
       tile(std::true_type{});
     else
       tile(std::false_type{});
+  };
+
+  if (t_lo < t_hi) issue(t_lo * BN, 0);
+  for (int64_t t = t_lo; t < t_hi; t += 2) {
+    step(std::integral_constant<int, 0>{}, t);
+    if (t + 1 < t_hi) step(std::integral_constant<int, 1>{}, t + 1);
   }
 
   const float l_tot = l_i + __shfl_xor(l_i, 32, 64);
@@ -248,7 +229,7 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
       }
     if (g == 0)
       a.lse_out[(b * a.Hq + hq) * a.Sq + my_q] =
-          l_tot > 0.f ? m_i * a.scale + logf(l_tot) : -INFINITY;
+          l_tot > 0.f ? m_ref * a.scale + logf(l_tot) : -INFINITY;
   }
 }
 
