@@ -184,6 +184,8 @@ def main():
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--seq", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--default-gemm", action="store_true",
+                    help="use hipBLASLt's default solution heuristic instead of the recorded table")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -194,7 +196,10 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda:0")
     from zorse_amd import flops
+    from zorse_amd.gemm_tuning import use_tuned_gemms
     from zorse_amd.stage import StageRunner
+
+    tuned = use_tuned_gemms(not args.default_gemm)
 
     S, B = args.seq, 1
     cfg, layers, g = build_stage(args.layers, dev)
@@ -246,6 +251,9 @@ def main():
                    "layers": args.layers, "hidden": spec.hidden, "heads": spec.heads,
                    "head_dim": spec.head_dim, "ffn": spec.ffn, "micro_batch": B, "seq_len": S,
                    "global_batch": B, "parallelism": "none (1 GPU)",
+                   "projection_gemms": "hipBLASLt via torch.mm/addmm" + (
+                       " (recorded TunableOp solutions, zorse_amd/tunableop_gfx950.csv)"
+                       if tuned else " (default heuristic)"),
                    "stage_tokens_per_s": round(B * S / (ms_step / 1e3), 1),
                    "layer_fwd_bwd_tflops": round(layer_tflops, 1)},
         "roofline": {"bound": "mfma", "achieved": a["achieved"], "peak": a["peak"],

@@ -3,8 +3,9 @@
 // One pass over HBM: read p, g, m, v; write p, m, v (and the low-precision
 // compute copy of p when requested).  28 bytes per element with an fp32
 // grad, 26 with a bf16/fp16 grad, +2 for the low-precision copy.  Each thread
-// handles 4 consecutive elements per iteration (16-byte fp32 accesses) in a
-// grid-stride loop sized to keep every CU busy with several workgroups.
+// handles 8 consecutive elements per iteration (16-byte accesses on every
+// stream) in a grid-stride loop sized to keep every CU busy with several
+// workgroups; a scalar kernel finishes unaligned heads and ragged tails.
 #include <cmath>
 
 #include "zk_common.h"
@@ -80,28 +81,84 @@ __device__ __forceinline__ float adam_one(float& p, float g, float& m, float& v,
   return p;
 }
 
-// L = low-precision copy type; L = float means "no copy".
+// 8 elements per thread per iteration: p, m, v as two 16-byte accesses each,
+// the gradient and the low-precision copy as one 16-byte access for 2-byte
+// types (two for fp32).  L = float with kCopy = false means "no copy".
+template <typename G>
+__device__ __forceinline__ void load_grad8(const G* g, int64_t i, float (&o)[8]) {
+  float a[4], b[4];
+  load_grad4<G>(g, i, a);
+  load_grad4<G>(g, i + 4, b);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    o[k] = a[k];
+    o[k + 4] = b[k];
+  }
+}
+template <>
+__device__ __forceinline__ void load_grad8<bf16>(const bf16* g, int64_t i, float (&o)[8]) {
+  const bf16x8 a = *reinterpret_cast<const bf16x8*>(g + i);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) o[k] = static_cast<float>(a[k]);
+}
+template <>
+__device__ __forceinline__ void load_grad8<f16>(const f16* g, int64_t i, float (&o)[8]) {
+  const f16x8 a = *reinterpret_cast<const f16x8*>(g + i);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) o[k] = static_cast<float>(a[k]);
+}
+
+template <typename L>
+__device__ __forceinline__ void store8(L* dst, const float4& x, const float4& y) {
+  store4<L>(dst, x);
+  store4<L>(dst + 4, y);
+}
+template <>
+__device__ __forceinline__ void store8<bf16>(bf16* dst, const float4& x, const float4& y) {
+  const bf16x8 a = {static_cast<bf16>(x.x), static_cast<bf16>(x.y), static_cast<bf16>(x.z),
+                    static_cast<bf16>(x.w), static_cast<bf16>(y.x), static_cast<bf16>(y.y),
+                    static_cast<bf16>(y.z), static_cast<bf16>(y.w)};
+  *reinterpret_cast<bf16x8*>(dst) = a;
+}
+template <>
+__device__ __forceinline__ void store8<f16>(f16* dst, const float4& x, const float4& y) {
+  const f16x8 a = {static_cast<f16>(x.x), static_cast<f16>(x.y), static_cast<f16>(x.z),
+                   static_cast<f16>(x.w), static_cast<f16>(y.x), static_cast<f16>(y.y),
+                   static_cast<f16>(y.z), static_cast<f16>(y.w)};
+  *reinterpret_cast<f16x8*>(dst) = a;
+}
+
 template <typename G, typename L, bool kCopy>
-__global__ __launch_bounds__(256) void adamw_vec4(
+__global__ __launch_bounds__(256) void adamw_vec8(
     float* __restrict__ p, const G* __restrict__ g, float* __restrict__ m,
-    float* __restrict__ v, L* __restrict__ lowp, int64_t n4, AdamScalars s) {
+    float* __restrict__ v, L* __restrict__ lowp, int64_t n8, AdamScalars s) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-       q < n4; q += stride) {
-    const int64_t i = q * 4;
-    float4 pv = *reinterpret_cast<const float4*>(p + i);
-    float4 mv = *reinterpret_cast<const float4*>(m + i);
-    float4 vv = *reinterpret_cast<const float4*>(v + i);
-    float gv[4];
-    load_grad4<G>(g, i, gv);
-    adam_one(pv.x, gv[0], mv.x, vv.x, s);
-    adam_one(pv.y, gv[1], mv.y, vv.y, s);
-    adam_one(pv.z, gv[2], mv.z, vv.z, s);
-    adam_one(pv.w, gv[3], mv.w, vv.w, s);
-    *reinterpret_cast<float4*>(p + i) = pv;
-    *reinterpret_cast<float4*>(m + i) = mv;
-    *reinterpret_cast<float4*>(v + i) = vv;
-    if (kCopy) store4<L>(lowp + i, pv);
+       q < n8; q += stride) {
+    const int64_t i = q * 8;
+    float4 p0 = *reinterpret_cast<const float4*>(p + i);
+    float4 p1 = *reinterpret_cast<const float4*>(p + i + 4);
+    float4 m0 = *reinterpret_cast<const float4*>(m + i);
+    float4 m1 = *reinterpret_cast<const float4*>(m + i + 4);
+    float4 v0 = *reinterpret_cast<const float4*>(v + i);
+    float4 v1 = *reinterpret_cast<const float4*>(v + i + 4);
+    float gv[8];
+    load_grad8<G>(g, i, gv);
+    adam_one(p0.x, gv[0], m0.x, v0.x, s);
+    adam_one(p0.y, gv[1], m0.y, v0.y, s);
+    adam_one(p0.z, gv[2], m0.z, v0.z, s);
+    adam_one(p0.w, gv[3], m0.w, v0.w, s);
+    adam_one(p1.x, gv[4], m1.x, v1.x, s);
+    adam_one(p1.y, gv[5], m1.y, v1.y, s);
+    adam_one(p1.z, gv[6], m1.z, v1.z, s);
+    adam_one(p1.w, gv[7], m1.w, v1.w, s);
+    *reinterpret_cast<float4*>(p + i) = p0;
+    *reinterpret_cast<float4*>(p + i + 4) = p1;
+    *reinterpret_cast<float4*>(m + i) = m0;
+    *reinterpret_cast<float4*>(m + i + 4) = m1;
+    *reinterpret_cast<float4*>(v + i) = v0;
+    *reinterpret_cast<float4*>(v + i + 4) = v1;
+    if (kCopy) store8<L>(lowp + i, p0, p1);
   }
 }
 
@@ -125,20 +182,20 @@ __global__ __launch_bounds__(256) void adamw_scalar(
 
 template <typename G>
 static void launch_vec(float* p, const void* g, float* m, float* v, void* lowp,
-                       int ldt, int64_t n4, const AdamScalars& s, int grid,
+                       int ldt, int64_t n8, const AdamScalars& s, int grid,
                        hipStream_t st) {
   if (lowp == nullptr)
-    hipLaunchKernelGGL((adamw_vec4<G, float, false>), dim3(grid), dim3(256), 0,
-                       st, p, (const G*)g, m, v, (float*)nullptr, n4, s);
+    hipLaunchKernelGGL((adamw_vec8<G, float, false>), dim3(grid), dim3(256), 0,
+                       st, p, (const G*)g, m, v, (float*)nullptr, n8, s);
   else if (ldt == ZK_BF16)
-    hipLaunchKernelGGL((adamw_vec4<G, bf16, true>), dim3(grid), dim3(256), 0,
-                       st, p, (const G*)g, m, v, (bf16*)lowp, n4, s);
+    hipLaunchKernelGGL((adamw_vec8<G, bf16, true>), dim3(grid), dim3(256), 0,
+                       st, p, (const G*)g, m, v, (bf16*)lowp, n8, s);
   else if (ldt == ZK_F16)
-    hipLaunchKernelGGL((adamw_vec4<G, f16, true>), dim3(grid), dim3(256), 0,
-                       st, p, (const G*)g, m, v, (f16*)lowp, n4, s);
+    hipLaunchKernelGGL((adamw_vec8<G, f16, true>), dim3(grid), dim3(256), 0,
+                       st, p, (const G*)g, m, v, (f16*)lowp, n8, s);
   else
-    hipLaunchKernelGGL((adamw_vec4<G, float, true>), dim3(grid), dim3(256), 0,
-                       st, p, (const G*)g, m, v, (float*)lowp, n4, s);
+    hipLaunchKernelGGL((adamw_vec8<G, float, true>), dim3(grid), dim3(256), 0,
+                       st, p, (const G*)g, m, v, (float*)lowp, n8, s);
 }
 
 }  // namespace zk
@@ -179,21 +236,21 @@ extern "C" int zk_adamw_step(float* param, const void* grad, int grad_dtype,
   const int gbytes = dtype_bytes(grad_dtype);
   const bool vec = aligned(param, 16) && aligned(exp_avg, 16) &&
                    aligned(exp_avg_sq, 16) && aligned(grad, 4 * gbytes) &&
-                   (param_lowp == nullptr ||
-                    aligned(param_lowp, 4 * dtype_bytes(lowp_dtype)));
-  const int64_t n4 = vec ? n / 4 : 0;
-  const int max_grid = device_cus() * 8;
-  if (n4 > 0) {
-    int64_t want = (n4 + 255) / 256;
+                   aligned(grad, 16) &&
+                   (param_lowp == nullptr || aligned(param_lowp, 16));
+  const int64_t n8 = vec ? n / 8 : 0;
+  const int max_grid = device_cus() * 16;
+  if (n8 > 0) {
+    int64_t want = (n8 + 255) / 256;
     const int grid = static_cast<int>(want < max_grid ? want : max_grid);
     if (grad_dtype == ZK_F32)
-      launch_vec<float>(param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_dtype, n4, s, grid, st);
+      launch_vec<float>(param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_dtype, n8, s, grid, st);
     else if (grad_dtype == ZK_BF16)
-      launch_vec<bf16>(param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_dtype, n4, s, grid, st);
+      launch_vec<bf16>(param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_dtype, n8, s, grid, st);
     else
-      launch_vec<f16>(param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_dtype, n4, s, grid, st);
+      launch_vec<f16>(param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_dtype, n8, s, grid, st);
   }
-  const int64_t begin = n4 * 4;
+  const int64_t begin = n8 * 8;
   if (begin < n) {
     int64_t want = (n - begin + 255) / 256;
     const int grid = static_cast<int>(want < max_grid ? want : max_grid);

@@ -69,6 +69,7 @@ template <int D>
 struct DkdvCfg {
   static constexpr int BK = 128;              // keys per workgroup (32 per wave)
   static constexpr int MQ = 64;               // queries per block
+  static constexpr int MB = MQ / 32;          // 32-row MFMA blocks per query block
 };
 
 template <typename T, int D>
@@ -81,8 +82,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
   // of the block's lse2 / delta vectors so every wave issues the same loads.
   __shared__ __attribute__((aligned(16))) T Qs[2][MQ * D];
   __shared__ __attribute__((aligned(16))) T dOs[2][MQ * D];
-  __shared__ __attribute__((aligned(16))) float lse2s[2][4][MQ];
-  __shared__ __attribute__((aligned(16))) float dels[2][4][MQ];
+  __shared__ __attribute__((aligned(16))) float lse2s[2][4][64];  // 64 lanes load, MQ used
+  __shared__ __attribute__((aligned(16))) float dels[2][4][64];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, g = lane >> 5;
@@ -174,24 +175,25 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
     const T* dOt = dOs[st];
     const float* l2v = lse2s[st][wave];
     const float* dlv = dels[st][wave];
+    const int qb32 = static_cast<int>(qb0);
 
-    f32x16 s[2], dp[2];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      s[mb] = f32x16{};
-      dp[mb] = f32x16{};
+    // S and dP of the 32-query half mb (rows 32 mb .. +31 of the block)
+    auto scores = [&](int mb, f32x16& sv, f32x16& dpv) {
+      sv = f32x16{};
+      dpv = f32x16{};
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
         const V8 qa = *reinterpret_cast<const V8*>(&Qt[tile_off<D>(32 * mb + l32, 16 * ks + 8 * g)]);
-        s[mb] = M::mma(qa, kreg[ks], s[mb]);
+        sv = M::mma(qa, kreg[ks], sv);
         const V8 da = *reinterpret_cast<const V8*>(&dOt[tile_off<D>(32 * mb + l32, 16 * ks + 8 * g)]);
-        dp[mb] = M::mma(da, vreg[ks], dp[mb]);
+        dpv = M::mma(da, vreg[ks], dpv);
       }
-    }
-    // P and dS; element j of block mb is query 32 mb + 8 (j/4) + 4 g + j%4
-    V8 pb[4], sb[4];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    };
+    // P and dS of half mb, packed as the B operands of two 16-query MFMA steps;
+    // element j is query 32 mb + 8 (j/4) + 4 g + j%4
+    auto probs = [&](auto mask_tag, int mb, const f32x16& sv, const f32x16& dpv, V8 (&pb)[2],
+                     V8 (&sb)[2]) {
+      constexpr bool kMask = decltype(mask_tag)::value;
 #pragma unroll
       for (int a4 = 0; a4 < 4; ++a4) {
         const int r0 = 32 * mb + 8 * a4 + 4 * g;
@@ -202,28 +204,71 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int j = 4 * a4 + e;
-          float p = __builtin_amdgcn_exp2f(fmaf(s[mb][j], c2, -lv[e]));
-          if (need_mask && !visible32(static_cast<int>(qb0) + r0 + e, ik, Sq32, Skv32,
-                                      a.causal, W32))
-            p = 0.f;
-          const float ds = p * (dp[mb][j] - dl[e]);
-          pb[2 * mb + (j >> 3)][j & 7] = static_cast<T>(p);
-          sb[2 * mb + (j >> 3)][j & 7] = static_cast<T>(ds);
+          float p = __builtin_amdgcn_exp2f(fmaf(sv[j], c2, -lv[e]));
+          if (kMask && !visible32(qb32 + r0 + e, ik, Sq32, Skv32, a.causal, W32)) p = 0.f;
+          pb[j >> 3][j & 7] = static_cast<T>(p);
+          sb[j >> 3][j & 7] = static_cast<T>(p * (dpv[j] - dl[e]));
         }
       }
-    // dV^T += dO^T P ; dK^T += Q^T dS.  Step kk covers queries 16 kk + perm:
-    // lane half g holds queries 16 kk + 4 g + 0..3 and 16 kk + 8 + 4 g + 0..3.
+    };
+    // dV^T += dO^T P ; dK^T += Q^T dS over the two 16-query steps of half mb.
+    // Step kk covers queries 16 kk + perm: lane half g holds queries
+    // 16 kk + 4 g + 0..3 and 16 kk + 8 + 4 g + 0..3.
+    auto accumulate = [&](int mb, const V8 (&pb)[2], const V8 (&sb)[2]) {
 #pragma unroll
-    for (int kk = 0; kk < MQ / 16; ++kk) {
-      const int klo = 16 * kk + 4 * g, khi = 16 * kk + 8 + 4 * g;
+      for (int h = 0; h < 2; ++h) {
+        const int kk = 2 * mb + h;
+        const int klo = 16 * kk + 4 * g, khi = 16 * kk + 8 + 4 * g;
 #pragma unroll
-      for (int nt = 0; nt < D / 32; ++nt) {
-        const V8 dA = lds_tr_operand<T, D>(dOt, 32 * nt, klo, khi);
-        dv[nt] = M::mma(dA, pb[kk], dv[nt]);
-        const V8 qA = lds_tr_operand<T, D>(Qt, 32 * nt, klo, khi);
-        dk[nt] = M::mma(qA, sb[kk], dk[nt]);
+        for (int nt = 0; nt < D / 32; ++nt) {
+          const V8 dA = lds_tr_operand<T, D>(dOt, 32 * nt, klo, khi);
+          dv[nt] = M::mma(dA, pb[h], dv[nt]);
+          const V8 qA = lds_tr_operand<T, D>(Qt, 32 * nt, klo, khi);
+          dk[nt] = M::mma(qA, sb[h], dk[nt]);
+        }
       }
-    }
+    };
+    // Software pipeline over the two halves: the VALU work of one half is
+    // issued between MFMAs that do not depend on it.
+    auto body = [&](auto mask_tag) {
+      f32x16 s0, dp0, s1, dp1;
+      V8 pb0[2], sb0[2], pb1[2], sb1[2];
+      scores(0, s0, dp0);
+      scores(1, s1, dp1);
+      probs(mask_tag, 0, s0, dp0, pb0, sb0);
+      accumulate(0, pb0, sb0);
+      probs(mask_tag, 1, s1, dp1, pb1, sb1);
+      accumulate(1, pb1, sb1);
+      // Issue order for the scheduler (groups: DS read 0x100, MFMA 0x008,
+      // VALU 0x002): the score MFMAs of half 1 carry the softmax of half 0,
+      // the dV / dK MFMAs of half 0 carry the softmax of half 1.
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+    };
+    if (need_mask)
+      body(std::true_type{});
+    else
+      body(std::false_type{});
   };
 
   if (n_iter > 0) issue(0, 0);
@@ -263,7 +308,7 @@ struct DqCfg {
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dq(AttnArgs a, int64_t n_qt) {
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) {
   typedef DqCfg<D> C;
   typedef Mfma<T> M;
   typedef typename M::vec8 V8;

@@ -1,19 +1,24 @@
 // RMSNorm forward / backward for gfx950.
 //
-// One workgroup per row (forward) keeps the row in registers: NT threads x
-// MAXCH chunks of 8 elements (16-byte loads for 2-byte types), so x is read
-// once and y written once -- the HBM minimum.  The backward walks rows with a
-// grid of at most kBwdParts workgroups; each thread owns fixed columns, so the
-// weight gradient accumulates in registers and is written as one fp32 partial
-// row per workgroup, then reduced by a second kernel (deterministic, no
-// atomics).  Rows whose width is not a multiple of 8 (or misaligned buffers)
-// take the scalar kernels, which read the row twice.
+// Vector kernels: NT threads x CH chunks of 8 elements per row (16-byte
+// accesses for 2-byte types), CH a compile-time constant so a row lives in
+// exactly CH x 8 registers per thread.  The forward runs one workgroup per
+// row: x is read once and y written once, the HBM minimum.  The backward
+// walks rows in groups of kBwdRows with a grid of at most kBwdParts
+// workgroups: the group's dy, h (and residual gradient) loads are all issued
+// before its row reductions, the row sums share one pair of barriers, each
+// thread accumulates the weight gradient of its fixed columns in registers,
+// and every workgroup writes one fp32 partial row that a second kernel
+// reduces deterministically (no atomics).  Rows whose width is not a
+// multiple of 8, wider than 8192, or misaligned buffers take the scalar
+// kernels, which read the row twice.
 #include "vec.h"
 
 namespace zk {
 
-static constexpr int kBwdParts = 512;
-static constexpr int kMaxCh = 4;
+static constexpr int kBwdParts = 512;  // workgroups (= dw partial rows) of the backward
+static constexpr int kBwdRows = 4;     // rows a backward workgroup keeps in flight
+static constexpr int kMaxCh = 4;       // chunks of 8 per thread: hidden <= 256 * 4 * 8
 
 template <int NT>
 __device__ __forceinline__ float block_sum(float v, float* red) {
@@ -32,7 +37,7 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 }
 
 // ---------------------------------------------------------------- forward ---
-template <typename T, typename W, int NT>
+template <typename T, typename W, int NT, int CH>
 __global__ __launch_bounds__(NT) void rmsnorm_fwd_vec(
     const T* __restrict__ x, const T* __restrict__ res, T* __restrict__ hout,
     const W* __restrict__ w, T* __restrict__ y, float* __restrict__ rstd,
@@ -41,10 +46,10 @@ __global__ __launch_bounds__(NT) void rmsnorm_fwd_vec(
   const int64_t row = blockIdx.x;
   const T* xr = x + row * hidden;
   const int nchunk = static_cast<int>(hidden / 8);
-  float v[kMaxCh][8];
+  float v[CH][8];
   float ss = 0.f;
 #pragma unroll
-  for (int c = 0; c < kMaxCh; ++c) {
+  for (int c = 0; c < CH; ++c) {
     const int ch = threadIdx.x + c * NT;
     if (ch < nchunk) {
       Vec8<T>::load(xr + ch * 8, v[c]);
@@ -63,7 +68,7 @@ __global__ __launch_bounds__(NT) void rmsnorm_fwd_vec(
   const float r = 1.0f / sqrtf(ss / static_cast<float>(hidden) + eps);
   if (threadIdx.x == 0) rstd[row] = r;
 #pragma unroll
-  for (int c = 0; c < kMaxCh; ++c) {
+  for (int c = 0; c < CH; ++c) {
     const int ch = threadIdx.x + c * NT;
     if (ch < nchunk) {
       float w8[8], o[8];
@@ -105,63 +110,115 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_scalar(
 }
 
 // --------------------------------------------------------------- backward ---
-template <typename T, typename W, int NT>
-__global__ __launch_bounds__(NT) void rmsnorm_bwd_vec(
+// R rows are processed together: all their loads are issued before the
+// first reduction, and the R row sums share one pair of barriers, so a
+// workgroup keeps R rows of dy and h in flight.
+template <int NT, int R>
+__device__ __forceinline__ void block_sum_rows(float (&v)[R], float* red) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int r = 0; r < R; ++r) v[r] = wave_sum(v[r]);
+  if (NT > 64) {
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) red[r * (NT / 64) + wave] = v[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float t = 0.f;
+#pragma unroll
+      for (int i = 0; i < NT / 64; ++i) t += red[r * (NT / 64) + i];
+      v[r] = t;
+    }
+    __syncthreads();
+  }
+}
+
+template <typename T, typename W, int NT, int R, int CH, bool kRes>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2)))
+void rmsnorm_bwd_vec(
     const T* __restrict__ dy, const T* __restrict__ h, const W* __restrict__ w,
     const float* __restrict__ rstd, const T* __restrict__ dres,
     T* __restrict__ dx, float* __restrict__ part, int64_t rows,
     int64_t hidden) {
-  __shared__ float red[NT / 64];
+  __shared__ float red[R * (NT / 64)];
   const int nchunk = static_cast<int>(hidden / 8);
-  float wv[kMaxCh][8], dw[kMaxCh][8];
+  float wv[CH][8], dw[CH][8];
 #pragma unroll
-  for (int c = 0; c < kMaxCh; ++c) {
+  for (int c = 0; c < CH; ++c) {
     const int ch = threadIdx.x + c * NT;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) dw[c][i] = 0.f;
+    for (int i = 0; i < 8; ++i) {
+      dw[c][i] = 0.f;
+      wv[c][i] = 0.f;
+    }
     if (ch < nchunk) Vec8<W>::load(w + ch * 8, wv[c]);
   }
-  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
-    const float r = rstd[row];
-    float g[kMaxCh][8], xh[kMaxCh][8];
-    float dot = 0.f;
+  for (int64_t row0 = static_cast<int64_t>(blockIdx.x) * R; row0 < rows;
+       row0 += static_cast<int64_t>(gridDim.x) * R) {
+    Raw8<T> d8[R][CH], h8[R][CH], g8[kRes ? R : 1][CH];
+    float dot[R], r[R];
 #pragma unroll
-    for (int c = 0; c < kMaxCh; ++c) {
-      const int ch = threadIdx.x + c * NT;
-      if (ch < nchunk) {
-        float d8[8], h8[8];
-        Vec8<T>::load(dy + row * hidden + ch * 8, d8);
-        Vec8<T>::load(h + row * hidden + ch * 8, h8);
+    for (int k = 0; k < R; ++k) {
+      const int64_t row = row0 + k < rows ? row0 + k : rows - 1;
+      r[k] = row0 + k < rows ? rstd[row] : 0.f;  // r = 0: the row contributes nothing
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          xh[c][i] = h8[i] * r;
-          g[c][i] = d8[i] * wv[c][i];
-          dot = fmaf(g[c][i], xh[c][i], dot);
-          dw[c][i] = fmaf(d8[i], round_to<T>(xh[c][i]), dw[c][i]);
+      for (int c = 0; c < CH; ++c) {
+        const int ch = threadIdx.x + c * NT;
+        if (ch < nchunk) {
+          d8[k][c].load(dy + row * hidden + ch * 8);
+          h8[k][c].load(h + row * hidden + ch * 8);
+          if (kRes) g8[kRes ? k : 0][c].load(dres + row * hidden + ch * 8);
+        } else {
+          d8[k][c].zero();
+          h8[k][c].zero();
         }
       }
     }
-    dot = block_sum<NT>(dot, red);
-    const float mean = dot / static_cast<float>(hidden);
 #pragma unroll
-    for (int c = 0; c < kMaxCh; ++c) {
-      const int ch = threadIdx.x + c * NT;
-      if (ch < nchunk) {
-        float o[8];
+    for (int k = 0; k < R; ++k) {
+      dot[k] = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = r * (g[c][i] - xh[c][i] * mean);
-        if (dres != nullptr) {
-          float r8[8];
-          Vec8<T>::load(dres + row * hidden + ch * 8, r8);
+      for (int c = 0; c < CH; ++c)
 #pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] += r8[i];
+        for (int i = 0; i < 8; ++i) {
+          const float xh = h8[k][c][i] * r[k];
+          dot[k] = fmaf(d8[k][c][i] * wv[c][i], xh, dot[k]);
+          dw[c][i] = fmaf(d8[k][c][i], round_to<T>(xh), dw[c][i]);
         }
-        Vec8<T>::store(dx + row * hidden + ch * 8, o);
+    }
+    block_sum_rows<NT, R>(dot, red);
+#pragma unroll
+    for (int k = 0; k < R; ++k)
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        d8[k][c].opaque();
+        h8[k][c].opaque();
+      }
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const int64_t row = row0 + k;
+      if (row >= rows) break;
+      const float mean = dot[k] / static_cast<float>(hidden);
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int ch = threadIdx.x + c * NT;
+        if (ch < nchunk) {
+          float o[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float xh = h8[k][c][i] * r[k];
+            o[i] = r[k] * (d8[k][c][i] * wv[c][i] - xh * mean);
+            if (kRes) o[i] += g8[kRes ? k : 0][c][i];
+          }
+          Vec8<T>::store(dx + row * hidden + ch * 8, o);
+        }
       }
     }
   }
 #pragma unroll
-  for (int c = 0; c < kMaxCh; ++c) {
+  for (int c = 0; c < CH; ++c) {
     const int ch = threadIdx.x + c * NT;
     if (ch < nchunk)
       Vec8<float>::store(part + static_cast<int64_t>(blockIdx.x) * hidden + ch * 8,
@@ -203,46 +260,81 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_scalar(
 }
 
 // dw[c] = sum_p part[p][c]  (optionally added to the existing dw).  A
-// workgroup owns 64 columns; its 4 waves stride over the partial rows and
-// meet in LDS.  nparts == 0 writes zeros (or leaves dw unchanged).
-__global__ __launch_bounds__(256) void rmsnorm_dw_reduce(
+// workgroup owns 64 columns; its 16 waves stride over the partial rows with 4
+// independent running sums each and meet in LDS.  nparts == 0 writes zeros
+// (or leaves dw unchanged).
+__global__ __launch_bounds__(1024) void rmsnorm_dw_reduce(
     const float* __restrict__ part, int64_t nparts, int64_t hidden,
     void* __restrict__ dw, int wdt, int accumulate) {
-  __shared__ float red[4][64];
+  __shared__ float red[16][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t c = static_cast<int64_t>(blockIdx.x) * 64 + lane;
-  float s = 0.f;
-  if (c < hidden)
-    for (int64_t p = wave; p < nparts; p += 4) s += part[p * hidden + c];
-  red[wave][lane] = s;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  if (c < hidden) {
+    int64_t p = wave;
+    for (; p + 48 < nparts; p += 64) {
+      s0 += part[p * hidden + c];
+      s1 += part[(p + 16) * hidden + c];
+      s2 += part[(p + 32) * hidden + c];
+      s3 += part[(p + 48) * hidden + c];
+    }
+    for (; p < nparts; p += 16) s0 += part[p * hidden + c];
+  }
+  red[wave][lane] = (s0 + s1) + (s2 + s3);
   __syncthreads();
   if (wave == 0 && c < hidden) {
-    s = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
-    if (accumulate) s += load_dt(dw, c, wdt);
-    store_dt(dw, c, wdt, s);
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t += red[i][lane];
+    if (accumulate) t += load_dt(dw, c, wdt);
+    store_dt(dw, c, wdt, t);
   }
 }
 
 // ------------------------------------------------------------ dispatch ------
-static int pick_threads(int64_t hidden) {
+// Threads per row and chunks per thread for a row of `hidden` elements.
+static void pick_shape(int64_t hidden, int& nt, int& ch) {
   const int64_t nchunk = hidden / 8;
-  if (nchunk > 128 * kMaxCh) return 256;
-  if (nchunk > 64 * kMaxCh) return 128;
-  return 64;
+  nt = nchunk <= 64 ? 64 : nchunk <= 128 ? 128 : 256;
+  ch = static_cast<int>((nchunk + nt - 1) / nt);
 }
 
 template <typename T, typename W>
 static void launch_fwd_vec(const void* x, const void* res, void* hout,
                            const void* w, void* y, float* rstd, int64_t rows,
                            int64_t hidden, float eps, hipStream_t s) {
-  const int nt = pick_threads(hidden);
-#define ZK_LAUNCH(NT)                                                       \
-  hipLaunchKernelGGL((rmsnorm_fwd_vec<T, W, NT>), dim3(rows), dim3(NT), 0, s, \
-                     (const T*)x, (const T*)res, (T*)hout, (const W*)w,     \
-                     (T*)y, rstd, hidden, eps)
-  if (nt == 256) ZK_LAUNCH(256);
-  else if (nt == 128) ZK_LAUNCH(128);
-  else ZK_LAUNCH(64);
+  int nt, ch;
+  pick_shape(hidden, nt, ch);
+#define ZK_LAUNCH(NT, CH)                                                          \
+  hipLaunchKernelGGL((rmsnorm_fwd_vec<T, W, NT, CH>), dim3(rows), dim3(NT), 0, s,  \
+                     (const T*)x, (const T*)res, (T*)hout, (const W*)w, (T*)y, rstd, \
+                     hidden, eps)
+  if (nt == 64) ZK_LAUNCH(64, 1);
+  else if (nt == 128) ZK_LAUNCH(128, 1);
+  else if (ch == 1) ZK_LAUNCH(256, 1);
+  else if (ch == 2) ZK_LAUNCH(256, 2);
+  else if (ch == 3) ZK_LAUNCH(256, 3);
+  else ZK_LAUNCH(256, 4);
+#undef ZK_LAUNCH
+}
+
+template <typename T, typename W, bool kRes>
+static void launch_bwd_vec_r(const void* dy, const void* h, const void* w,
+                             const float* rstd, const void* dres, void* dx,
+                             float* part, int64_t nparts, int64_t rows,
+                             int64_t hidden, hipStream_t s) {
+  int nt, ch;
+  pick_shape(hidden, nt, ch);
+#define ZK_LAUNCH(NT, CH)                                                          \
+  hipLaunchKernelGGL((rmsnorm_bwd_vec<T, W, NT, kBwdRows, CH, kRes>), dim3(nparts), \
+                     dim3(NT), 0, s, (const T*)dy, (const T*)h, (const W*)w, rstd,  \
+                     (const T*)dres, (T*)dx, part, rows, hidden)
+  if (nt == 64) ZK_LAUNCH(64, 1);
+  else if (nt == 128) ZK_LAUNCH(128, 1);
+  else if (ch == 1) ZK_LAUNCH(256, 1);
+  else if (ch == 2) ZK_LAUNCH(256, 2);
+  else if (ch == 3) ZK_LAUNCH(256, 3);
+  else ZK_LAUNCH(256, 4);
 #undef ZK_LAUNCH
 }
 
@@ -251,15 +343,10 @@ static void launch_bwd_vec(const void* dy, const void* h, const void* w,
                            const float* rstd, const void* dres, void* dx,
                            float* part, int64_t nparts, int64_t rows,
                            int64_t hidden, hipStream_t s) {
-  const int nt = pick_threads(hidden);
-#define ZK_LAUNCH(NT)                                                          \
-  hipLaunchKernelGGL((rmsnorm_bwd_vec<T, W, NT>), dim3(nparts), dim3(NT), 0, s, \
-                     (const T*)dy, (const T*)h, (const W*)w, rstd,             \
-                     (const T*)dres, (T*)dx, part, rows, hidden)
-  if (nt == 256) ZK_LAUNCH(256);
-  else if (nt == 128) ZK_LAUNCH(128);
-  else ZK_LAUNCH(64);
-#undef ZK_LAUNCH
+  if (dres != nullptr)
+    launch_bwd_vec_r<T, W, true>(dy, h, w, rstd, dres, dx, part, nparts, rows, hidden, s);
+  else
+    launch_bwd_vec_r<T, W, false>(dy, h, w, rstd, dres, dx, part, nparts, rows, hidden, s);
 }
 
 template <typename T>
@@ -284,7 +371,7 @@ static void dispatch_w_bwd(int wdt, const void* dy, const void* h,
 
 static bool vec_ok(int64_t hidden, int adt, int wdt,
                    std::initializer_list<const void*> ptrs) {
-  if (hidden % 8 != 0 || hidden / 8 > 256 * kMaxCh) return false;
+  if (hidden % 8 != 0 || hidden / 8 > 256 * kMaxCh) return false;  // hidden <= 8192
   for (const void* p : ptrs)
     if (p != nullptr && !aligned(p, 16)) return false;
   (void)adt;
@@ -325,7 +412,8 @@ extern "C" int zk_rmsnorm_fwd(const void* x, const void* residual, void* h_out,
 
 extern "C" int64_t zk_rmsnorm_bwd_workspace(int64_t rows, int64_t hidden) {
   if (rows <= 0 || hidden <= 0) return 0;
-  const int64_t parts = rows < kBwdParts ? rows : kBwdParts;
+  const int64_t groups = (rows + kBwdRows - 1) / kBwdRows;
+  const int64_t parts = groups < kBwdParts ? groups : kBwdParts;
   return parts * hidden;
 }
 
@@ -359,7 +447,7 @@ extern "C" int zk_rmsnorm_bwd(const void* dy, const void* h, const void* w,
                        w, rstd, dres, dx, workspace, rows, hidden, act_dtype,
                        w_dtype);
   }
-  hipLaunchKernelGGL(rmsnorm_dw_reduce, dim3((hidden + 63) / 64), dim3(256),
+  hipLaunchKernelGGL(rmsnorm_dw_reduce, dim3((hidden + 63) / 64), dim3(1024),
                      0, s, workspace, parts, hidden, dw, w_dtype, accumulate);
   return launch_status("zk_rmsnorm_bwd");
 }

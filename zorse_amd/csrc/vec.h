@@ -51,4 +51,40 @@ struct Vec8<f16> {
   }
 };
 
+// 8 elements kept in their storage format (4 VGPRs for 2-byte types) and
+// widened on use: lets a kernel keep several rows in flight cheaply.
+template <typename T>
+struct Raw8 {
+  uint4 u;
+  __device__ __forceinline__ void load(const T* p) { u = *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ float operator[](int i) const {
+    typedef T T8 __attribute__((ext_vector_type(8)));
+    return static_cast<float>(__builtin_bit_cast(T8, u)[i]);
+  }
+  __device__ __forceinline__ void zero() { u = make_uint4(0, 0, 0, 0); }
+  // Hide the value from the optimizer so widened copies are not kept alive
+  // across a barrier (they are recomputed from the packed form instead).
+  __device__ __forceinline__ void opaque() {
+    asm volatile("" : "+v"(u.x), "+v"(u.y), "+v"(u.z), "+v"(u.w));
+  }
+};
+template <>
+struct Raw8<float> {
+  float4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = reinterpret_cast<const float4*>(p)[0];
+    b = reinterpret_cast<const float4*>(p)[1];
+  }
+  __device__ __forceinline__ float operator[](int i) const {
+    const float4& v = i < 4 ? a : b;
+    const int j = i & 3;
+    return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
+  }
+  __device__ __forceinline__ void zero() { a = b = make_float4(0.f, 0.f, 0.f, 0.f); }
+  __device__ __forceinline__ void opaque() {
+    asm volatile("" : "+v"(a.x), "+v"(a.y), "+v"(a.z), "+v"(a.w));
+    asm volatile("" : "+v"(b.x), "+v"(b.y), "+v"(b.z), "+v"(b.w));
+  }
+};
+
 }  // namespace zk
