@@ -169,3 +169,50 @@ def test_flop_and_byte_counts_match_survey_table():
     spec = LayerSpec(hidden=4096, heads=32, kv_heads=32, head_dim=128, ffn=11008)
     assert round(flops.layer_fwd_bwd_flops(spec, 1, 4096) / 1e12, 3) == 5.455
     assert flops.adamw_bytes(202_383_360, 4, False) == 28 * 202_383_360
+
+
+def test_llama_v2_structure_and_ffn_rule():
+    from zorse_amd import llama_v2 as V
+    # FeedForward width rule (models/llama_v2.py:300-309)
+    assert V.ffn_hidden_dim(V.ModelArgs(dim=4096)) == 11008
+    assert V.ffn_hidden_dim(V.ModelArgs(dim=512, multiple_of=64)) == 1408
+    assert V.ffn_hidden_dim(V.ModelArgs(dim=512, intermediate_size=777)) == 777
+    args = V.ModelArgs(dim=64, n_heads=4, n_kv_heads=2, n_layers=2, vocab_size=32,
+                       multiple_of=16)
+    blk = V.TransformerBlock(1, args)
+    assert blk.spec.interleaved_rope and blk.spec.eps == 1e-5 and blk.spec.kv_heads == 2
+    assert blk.attention.wk.weight.shape == (32, 64)
+    assert blk.feed_forward.w2.weight.shape == (64, V.ffn_hidden_dim(args))
+    names = [n for n, _ in blk.orig_named_parameters()]
+    assert "feed_forward.w3.weight" in names and names[-1] == "ffn_norm.weight"
+    assert abs(blk.weight_init_std - 0.02 / 2.0) < 1e-12
+    with torch.device("meta"):
+        m = V.get_model("deepspeedllamav2_7b", vocab_size=64, seq_length=32, layers=1)
+    assert m._hidden_size == 4096 and m.layers[0].flat_param.numel() == 202_383_360
+    assert m.join_layers()[-1] is m.output_layer
+
+
+def test_profiler_table_format_and_fit():
+    """The latency-table entry written for MI355X follows
+    utils/runtime_estimator.py:388-414 and reads back the way
+    utils/optimizer_utils.py:59-125 reads it (profiled list per batch size,
+    linear fit beyond)."""
+    import json
+    import tempfile
+    from zorse_amd import profiler as P
+    assert P.clean_gpu_name("AMD Instinct MI355X") == "mi355x"
+    assert P.GPU_MEMORY["mi355x"] == 288.0 and P.GPU_TFLOPS["bfloat16"]["mi355x"] == 2516.6
+    slope, icpt = P.fit_line([3.0, 5.0, 7.0, 9.0])
+    assert abs(slope - 2.0) < 1e-12 and abs(icpt - 1.0) < 1e-12
+    entry = [P.fit_line([1.0, 2.1, 2.9]), P.fit_line([2.0, 4.2, 5.8]), [1.0, 2.1, 2.9],
+             [2.0, 4.2, 5.8]]
+    with tempfile.TemporaryDirectory() as d:
+        path = d + "/model_latencies.json"
+        P.update_latency_table(path, "deepspeedllama_7b", "mi355x", 4096, "bfloat16", entry)
+        P.update_latency_table(path, "deepspeedllama_7b", "mi355x", 512, "bfloat16", entry)
+        table = json.load(open(path))
+    rt = table["deepspeedllama_7b"]["mi355x"]["4096"]["bfloat16"]
+    assert isinstance(rt, list) and len(rt) == 4 and rt[2][1] == 2.1 and rt[3][2] == 5.8
+    (sf, i_f), (sb, ib) = rt[0], rt[1]
+    assert abs((sf * 5 + i_f) - (entry[0][0] * 5 + entry[0][1])) < 1e-12
+    assert set(table["deepspeedllama_7b"]["mi355x"]) == {"4096", "512"}

@@ -246,3 +246,52 @@ def test_stage_runner_optimizer_in_backwards(dev):
         assert_close(master, flat0, torch.float32, f"layer {i} master")
         assert torch.equal(layer.flat_param.detach().cpu(), master.cpu().to(dtype))
         assert layer.flat_param.grad is None
+
+
+# ------------------------------------------------------------- llama_v2 block --
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_llama_v2_block_vs_oracle(dev, dtype):
+    """torchtitan-style TransformerBlock (models/llama_v2.py:328-399):
+    interleaved complex RoPE, RMSNorm eps 1e-5, GQA 2:1, causal."""
+    from zorse_amd import llama_v2 as V
+    args = V.ModelArgs(dim=256, n_heads=2, n_kv_heads=1, n_layers=4, vocab_size=64,
+                       multiple_of=128, rope_theta=1e4)
+    blk = V.TransformerBlock(2, args, generator=torch.Generator().manual_seed(5),
+                             param_dtype=dtype).to(dev)
+    with torch.no_grad():
+        for k in ("ln1", "ln2"):
+            blk.param_view(k).copy_(1 + 0.1 * torch.randn(256, generator=torch.Generator().manual_seed(6)))
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(1, 200, 256, generator=g).to(dtype)
+    dout = torch.randn(1, 200, 256, generator=g).to(dtype)
+    xg = x.to(dev).requires_grad_(True)
+    out = blk(xg)
+    out.backward(dout.to(dev))
+    s = blk.spec
+    shape = O.LayerShape(hidden=s.hidden, heads=s.heads, kv_heads=s.kv_heads, head_dim=s.head_dim,
+                         ffn=s.ffn, eps=s.eps, theta=s.rope_theta)
+    p = _oracle_params(blk, dtype)
+    rout, rdx, rg = O.layer_fwd_bwd(x.double(), p, shape, dout.double(), rope="interleaved")
+    assert_close(out, rout, dtype, "out")
+    assert_close(xg.grad, rdx, dtype, "dx")
+    offs = s.offsets()
+    for k in O.PARAM_ORDER:
+        a, b = offs[k]
+        assert_close(blk.flat_param.grad[a:b].view(rg[k].shape), rg[k], dtype, "d" + k)
+
+
+def test_profiler_protocol_small(dev):
+    """The layer-profiler counterpart runs its protocol end to end on a small
+    layer: positive kernel times per batch size, a line fit, and the
+    optimizer latency for several shard counts."""
+    from zorse_amd import llama_simple as L
+    from zorse_amd import profiler as P
+    cfg = L.llama_config(hidden_size=256, num_attention_heads=2, intermediate_size=512)
+    layer = L.Block(cfg, 0).to(dev)
+    times = [P.get_compute_latency(layer, bs, 128, 256, torch.bfloat16, vocab_size=512,
+                                   num_iterations=3, delay=0.0) for bs in (1, 2)]
+    assert all(f > 0 and b > 0 for f, b in times)
+    assert P.get_optimizer_latency(layer, 1, num_iterations=3) > 0
+    assert P.get_optimizer_latency(layer, 4, num_iterations=3) > 0
+    assert P.gpu_name() == "mi355x"

@@ -146,46 +146,32 @@ class LlamaMLP(nn.Module):
 
 # -------------------------------------------------------------- the layer --
 
-class LlamaDecoderLayer(nn.Module):
-    """LlamaDecoderLayer (models/llama_simple.py:391-487) over one flat
-    parameter.  ``dtype`` is accepted for signature compatibility (the
-    reference uses it only to pick the attention class); parameters are
-    created in ``param_dtype``: fp32 (the nn.Linear default) for the
-    profiler's autocast protocol, or bf16 / fp16 for the pipeline's mixed
-    precision, where the optimizer keeps the fp32 master."""
+class FlatDecoderLayer(nn.Module):
+    """A decoder layer whose parameters live in ONE flat buffer laid out as
+    LayerSpec.offsets() (q, k, v, o, gate, up, down, ln1, ln2); the named
+    weights of the reference modules are views of it.  Subclasses create the
+    reference's submodule names."""
 
-    def __init__(self, config, layer_idx: int, dtype=torch.float32, *,
-                 sliding_window=None, device=None, param_dtype=torch.float32,
+    def __init__(self, spec: LayerSpec, *, device=None, param_dtype=torch.float32,
                  init_std: float | None = None, generator: torch.Generator | None = None):
         super().__init__()
-        self.spec = spec_from_config(config, sliding_window)
-        self.hidden_size = self.spec.hidden
-        self.layer_idx = layer_idx
-        self._offsets = self.spec.offsets()
-        self.flat_param = nn.Parameter(torch.empty(self.spec.numel, dtype=param_dtype,
-                                                   device=device))
-        self.self_attn = LlamaAttention(self, self.spec, layer_idx)
-        self.mlp = LlamaMLP(self, self.spec)
-        self.input_layernorm = FlatRMSNorm(self, "ln1", self.spec.hidden, self.spec.eps)
-        self.post_attention_layernorm = FlatRMSNorm(self, "ln2", self.spec.hidden,
-                                                    self.spec.eps)
+        self.spec = spec
+        self._offsets = spec.offsets()
+        self.flat_param = nn.Parameter(torch.empty(spec.numel, dtype=param_dtype, device=device))
         self._lowp_cache = None
-        self.reset_parameters(init_std, generator)
+        self._init_std, self._init_gen = init_std, generator
 
     # -- parameters -----------------------------------------------------------
     def param_view(self, name: str) -> torch.Tensor:
         a, b = self._offsets[name]
         return self.flat_param[a:b].view(self.spec.shapes()[name])
 
+    ORIG_NAMES: dict = {}
+
     def orig_named_parameters(self):
         """(reference parameter name, view) pairs in registration order."""
-        names = {"q": "self_attn.q_proj.weight", "k": "self_attn.k_proj.weight",
-                 "v": "self_attn.v_proj.weight", "o": "self_attn.o_proj.weight",
-                 "gate": "mlp.gate_proj.weight", "up": "mlp.up_proj.weight",
-                 "down": "mlp.down_proj.weight", "ln1": "input_layernorm.weight",
-                 "ln2": "post_attention_layernorm.weight"}
         for k in self._offsets:
-            yield names[k], self.param_view(k)
+            yield self.ORIG_NAMES.get(k, k), self.param_view(k)
 
     @torch.no_grad()
     def reset_parameters(self, std: float | None = None,
@@ -224,7 +210,45 @@ class LlamaDecoderLayer(nn.Module):
         self._lowp_cache = (key, w)
         return w
 
-    # -- forward --------------------------------------------------------------
+    def _run(self, x: torch.Tensor) -> torch.Tensor:
+        """The fused layer on x [B, S, h]; under autocast an fp32 input runs in
+        the autocast dtype (the profiler protocol)."""
+        cdt = x.dtype
+        if cdt == torch.float32 and torch.is_autocast_enabled("cuda"):
+            cdt = torch.get_autocast_dtype("cuda")
+            x = x.to(cdt)
+        return DecoderLayerFunction.apply(x, self.flat_param, self.spec,
+                                          self._compute_weights(cdt))
+
+
+class LlamaDecoderLayer(FlatDecoderLayer):
+    """LlamaDecoderLayer (models/llama_simple.py:391-487) over one flat
+    parameter.  ``dtype`` is accepted for signature compatibility (the
+    reference uses it only to pick the attention class); parameters are
+    created in ``param_dtype``: fp32 (the nn.Linear default) for the
+    profiler's autocast protocol, or bf16 / fp16 for the pipeline's mixed
+    precision, where the optimizer keeps the fp32 master."""
+
+    ORIG_NAMES = {"q": "self_attn.q_proj.weight", "k": "self_attn.k_proj.weight",
+                  "v": "self_attn.v_proj.weight", "o": "self_attn.o_proj.weight",
+                  "gate": "mlp.gate_proj.weight", "up": "mlp.up_proj.weight",
+                  "down": "mlp.down_proj.weight", "ln1": "input_layernorm.weight",
+                  "ln2": "post_attention_layernorm.weight"}
+
+    def __init__(self, config, layer_idx: int, dtype=torch.float32, *,
+                 sliding_window=None, device=None, param_dtype=torch.float32,
+                 init_std: float | None = None, generator: torch.Generator | None = None):
+        super().__init__(spec_from_config(config, sliding_window), device=device,
+                         param_dtype=param_dtype)
+        self.hidden_size = self.spec.hidden
+        self.layer_idx = layer_idx
+        self.self_attn = LlamaAttention(self, self.spec, layer_idx)
+        self.mlp = LlamaMLP(self, self.spec)
+        self.input_layernorm = FlatRMSNorm(self, "ln1", self.spec.hidden, self.spec.eps)
+        self.post_attention_layernorm = FlatRMSNorm(self, "ln2", self.spec.hidden,
+                                                    self.spec.eps)
+        self.reset_parameters(init_std, generator)
+
     def forward(self, hidden_states, attention_mask=None, position_ids=None,
                 past_key_value=None, output_attentions=False, use_cache=False,
                 cache_position=None, **kwargs):
@@ -239,14 +263,7 @@ class LlamaDecoderLayer(nn.Module):
             if pos.numel() != S or (pos.device.type == "cpu" and not torch.equal(
                     pos, torch.arange(S, dtype=pos.dtype))):
                 raise NotImplementedError("only position_ids = arange(S) are supported")
-        x = hidden_states
-        cdt = x.dtype
-        if cdt == torch.float32 and torch.is_autocast_enabled("cuda"):
-            cdt = torch.get_autocast_dtype("cuda")
-            x = x.to(cdt)
-        out = DecoderLayerFunction.apply(x, self.flat_param, self.spec,
-                                         self._compute_weights(cdt))
-        return (out,)
+        return (self._run(hidden_states),)
 
 
 class Block(nn.Module):
