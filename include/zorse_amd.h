@@ -177,6 +177,27 @@ int zk_adamw_step(float* param, const void* grad, int grad_dtype,
                   double beta2, double eps, double weight_decay, int64_t step,
                   zk_stream_t stream);
 
+/* ------------------------------------------------- LM head cross-entropy --
+ * Replaces the last stage's loss, F.cross_entropy(out.flatten(0, 1),
+ * target.flatten(0, 1)) (zorse_utils/pipeline_schedule_v2.py:181-184) over
+ * the logits of the output layer (models/llama_simple.py:559-561), computed
+ * one vocabulary chunk at a time so [tokens, vocab] logits never exist.
+ * logits: [rows, cols] chunk (row stride ld) holding vocabulary columns
+ * col0 .. col0 + cols - 1; labels: int64 [rows], negative = ignored.
+ * zk_ce_fwd_chunk folds the chunk into the running fp32 max / sum-of-exp per
+ * row (run_max starts at -inf, run_sum at 0) and stores the label's logit in
+ * target_logit when the label is inside the chunk; after the last chunk
+ * lse = run_max + log(run_sum) and loss_row = lse - target_logit.
+ * zk_ce_bwd_chunk overwrites the chunk with
+ * scale * (exp(logit - lse) - [column == label]) (0 for ignored rows). */
+int zk_ce_fwd_chunk(const void* logits, int64_t rows, int64_t cols, int64_t ld,
+                    const int64_t* labels, int64_t col0, float* run_max,
+                    float* run_sum, float* target_logit, int dtype,
+                    zk_stream_t stream);
+int zk_ce_bwd_chunk(void* logits, int64_t rows, int64_t cols, int64_t ld,
+                    const int64_t* labels, int64_t col0, const float* lse,
+                    float scale, int dtype, zk_stream_t stream);
+
 /* ------------------------------------------------------------- Utilities --
  * Dtype conversion of a contiguous buffer (the autocast weight cast and the
  * grad cast of utils/patch.py:115-119 when done outside the AdamW kernel).

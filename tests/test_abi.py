@@ -216,3 +216,11 @@ def test_profiler_table_format_and_fit():
     (sf, i_f), (sb, ib) = rt[0], rt[1]
     assert abs((sf * 5 + i_f) - (entry[0][0] * 5 + entry[0][1])) < 1e-12
     assert set(table["deepspeedllama_7b"]["mi355x"]) == {"4096", "512"}
+
+
+def test_ce_chunk_validation(lib):
+    p = ctypes.c_void_p(16)
+    assert lib.zk_ce_fwd_chunk(p, 4, 8, 4, p, 0, p, p, p, 2, None) == -1     # ld < cols
+    assert lib.zk_ce_fwd_chunk(p, 4, 8, 8, None, 0, p, p, p, 2, None) == -1  # null labels
+    assert lib.zk_ce_bwd_chunk(p, 4, 8, 8, p, 0, p, 1.0, 9, None) == -2      # bad dtype
+    assert lib.zk_ce_fwd_chunk(ctypes.c_void_p(18), 4, 8, 8, p, 0, p, p, p, 2, None) == -3

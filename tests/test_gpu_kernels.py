@@ -306,3 +306,33 @@ def test_cast(dev):
     assert torch.equal(y, x.to(torch.bfloat16))
     K.cast_(x, y, accumulate=True)
     assert torch.equal(y, (x.to(torch.bfloat16).float() + x).to(torch.bfloat16))
+
+
+# ------------------------------------------------------ LM head + cross-entropy --
+
+@pytest.mark.parametrize("dtype,V,chunk", [(torch.float32, 1000, 384), (torch.bfloat16, 4096, 1024),
+                                           (torch.float16, 3000, 8192), (torch.bfloat16, 1003, 256)])
+def test_lm_head_cross_entropy_chunked(dev, dtype, V, chunk):
+    """Chunked CE (the last stage's loss, zorse_utils/pipeline_schedule_v2.py:
+    181-184) vs fp64 F.cross_entropy on full logits, with ignored (-100)
+    labels, a ragged last chunk and several chunks."""
+    from zorse_amd.lm_head import lm_head_cross_entropy
+    g = torch.Generator().manual_seed(70)
+    T, h = 96, 128
+    x = torch.randn(T, h, generator=g).to(dtype)
+    w = (0.05 * torch.randn(V, h, generator=g)).to(dtype)
+    labels = torch.randint(0, V, (T,), generator=g)
+    labels[::7] = -100
+    xd = x.to(dev).requires_grad_(True)
+    wd = w.to(dev).requires_grad_(True)
+    loss = lm_head_cross_entropy(xd, wd, labels.to(dev), chunk=chunk)
+    loss.backward()
+    xr = x.double().requires_grad_(True)
+    wr = w.double().requires_grad_(True)
+    ref = torch.nn.functional.cross_entropy(xr @ wr.t(), labels, ignore_index=-100)
+    ref.backward()
+    assert abs(loss.item() - ref.item()) <= 1e-3 * max(1.0, abs(ref.item()))
+    if dtype == torch.float32:
+        assert abs(loss.item() - ref.item()) <= 1e-4 * abs(ref.item())
+    assert_close(xd.grad, xr.grad, dtype, "dx")
+    assert_close(wd.grad, wr.grad, dtype, "dW")

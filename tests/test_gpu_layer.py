@@ -134,8 +134,8 @@ def test_layer_fwd_bwd_vs_oracle(dev, name):
 
 def test_cfg1_head_and_cross_entropy_loss(dev):
     """BASELINE cfg1 end to end: layer + final RMSNorm + linear head + CE over
-    integer labels (vocab 1000), fp32; loss agreement 1e-3 (relative 1e-4 on
-    the fp32 path)."""
+    integer labels (vocab 1000), fp32, all on this build's kernels (chunked
+    vocabulary CE); loss agreement 1e-3 (relative 1e-4 on the fp32 path)."""
     from zorse_amd import llama_simple as L
     kw, _, dtype, (B, S) = CONFIGS["cfg1_fp32"]
     layer = _layer(kw, dev, seed=0)
@@ -145,9 +145,12 @@ def test_cfg1_head_and_cross_entropy_loss(dev):
     x = torch.randn(B, S, 256, generator=g)
     labels = torch.randint(0, 1000, (B, S), generator=g)
     xg = x.to(dev).requires_grad_(True)
-    hw = head.to(dev).requires_grad_(True)
-    logits = torch.nn.functional.linear(norm(layer(xg)[0]), hw)
-    loss = torch.nn.functional.cross_entropy(logits.flatten(0, 1), labels.to(dev).flatten())
+    lm_head = torch.nn.Linear(256, 1000, bias=False).to(dev)
+    with torch.no_grad():
+        lm_head.weight.copy_(head)
+    hw = lm_head.weight
+    from zorse_amd.lm_head import OutputLayerLoss
+    loss = OutputLayerLoss(norm, lm_head, chunk=384)(layer(xg)[0], labels.to(dev))
     loss.backward()
     p = _oracle_params(layer, torch.float32)
     xr = x.double().requires_grad_(True)

@@ -83,6 +83,9 @@ SIGNATURES = {
     "zk_adamw_step": (_int, [_ptr, _ptr, _int, _ptr, _ptr, _ptr, _int, _i64,
                              _f64, _f64, _f64, _f64, _f64, _i64, _ptr]),
     "zk_cast": (_int, [_ptr, _int, _ptr, _int, _i64, _int, _ptr]),
+    "zk_ce_fwd_chunk": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr, _int,
+                               _ptr]),
+    "zk_ce_bwd_chunk": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _f32, _int, _ptr]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,107 @@
+"""Output layer + cross-entropy of the last pipeline stage, chunked over the
+vocabulary.
+
+Replaces ``output_layer = Sequential(norm, lm_head)`` (models/llama_simple.py:
+559-561) followed by ``F.cross_entropy(out.flatten(0, 1), target.flatten(0,
+1))`` (zorse_utils/pipeline_schedule_v2.py:181-184).  The reference
+materialises [tokens, vocab] logits (and their fp32 softmax under autocast);
+here the vocabulary is processed in chunks of ``chunk`` columns:
+  forward   per chunk: logits_c = x W_c^T (hipBLASLt), then zk_ce_fwd_chunk
+            folds it into a running log-sum-exp and picks the label logit;
+            loss = mean over non-ignored tokens of (lse - label logit);
+  backward  per chunk: logits_c is recomputed, zk_ce_bwd_chunk turns it in
+            place into g (softmax - onehot) / n_valid, then dx += dlogits_c
+            W_c (fp32 accumulator) and dW_c = dlogits_c^T x.
+Only [tokens, chunk] logits and fp32 per-token vectors are ever live.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import kernels as K
+from ._abi import check, dtype_code, lib, ptr, stream_handle
+from .functional import rms_norm
+
+
+def _fwd_chunk(logits, labels, col0, run_max, run_sum, target):
+    check(lib().zk_ce_fwd_chunk(ptr(logits), logits.shape[0], logits.shape[1], logits.stride(0),
+                                ptr(labels), col0, ptr(run_max), ptr(run_sum), ptr(target),
+                                dtype_code(logits.dtype), stream_handle(logits.device)),
+          "zk_ce_fwd_chunk")
+
+
+def _bwd_chunk(logits, labels, col0, lse, scale):
+    check(lib().zk_ce_bwd_chunk(ptr(logits), logits.shape[0], logits.shape[1], logits.stride(0),
+                                ptr(labels), col0, ptr(lse), float(scale),
+                                dtype_code(logits.dtype), stream_handle(logits.device)),
+          "zk_ce_bwd_chunk")
+
+
+class LMHeadCrossEntropyFunction(torch.autograd.Function):
+    """loss = mean_t CE(x_t W^T, label_t) over tokens whose label >= 0."""
+
+    @staticmethod
+    def forward(ctx, x, weight, labels, chunk):
+        K._require_gpu(x, weight, labels)
+        if x.dim() != 2 or weight.dim() != 2 or x.shape[1] != weight.shape[1]:
+            raise ValueError("x must be [T, h] and weight [V, h]")
+        if labels.dtype != torch.int64 or labels.shape != (x.shape[0],):
+            raise ValueError("labels must be int64 [T]")
+        x = x.contiguous()
+        w = weight if weight.dtype == x.dtype else weight.to(x.dtype)
+        labels = labels.contiguous()
+        T, V = x.shape[0], w.shape[0]
+        run_max = torch.full((T,), float("-inf"), device=x.device, dtype=torch.float32)
+        run_sum = torch.zeros(T, device=x.device, dtype=torch.float32)
+        target = torch.zeros(T, device=x.device, dtype=torch.float32)
+        for c0 in range(0, V, chunk):
+            logits = torch.mm(x, w[c0:c0 + chunk].t())
+            _fwd_chunk(logits, labels, c0, run_max, run_sum, target)
+        lse = run_max + torch.log(run_sum)
+        valid = labels >= 0
+        n_valid = valid.sum()
+        loss = torch.where(valid, lse - target, torch.zeros_like(lse)).sum() / n_valid.clamp(min=1)
+        ctx.save_for_backward(x, w, labels, lse, n_valid)
+        ctx.chunk = chunk
+        ctx.weight_dtype = weight.dtype
+        return loss
+
+    @staticmethod
+    def backward(ctx, g):
+        x, w, labels, lse, n_valid = ctx.saved_tensors
+        chunk = ctx.chunk
+        T, V = x.shape[0], w.shape[0]
+        scale = (g / n_valid.clamp(min=1)).item()
+        dx = torch.zeros(x.shape, device=x.device, dtype=torch.float32)
+        dw = torch.empty_like(w)
+        for c0 in range(0, V, chunk):
+            wc = w[c0:c0 + chunk]
+            dlog = torch.mm(x, wc.t())
+            _bwd_chunk(dlog, labels, c0, lse, scale)
+            dx.add_(torch.mm(dlog, wc))
+            torch.mm(dlog.t(), x, out=dw[c0:c0 + chunk])
+        if dw.dtype != ctx.weight_dtype:
+            dw = dw.to(ctx.weight_dtype)
+        return dx.to(x.dtype), dw, None, None
+
+
+def lm_head_cross_entropy(x, weight, labels, chunk: int = 8192):
+    """Mean cross-entropy of logits x W^T against labels (negative = ignored);
+    x [..., h] is flattened over its leading dims."""
+    h = x.shape[-1]
+    return LMHeadCrossEntropyFunction.apply(x.reshape(-1, h), weight, labels.reshape(-1),
+                                            int(chunk))
+
+
+class OutputLayerLoss(torch.nn.Module):
+    """norm -> lm_head -> cross-entropy, the last stage's tail, without the
+    [tokens, vocab] logits: wraps an existing ``norm`` (RMSNorm module) and
+    ``lm_head`` (nn.Linear without bias)."""
+
+    def __init__(self, norm, lm_head, chunk: int = 8192):
+        super().__init__()
+        self.norm, self.lm_head, self.chunk = norm, lm_head, chunk
+
+    def forward(self, x, labels):
+        y = rms_norm(x, self.norm.weight, self.norm.variance_epsilon)
+        return lm_head_cross_entropy(y, self.lm_head.weight, labels, self.chunk)
