@@ -32,6 +32,25 @@ HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
 H100_FP16_LAYER_TOKS = 221_477   # data/model_latencies.json:7551, 7B layer seq 4096 fp16
 
 
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "hbm_traffic_cfg4.md")
+
+
+def recorded_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (calibrated against a 1 GiB copy), or
+    None when it has not been recorded."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
+                    return int(parts[2])
+    except OSError:
+        return None
+    return None
+
+
 def _events_time(fn, iters: int, warm: int = 2) -> float:
     """Average milliseconds per call of ``fn`` between HIP events recorded on
     torch's current stream (the stream every kernel here is launched on)."""
@@ -68,87 +87,107 @@ def build_stage(n_layers, dev, seed=3):
     return cfg, layers, g
 
 
+class KernelCases:
+    """The hand-written kernels at the stage's shapes, each as a zero-argument
+    launcher plus its algorithmic work per launch.  HBM-bound cases rotate
+    through enough buffers that the working set exceeds the 256 MB Infinity
+    Cache.  ``copy`` is a plain device copy of 1 GiB (read 1 GiB, write
+    1 GiB), the calibration for the FETCH_SIZE / WRITE_SIZE counters."""
+
+    NAMES = ("attn_fwd", "attn_bwd", "rmsnorm_fwd", "rmsnorm_bwd", "adamw", "copy")
+
+    def __init__(self, dev, spec, S):
+        self.dev, self.spec, self.S = dev, spec, S
+
+    def make(self, name):
+        from zorse_amd import flops
+        from zorse_amd import kernels as K
+        dev, spec, S = self.dev, self.spec, self.S
+        torch.manual_seed(0)
+        B, H, d, h = 1, spec.heads, spec.head_dim, spec.hidden
+        T = B * S
+        if name in ("attn_fwd", "attn_bwd"):
+            q = torch.randn(B, S, H, d, device=dev, dtype=torch.bfloat16)
+            k = torch.randn(B, S, H, d, device=dev, dtype=torch.bfloat16)
+            v = torch.randn(B, S, H, d, device=dev, dtype=torch.bfloat16)
+            o, lse = K.attn_fwd(q, k, v)
+            if name == "attn_fwd":
+                return (lambda: K.attn_fwd(q, k, v, out=o)), flops.attn_fwd_flops(B, H, d, S, S)
+            do = torch.randn_like(q)
+            dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+            return ((lambda: K.attn_bwd(q, k, v, o, do, lse, dq=dq, dk=dk, dv=dv)),
+                    flops.attn_bwd_flops(B, H, d, S, S))
+        if name in ("rmsnorm_fwd", "rmsnorm_bwd"):
+            nbuf = 8
+            xs = [torch.randn(T, h, device=dev, dtype=torch.bfloat16) for _ in range(nbuf)]
+            w = torch.ones(h, device=dev, dtype=torch.bfloat16)
+            ys = [torch.empty_like(x) for x in xs]
+            rs = [torch.empty(T, device=dev, dtype=torch.float32) for _ in xs]
+            for i in range(nbuf):
+                K.rmsnorm_fwd(xs[i], w, 1e-6, out=(ys[i], rs[i]))
+            it = [0]
+            if name == "rmsnorm_fwd":
+                def run():
+                    i = it[0] % nbuf
+                    it[0] += 1
+                    K.rmsnorm_fwd(xs[i], w, 1e-6, out=(ys[i], rs[i]))
+                return run, flops.rmsnorm_fwd_bytes(T, h)
+            ws = torch.empty(K.rmsnorm_bwd_workspace_elems(T, h), device=dev, dtype=torch.float32)
+            dw = torch.empty(h, device=dev, dtype=torch.bfloat16)
+
+            def run():
+                i = it[0] % nbuf
+                it[0] += 1
+                K.rmsnorm_bwd(xs[(i + 1) % nbuf], xs[i], w, rs[i], dw=dw,
+                              out=ys[(i + 2) % nbuf], workspace=ws)
+            return run, flops.rmsnorm_bwd_bytes(T, h)
+        if name == "adamw":
+            n = spec.numel
+            p = torch.randn(n, device=dev)
+            m = torch.zeros(n, device=dev)
+            vv = torch.zeros(n, device=dev)
+            gr = torch.randn(n, device=dev, dtype=torch.bfloat16)
+            lowp = torch.empty(n, device=dev, dtype=torch.bfloat16)
+            step = [0]
+
+            def run():
+                step[0] += 1
+                K.adamw_step(p, gr, m, vv, lr=1e-4, beta1=0.9, beta2=0.95, eps=1e-8,
+                             weight_decay=0.1, step=step[0], lowp_out=lowp)
+            return run, flops.adamw_bytes(n, 2, True)
+        if name == "copy":
+            src = torch.empty(1 << 28, device=dev, dtype=torch.float32).normal_()
+            dst = torch.empty_like(src)
+            return (lambda: dst.copy_(src)), 2 * src.numel() * 4
+        raise ValueError(f"unknown kernel case {name!r}; one of {self.NAMES}")
+
+
 def measure_kernels(dev, spec, S):
     """Live HIP-event timings of the hand-written kernels at the stage's
-    shapes.  HBM-bound kernels rotate through enough buffers that the working
-    set exceeds the 256 MB Infinity Cache."""
-    from zorse_amd import flops
-    from zorse_amd import kernels as K
-    torch.manual_seed(0)
-    B, H, d, h = 1, spec.heads, spec.head_dim, spec.hidden
-    q = torch.randn(B, S, H, d, device=dev, dtype=torch.bfloat16)
-    k = torch.randn(B, S, H, d, device=dev, dtype=torch.bfloat16)
-    v = torch.randn(B, S, H, d, device=dev, dtype=torch.bfloat16)
-    do = torch.randn(B, S, H, d, device=dev, dtype=torch.bfloat16)
-    o, lse = K.attn_fwd(q, k, v)
-    t_fwd = _events_time(lambda: K.attn_fwd(q, k, v, out=o), 20)
-    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    t_bwd = _events_time(lambda: K.attn_bwd(q, k, v, o, do, lse, dq=dq, dk=dk, dv=dv), 10)
-    f_fwd = flops.attn_fwd_flops(B, H, d, S, S, True, 0)
-    f_bwd = flops.attn_bwd_flops(B, H, d, S, S, True, 0)
-    del q, k, v, do, o, dq, dk, dv
-
-    T = B * S
-    nbuf = 8
-    xs = [torch.randn(T, h, device=dev, dtype=torch.bfloat16) for _ in range(nbuf)]
-    w = torch.ones(h, device=dev, dtype=torch.bfloat16)
-    ys = [torch.empty_like(x) for x in xs]
-    rs = [torch.empty(T, device=dev, dtype=torch.float32) for _ in xs]
-    it = [0]
-
-    def rms_fwd():
-        i = it[0] % nbuf
-        it[0] += 1
-        K.rmsnorm_fwd(xs[i], w, 1e-6, out=(ys[i], rs[i]))
-    t_rms = _events_time(rms_fwd, 4 * nbuf, warm=nbuf)
-    dxs = ys
-    ws = torch.empty(K.rmsnorm_bwd_workspace_elems(T, h), device=dev, dtype=torch.float32)
-    dw = torch.empty(h, device=dev, dtype=torch.bfloat16)
-
-    def rms_bwd():
-        i = it[0] % nbuf
-        it[0] += 1
-        j = (i + 1) % nbuf
-        K.rmsnorm_bwd(xs[j], xs[i], w, rs[i], dw=dw, out=dxs[(i + 2) % nbuf], workspace=ws)
-    t_rms_b = _events_time(rms_bwd, 4 * nbuf, warm=nbuf)
-    del xs, ys, rs, ws
-
-    n = spec.numel
-    p = torch.randn(n, device=dev)
-    m = torch.zeros(n, device=dev)
-    vv = torch.zeros(n, device=dev)
-    gr = torch.randn(n, device=dev, dtype=torch.bfloat16)
-    lowp = torch.empty(n, device=dev, dtype=torch.bfloat16)
-    step = [0]
-
-    def adam():
-        step[0] += 1
-        K.adamw_step(p, gr, m, vv, lr=1e-4, beta1=0.9, beta2=0.95, eps=1e-8,
-                     weight_decay=0.1, step=step[0], lowp_out=lowp)
-    t_adam = _events_time(adam, 5)
-    del p, m, vv, gr, lowp
-
-    def rf(name, bound, achieved, peak, unit, ms, work):
-        return {"kernel": name, "bound": bound, "achieved": round(achieved, 1),
-                "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
-                "avg_ms": round(ms, 4), "work_per_launch": work}
-
-    out = {
-        "attn_fwd": rf("attn_fwd_kernel<bf16,128>", "mfma", f_fwd / t_fwd / 1e9,
-                       MFMA_BF16_PEAK_TFLOPS, "TFLOP/s", t_fwd, f_fwd),
-        "attn_bwd": rf("zk_attn_bwd (prep + attn_bwd_kernel<bf16,128> + dq store)", "mfma",
-                       f_bwd / t_bwd / 1e9, MFMA_BF16_PEAK_TFLOPS, "TFLOP/s", t_bwd, f_bwd),
-        "rmsnorm_fwd": rf("rmsnorm_fwd_vec<bf16,bf16,128>", "hbm",
-                          flops.rmsnorm_fwd_bytes(T, h) / t_rms / 1e6, HBM_PEAK_GBS, "GB/s",
-                          t_rms, flops.rmsnorm_fwd_bytes(T, h)),
-        "rmsnorm_bwd": rf("rmsnorm_bwd_vec<bf16,bf16,128> + dw reduce", "hbm",
-                          flops.rmsnorm_bwd_bytes(T, h) / t_rms_b / 1e6, HBM_PEAK_GBS, "GB/s",
-                          t_rms_b, flops.rmsnorm_bwd_bytes(T, h)),
-        "adamw": rf("adamw_vec4<bf16,bf16,true>", "hbm",
-                    flops.adamw_bytes(n, 2, True) / t_adam / 1e6, HBM_PEAK_GBS, "GB/s",
-                    t_adam, flops.adamw_bytes(n, 2, True)),
+    shapes (see KernelCases)."""
+    cases = KernelCases(dev, spec, S)
+    rows = {}
+    spec_of = {
+        "attn_fwd": ("attn_fwd_kernel<bf16,128>", "mfma", 20),
+        "attn_bwd": ("zk_attn_bwd (prep + attn_bwd_dkdv + attn_bwd_dq)", "mfma", 10),
+        "rmsnorm_fwd": ("rmsnorm_fwd_vec<bf16,bf16,256,2>", "hbm", 32),
+        "rmsnorm_bwd": ("rmsnorm_bwd_vec<bf16,bf16,256,4,2> + dw reduce", "hbm", 32),
+        "adamw": ("adamw_vec8<bf16,bf16,true>", "hbm", 10),
+        "copy": ("device copy 1 GiB (HBM reference)", "hbm", 5),
     }
-    return out
+    for name, (kname, bound, iters) in spec_of.items():
+        run, work = cases.make(name)
+        ms = _events_time(run, iters, warm=3)
+        if bound == "mfma":
+            ach, peak, unit = work / ms / 1e9, MFMA_BF16_PEAK_TFLOPS, "TFLOP/s"
+        else:
+            ach, peak, unit = work / ms / 1e6, HBM_PEAK_GBS, "GB/s"
+        rows[name] = {"kernel": kname, "bound": bound, "achieved": round(ach, 1), "peak": peak,
+                      "unit": unit, "frac": round(ach / peak, 4), "avg_ms": round(ms, 4),
+                      "work_per_launch": work}
+        del run
+        torch.cuda.empty_cache()
+    return rows
 
 
 def cpu_baseline(spec, S, seed=3):
@@ -184,6 +223,8 @@ def main():
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--seq", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel", choices=KernelCases.NAMES,
+                    help="launch only this kernel case --steps times (for rocprofv3 --pmc)")
     ap.add_argument("--default-gemm", action="store_true",
                     help="use hipBLASLt's default solution heuristic instead of the recorded table")
     args = ap.parse_args()
@@ -202,6 +243,14 @@ def main():
     tuned = use_tuned_gemms(not args.default_gemm)
 
     S, B = args.seq, 1
+    if args.kernel:
+        from zorse_amd.layer import LayerSpec
+        spec = LayerSpec(hidden=4096, heads=32, kv_heads=32, head_dim=128, ffn=11008)
+        run, work = KernelCases(dev, spec, S).make(args.kernel)
+        ms = _events_time(run, args.steps, warm=args.warmup)
+        print(json.dumps({"kernel": args.kernel, "launches": args.steps, "avg_ms": round(ms, 4),
+                          "work_per_launch": work}), flush=True)
+        return
     cfg, layers, g = build_stage(args.layers, dev)
     spec = layers[0].spec
     runner = StageRunner(layers, lr=1e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
@@ -230,7 +279,9 @@ def main():
     kern = measure_kernels(dev, spec, S)
     print("kernel timings done", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline(spec, S)
-    a = kern["attn_fwd"]
+    # the dominant hand-written kernel of the step (by time): the AdamW pass
+    a = kern["adamw"]
+    af, ab = kern["attn_fwd"], kern["attn_bwd"]
     line = {
         "metric": "decoder-layer fwd+bwd tokens/s at 1 GPU; attention TFLOP/s vs MFMA peak",
         "value": round(layer_toks, 1),
@@ -256,9 +307,17 @@ def main():
                        if tuned else " (default heuristic)"),
                    "stage_tokens_per_s": round(B * S / (ms_step / 1e3), 1),
                    "layer_fwd_bwd_tflops": round(layer_tflops, 1)},
-        "roofline": {"bound": "mfma", "achieved": a["achieved"], "peak": a["peak"],
-                     "unit": "TFLOP/s", "frac": a["frac"], "traffic": None,
-                     "kernel": a["kernel"], "avg_ms": a["avg_ms"]},
+        "roofline": {"bound": a["bound"], "achieved": a["achieved"], "peak": a["peak"],
+                     "unit": a["unit"], "frac": a["frac"],
+                     "traffic": recorded_traffic("adamw_vec8<bf16,bf16,true>"),
+                     "kernel": a["kernel"], "avg_ms": a["avg_ms"],
+                     "algorithmic_bytes": a["work_per_launch"]},
+        "attention_roofline": {
+            "fwd": {"kernel": af["kernel"], "achieved": af["achieved"], "peak": af["peak"],
+                    "unit": "TFLOP/s", "frac": af["frac"], "avg_ms": af["avg_ms"],
+                    "traffic": recorded_traffic("attn_fwd_kernel<bf16,128>")},
+            "bwd": {"kernel": ab["kernel"], "achieved": ab["achieved"], "peak": ab["peak"],
+                    "unit": "TFLOP/s", "frac": ab["frac"], "avg_ms": ab["avg_ms"]}},
         "kernels": kern,
         "cpu_baseline": cpu,
     }

@@ -132,26 +132,41 @@ template <typename G, typename L, bool kCopy>
 __global__ __launch_bounds__(256) void adamw_vec8(
     float* __restrict__ p, const G* __restrict__ g, float* __restrict__ m,
     float* __restrict__ v, L* __restrict__ lowp, int64_t n8, AdamScalars s) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-       q < n8; q += stride) {
+  // R groups of 8 elements per thread, R * 256 consecutive groups per
+  // workgroup; all R groups' loads are issued before any arithmetic.
+  constexpr int R = 2;
+  const int64_t q0 = static_cast<int64_t>(blockIdx.x) * (256 * R) + threadIdx.x;
+  float4 pa[R][2], ma[R][2], va[R][2];
+  float gv[R][8];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t q = q0 + 256 * r;
+    if (q < n8) {
+      const int64_t i = q * 8;
+      pa[r][0] = *reinterpret_cast<const float4*>(p + i);
+      pa[r][1] = *reinterpret_cast<const float4*>(p + i + 4);
+      ma[r][0] = *reinterpret_cast<const float4*>(m + i);
+      ma[r][1] = *reinterpret_cast<const float4*>(m + i + 4);
+      va[r][0] = *reinterpret_cast<const float4*>(v + i);
+      va[r][1] = *reinterpret_cast<const float4*>(v + i + 4);
+      load_grad8<G>(g, i, gv[r]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t q = q0 + 256 * r;
+    if (q >= n8) break;
     const int64_t i = q * 8;
-    float4 p0 = *reinterpret_cast<const float4*>(p + i);
-    float4 p1 = *reinterpret_cast<const float4*>(p + i + 4);
-    float4 m0 = *reinterpret_cast<const float4*>(m + i);
-    float4 m1 = *reinterpret_cast<const float4*>(m + i + 4);
-    float4 v0 = *reinterpret_cast<const float4*>(v + i);
-    float4 v1 = *reinterpret_cast<const float4*>(v + i + 4);
-    float gv[8];
-    load_grad8<G>(g, i, gv);
-    adam_one(p0.x, gv[0], m0.x, v0.x, s);
-    adam_one(p0.y, gv[1], m0.y, v0.y, s);
-    adam_one(p0.z, gv[2], m0.z, v0.z, s);
-    adam_one(p0.w, gv[3], m0.w, v0.w, s);
-    adam_one(p1.x, gv[4], m1.x, v1.x, s);
-    adam_one(p1.y, gv[5], m1.y, v1.y, s);
-    adam_one(p1.z, gv[6], m1.z, v1.z, s);
-    adam_one(p1.w, gv[7], m1.w, v1.w, s);
+    float4 &p0 = pa[r][0], &p1 = pa[r][1], &m0 = ma[r][0], &m1 = ma[r][1];
+    float4 &v0 = va[r][0], &v1 = va[r][1];
+    adam_one(p0.x, gv[r][0], m0.x, v0.x, s);
+    adam_one(p0.y, gv[r][1], m0.y, v0.y, s);
+    adam_one(p0.z, gv[r][2], m0.z, v0.z, s);
+    adam_one(p0.w, gv[r][3], m0.w, v0.w, s);
+    adam_one(p1.x, gv[r][4], m1.x, v1.x, s);
+    adam_one(p1.y, gv[r][5], m1.y, v1.y, s);
+    adam_one(p1.z, gv[r][6], m1.z, v1.z, s);
+    adam_one(p1.w, gv[r][7], m1.w, v1.w, s);
     *reinterpret_cast<float4*>(p + i) = p0;
     *reinterpret_cast<float4*>(p + i + 4) = p1;
     *reinterpret_cast<float4*>(m + i) = m0;
@@ -161,6 +176,9 @@ __global__ __launch_bounds__(256) void adamw_vec8(
     if (kCopy) store8<L>(lowp + i, p0, p1);
   }
 }
+
+// groups of 8 elements one workgroup of adamw_vec8 covers
+static constexpr int64_t kAdamGroupsPerBlock = 512;
 
 // Any alignment / tail: one element per thread, dtypes by runtime code.
 __global__ __launch_bounds__(256) void adamw_scalar(
@@ -241,8 +259,11 @@ extern "C" int zk_adamw_step(float* param, const void* grad, int grad_dtype,
   const int64_t n8 = vec ? n / 8 : 0;
   const int max_grid = device_cus() * 16;
   if (n8 > 0) {
-    int64_t want = (n8 + 255) / 256;
-    const int grid = static_cast<int>(want < max_grid ? want : max_grid);
+    // every group covered by exactly one thread (no grid-stride loop)
+    const int64_t want = (n8 + kAdamGroupsPerBlock - 1) / kAdamGroupsPerBlock;
+    ZK_REQUIRE(want < 0x7fffffff, ZK_EINVAL, "zk_adamw_step: shard too large (%lld)",
+               (long long)n);
+    const int grid = static_cast<int>(want);
     if (grad_dtype == ZK_F32)
       launch_vec<float>(param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_dtype, n8, s, grid, st);
     else if (grad_dtype == ZK_BF16)

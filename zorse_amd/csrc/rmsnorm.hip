@@ -17,7 +17,7 @@
 namespace zk {
 
 static constexpr int kBwdParts = 512;  // workgroups (= dw partial rows) of the backward
-static constexpr int kBwdRows = 4;     // rows a backward workgroup keeps in flight
+static constexpr int kBwdRows = 2;     // rows a backward workgroup keeps in flight
 static constexpr int kMaxCh = 4;       // chunks of 8 per thread: hidden <= 256 * 4 * 8
 
 template <int NT>
@@ -305,12 +305,22 @@ static void launch_fwd_vec(const void* x, const void* res, void* hout,
                            int64_t hidden, float eps, hipStream_t s) {
   int nt, ch;
   pick_shape(hidden, nt, ch);
+  // the forward keeps one row per workgroup: prefer 128 threads x up to 4
+  // chunks (more bytes in flight per thread, more workgroups per CU)
+  const int64_t nchunk = hidden / 8;
+  if (nt == 256 && nchunk <= 128 * kMaxCh) {
+    nt = 128;
+    ch = static_cast<int>((nchunk + 127) / 128);
+  }
 #define ZK_LAUNCH(NT, CH)                                                          \
   hipLaunchKernelGGL((rmsnorm_fwd_vec<T, W, NT, CH>), dim3(rows), dim3(NT), 0, s,  \
                      (const T*)x, (const T*)res, (T*)hout, (const W*)w, (T*)y, rstd, \
                      hidden, eps)
   if (nt == 64) ZK_LAUNCH(64, 1);
-  else if (nt == 128) ZK_LAUNCH(128, 1);
+  else if (nt == 128 && ch == 1) ZK_LAUNCH(128, 1);
+  else if (nt == 128 && ch == 2) ZK_LAUNCH(128, 2);
+  else if (nt == 128 && ch == 3) ZK_LAUNCH(128, 3);
+  else if (nt == 128) ZK_LAUNCH(128, 4);
   else if (ch == 1) ZK_LAUNCH(256, 1);
   else if (ch == 2) ZK_LAUNCH(256, 2);
   else if (ch == 3) ZK_LAUNCH(256, 3);
