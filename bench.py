@@ -170,8 +170,8 @@ def measure_kernels(dev, spec, S):
     spec_of = {
         "attn_fwd": ("attn_fwd_kernel<bf16,128>", "mfma", 20),
         "attn_bwd": ("zk_attn_bwd (prep + attn_bwd_dkdv + attn_bwd_dq)", "mfma", 10),
-        "rmsnorm_fwd": ("rmsnorm_fwd_vec<bf16,bf16,256,2>", "hbm", 32),
-        "rmsnorm_bwd": ("rmsnorm_bwd_vec<bf16,bf16,256,4,2> + dw reduce", "hbm", 32),
+        "rmsnorm_fwd": ("rmsnorm_fwd_vec<bf16,bf16,128,4>", "hbm", 32),
+        "rmsnorm_bwd": ("rmsnorm_bwd_vec<bf16,bf16,256,2,2> + dw reduce", "hbm", 32),
         "adamw": ("adamw_vec8<bf16,bf16,true>", "hbm", 10),
         "copy": ("device copy 1 GiB (HBM reference)", "hbm", 5),
     }
