@@ -132,25 +132,72 @@ __device__ __forceinline__ typename Mfma<T>::vec8 lds_tr_operand(const T* tile, 
 typedef __attribute__((address_space(1))) void gmem_void;
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <typename T, int D, int ROWS>
+template <typename T, int D, int ROWS, int NT = 256>
 __device__ __forceinline__ void tile_load_async(T* tile, const T* gbase, int64_t ld,
                                                 int64_t g0, int64_t nrows) {
   constexpr int CH = ROWS * D / 8;
-  static_assert(CH % 256 == 0, "tile must be a multiple of 256 chunks");
+  static_assert(CH % NT == 0, "tile must be a multiple of NT chunks");
   const int tid = threadIdx.x;
   const int wave_chunk0 = tid & ~63;
 #pragma unroll
-  for (int i = 0; i < CH / 256; ++i) {
-    const int p = i * 256 + tid;
+  for (int i = 0; i < CH / NT; ++i) {
+    const int p = i * NT + tid;
     const int row = p / (D / 8);
     const int c = (p % (D / 8)) ^ tile_sw<D>(row);
     int64_t gr = g0 + row;
     if (gr > nrows - 1) gr = nrows - 1;
     const T* src = gbase + gr * ld + c * 8;
-    T* dst = tile + (i * 256 + wave_chunk0) * 8;
+    T* dst = tile + (i * NT + wave_chunk0) * 8;
     __builtin_amdgcn_global_load_lds((gmem_void*)src, (lds_void*)dst, 16, 0, 0);
   }
 }
+
+// The same tile load with the per-lane address work done once.  For a tile
+// of ROWS x D elements each of the NT threads moves NI = ROWS * D / (8 NT)
+// chunks; chunk i of thread t lands in row RSTEP * i + t / (D / 8) at chunk
+// position (t % (D / 8)) ^ sw(row), and since RSTEP is a multiple of 16 the
+// swizzle (a function of row % 16) is the same for every i.  The per-lane
+// byte offset inside the tile is therefore one 32-bit value, and each
+// instruction's global address is a wave-uniform base (scalar registers)
+// plus that offset.  Tiles that run past `nrows` take the clamped path.
+template <typename T, int D, int ROWS, int NT = 256>
+struct TileLoader {
+  static constexpr int NI = ROWS * D / 8 / NT;
+  static constexpr int RSTEP = NT / (D / 8);
+  static_assert(NI >= 1 && RSTEP % 16 == 0, "unsupported tile shape");
+  uint32_t lane_off;  // bytes from the tile's first row
+
+  __device__ __forceinline__ void init(int64_t ld) {
+    const int tid = threadIdx.x;
+    const int row = tid / (D / 8);
+    const int c = (tid % (D / 8)) ^ tile_sw<D>(row);
+    lane_off = static_cast<uint32_t>(row * ld * static_cast<int64_t>(sizeof(T)) + c * 16);
+  }
+
+  // Rows g0 .. g0 + ROWS - 1 must all lie below the tensor's row count.
+  __device__ __forceinline__ void issue_full(T* tile, const T* gbase, int64_t ld,
+                                             int64_t g0) const {
+    const int wave_chunk0 = static_cast<int>(threadIdx.x) & ~63;
+    const char* sb = reinterpret_cast<const char*>(gbase + g0 * ld);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const char* src =
+          sb + static_cast<int64_t>(i) * RSTEP * ld * static_cast<int64_t>(sizeof(T)) + lane_off;
+      T* dst = tile + (i * NT + wave_chunk0) * 8;
+      __builtin_amdgcn_global_load_lds((gmem_void*)src, (lds_void*)dst, 16, 0, 0);
+    }
+  }
+
+  // `full` (wave-uniform) says that the tile lies below `nrows`; otherwise
+  // rows past the end are clamped.
+  __device__ __forceinline__ void issue(T* tile, const T* gbase, int64_t ld, int64_t g0,
+                                        int64_t nrows, bool full) const {
+    if (full)
+      issue_full(tile, gbase, ld, g0);
+    else
+      tile_load_async<T, D, ROWS, NT>(tile, gbase, ld, g0, nrows);
+  }
+};
 
 // Number of vector-memory instructions tile_load_async issues per wave.
 template <int D, int ROWS>

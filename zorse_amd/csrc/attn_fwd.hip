@@ -47,7 +47,8 @@ __device__ __forceinline__ float fast_exp2(float x) {
 // log2-domain growth of the running maximum tolerated before rescaling
 static constexpr float kRescaleThreshold = 8.0f;
 
-template <typename T, int D>
+// kFull: Skv is a multiple of the key tile, so no tile runs past the end.
+template <typename T, int D, bool kFull>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
   typedef FwdCfg<T, D> C;
@@ -90,10 +91,12 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
   const int64_t t_hi = kv_hi > kv_lo ? (kv_hi + BN - 1) / BN : t_lo;
 
   // K / V tiles double-buffered in LDS, loaded asynchronously one tile ahead
-  constexpr int NL = 2 * tile_load_insts<D, BN>();
+  TileLoader<T, D, BN> kload, vload;
+  kload.init(a.k_ss);
+  vload.init(a.v_ss);
   auto issue = [&](int64_t k0, int st) {
-    tile_load_async<T, D, BN>(Ks[st], Kp, a.k_ss, k0, a.Skv);
-    tile_load_async<T, D, BN>(Vs[st], Vp, a.v_ss, k0, a.Skv);
+    kload.issue(Ks[st], Kp, a.k_ss, k0, a.Skv, kFull);
+    vload.issue(Vs[st], Vp, a.v_ss, k0, a.Skv, kFull);
   };
 
   f32x16 o[D / 32];
@@ -101,22 +104,31 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
   for (int nt = 0; nt < D / 32; ++nt) o[nt] = f32x16{};
   float m_ref = -INFINITY, l_i = 0.f;
   const float c2 = a.scale_log2;
-  const int iq = static_cast<int>(my_q), Sq32 = static_cast<int>(a.Sq),
-            Skv32 = static_cast<int>(a.Skv), W32 = static_cast<int>(a.window);
+  // Visible keys of this lane's query form one range [vis_lo, vis_lo + vis_span]
+  // (causal: up to the query; window: the W keys ending at the query; always
+  // below Skv), so the element mask is one unsigned compare per score.
+  int vis_lo, vis_span;
+  {
+    const int iq = static_cast<int>(my_q);
+    int hi = static_cast<int>(a.Skv) - 1;
+    if (a.causal && iq < hi) hi = iq;
+    const int lo = a.window > 0 ? iq - static_cast<int>(a.window) + 1 : 0;
+    vis_lo = lo > 0 ? lo : 0;
+    vis_span = hi - vis_lo;
+    if (vis_span < 0 || my_q >= a.Sq) {  // nothing visible
+      vis_lo = 0x40000000;
+      vis_span = 0;
+    }
+  }
 
   // One pipeline step on LDS stage ST (a compile-time constant, so every LDS
   // address is a per-lane base plus an immediate offset).
   auto step = [&](auto stage_tag, int64_t t) {
     constexpr int st = decltype(stage_tag)::value;
     const int64_t k0 = t * BN;
-    __syncthreads();  // every wave is done with the other stage
-    if (t + 1 < t_hi) {
-      issue(k0 + BN, st ^ 1);
-      wait_vmcnt<NL>();  // this wave's loads of tile t have landed
-    } else {
-      wait_vmcnt<0>();
-    }
-    __syncthreads();  // ... and every other wave's
+    wait_vmcnt<0>();  // this wave's loads of tile t have landed
+    __syncthreads();  // ... and every other wave's; all are done with the other stage
+    if (t + 1 < t_hi) issue(k0 + BN, st ^ 1);
     const T* Kt = Ks[st];
     const T* Vt = Vs[st];
 
@@ -150,12 +162,14 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
         }
       }
       if (kMask) {
+        const int kb = static_cast<int>(k0) + 4 * g - vis_lo;
 #pragma unroll
         for (int tt = 0; tt < BN / 32; ++tt)
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
-            const int key = static_cast<int>(k0) + 32 * tt + 8 * (j >> 2) + 4 * g + (j & 3);
-            if (!visible32(iq, key, Sq32, Skv32, a.causal, W32)) s[tt][j] = -INFINITY;
+            const int rel = kb + 32 * tt + 8 * (j >> 2) + (j & 3);
+            s[tt][j] = static_cast<unsigned>(rel) <= static_cast<unsigned>(vis_span) ? s[tt][j]
+                                                                                    : -INFINITY;
           }
       }
       float mloc = -INFINITY;
@@ -312,6 +326,11 @@ int check_attn_desc(const zk_attn_desc* d, const char* who, bool bwd) {
         ZK_REQUIRE(s % 8 == 0, ZK_EALIGN,
                    "%s: grad strides must be multiples of 8 elements", who);
     }
+    // the tile loaders keep a 32-row span of one tensor in a 32-bit byte offset
+    const int64_t rs[] = {d->q_ss, d->k_ss, d->v_ss, d->o_ss};
+    for (int64_t s : rs)
+      ZK_REQUIRE(s >= 0 && s < (int64_t(1) << 26), ZK_EUNSUPPORTED,
+                 "%s: row stride %lld out of range", who, (long long)s);
   }
   ZK_REQUIRE(d->B * d->Hq * ((d->Sq + 127) / 128) < 0x7fffffffLL, ZK_EINVAL,
              "%s: grid too large", who);
@@ -358,7 +377,13 @@ extern "C" int zk_attn_fwd(const zk_attn_desc* desc, const void* q,
              ZK_EALIGN, "zk_attn_fwd: q/k/v/o must be 16-byte aligned");
   const int64_t n_qt = (desc->Sq + 127) / 128;
   const dim3 grid(static_cast<unsigned>(n_qt * desc->B * desc->Hq));
-#define ZK_FWD(T, D) hipLaunchKernelGGL((attn_fwd_kernel<T, D>), grid, dim3(256), 0, s, a, n_qt)
+#define ZK_FWD(T, D)                                                                    \
+  do {                                                                                  \
+    if (desc->Skv % FwdCfg<T, D>::BN == 0)                                              \
+      hipLaunchKernelGGL((attn_fwd_kernel<T, D, true>), grid, dim3(256), 0, s, a, n_qt);  \
+    else                                                                                \
+      hipLaunchKernelGGL((attn_fwd_kernel<T, D, false>), grid, dim3(256), 0, s, a, n_qt); \
+  } while (0)
   if (desc->dtype == ZK_BF16) {
     if (desc->d == 128) ZK_FWD(bf16, 128); else ZK_FWD(bf16, 64);
   } else {
