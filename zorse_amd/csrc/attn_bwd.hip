@@ -72,7 +72,8 @@ struct DkdvCfg {
   static constexpr int MB = MQ / 32;          // 32-row MFMA blocks per query block
 };
 
-template <typename T, int D>
+// kFull: Sq is a multiple of the query block, so no block runs past the end.
+template <typename T, int D, bool kFull>
 __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
   typedef DkdvCfg<D> C;
   typedef Mfma<T> M;
@@ -97,8 +98,21 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
   const int64_t kw0 = k0 + 32 * wave;
   const int64_t my_key = kw0 + l32;
   const float c2 = a.scale_log2;
-  const int ik = static_cast<int>(my_key), Sq32 = static_cast<int>(a.Sq),
-            Skv32 = static_cast<int>(a.Skv), W32 = static_cast<int>(a.window);
+  // Queries that see this lane's key form one range [vis_lo, vis_lo + vis_span]
+  // (causal: from the key on; window: the W queries starting at the key;
+  // below Sq), so the element mask is one unsigned compare per score.
+  int vis_lo, vis_span;
+  {
+    const int ik = static_cast<int>(my_key);
+    int hi = static_cast<int>(a.Sq) - 1;
+    if (a.window > 0 && ik + static_cast<int>(a.window) - 1 < hi) hi = ik + static_cast<int>(a.window) - 1;
+    vis_lo = a.causal ? ik : 0;
+    vis_span = hi - vis_lo;
+    if (vis_span < 0 || my_key >= a.Skv) {
+      vis_lo = 0x40000000;
+      vis_span = 0;
+    }
+  }
 
   const T* Kp = static_cast<const T*>(a.k) + b * a.k_sb + hk * a.k_sh;
   const T* Vp = static_cast<const T*>(a.v) + b * a.v_sb + hk * a.v_sh;
@@ -132,14 +146,16 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
   const int64_t nqb = qb_hi - qb_lo;
   const int64_t n_iter = nqb * n_rep;
 
-  constexpr int NL = 2 * tile_load_insts<D, MQ>() + 2;
+  TileLoader<T, D, MQ> qload, dload;
+  qload.init(a.q_ss);
+  dload.init(a.o_ss);
   auto issue = [&](int64_t it, int st) {
     const int64_t hq = hk * n_rep + it / nqb;
     const int64_t qb0 = (qb_lo + it % nqb) * MQ;
     const T* Qp = static_cast<const T*>(a.q) + b * a.q_sb + hq * a.q_sh;
     const T* Dp = static_cast<const T*>(a.dout) + b * a.o_sb + hq * a.o_sh;
-    tile_load_async<T, D, MQ>(Qs[st], Qp, a.q_ss, qb0, a.Sq);
-    tile_load_async<T, D, MQ>(dOs[st], Dp, a.o_ss, qb0, a.Sq);
+    qload.issue(Qs[st], Qp, a.q_ss, qb0, a.Sq, kFull);
+    dload.issue(dOs[st], Dp, a.o_ss, qb0, a.Sq, kFull);
     int64_t qi = qb0 + lane;
     if (qi > a.Sq - 1) qi = a.Sq - 1;
     const int64_t ri = (b * a.Hq + hq) * a.Sq + qi;
@@ -151,14 +167,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
   auto step = [&](auto stage_tag, int64_t it) {
     constexpr int st = decltype(stage_tag)::value;
     const int64_t qb0 = (qb_lo + it % nqb) * MQ;
-    __syncthreads();  // every wave is done with the other stage
-    if (it + 1 < n_iter) {
-      issue(it + 1, st ^ 1);
-      wait_vmcnt<NL>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    __syncthreads();
+    wait_vmcnt<0>();  // this wave's loads of block it have landed
+    __syncthreads();  // ... and every wave's; all are done with the other stage
+    if (it + 1 < n_iter) issue(it + 1, st ^ 1);
 
     // wave-uniform classification of this (query block, 32 keys) tile
     bool skip = false, need_mask = kw0 + 31 >= a.Skv || qb0 + MQ > a.Sq;
@@ -205,7 +216,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
         for (int e = 0; e < 4; ++e) {
           const int j = 4 * a4 + e;
           float p = __builtin_amdgcn_exp2f(fmaf(sv[j], c2, -lv[e]));
-          if (kMask && !visible32(qb32 + r0 + e, ik, Sq32, Skv32, a.causal, W32)) p = 0.f;
+          if (kMask && static_cast<unsigned>(qb32 + r0 + e - vis_lo) > static_cast<unsigned>(vis_span))
+            p = 0.f;
           pb[j >> 3][j & 7] = static_cast<T>(p);
           sb[j >> 3][j & 7] = static_cast<T>(p * (dpv[j] - dl[e]));
         }
@@ -307,7 +319,8 @@ struct DqCfg {
   static constexpr int BN = 64;               // keys per tile
 };
 
-template <typename T, int D>
+// kFull: Skv is a multiple of the key tile, so no tile runs past the end.
+template <typename T, int D, bool kFull>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) {
   typedef DqCfg<D> C;
   typedef Mfma<T> M;
@@ -328,8 +341,20 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) 
   const int64_t qw0 = q0 + 32 * wave;
   const int64_t my_q = qw0 + l32;
   const float c2 = a.scale_log2;
-  const int iq = static_cast<int>(my_q), Sq32 = static_cast<int>(a.Sq),
-            Skv32 = static_cast<int>(a.Skv), W32 = static_cast<int>(a.window);
+  // keys visible to this lane's query: [vis_lo, vis_lo + vis_span]
+  int vis_lo, vis_span;
+  {
+    const int iq = static_cast<int>(my_q);
+    int hi = static_cast<int>(a.Skv) - 1;
+    if (a.causal && iq < hi) hi = iq;
+    const int lo = a.window > 0 ? iq - static_cast<int>(a.window) + 1 : 0;
+    vis_lo = lo > 0 ? lo : 0;
+    vis_span = hi - vis_lo;
+    if (vis_span < 0 || my_q >= a.Sq) {
+      vis_lo = 0x40000000;
+      vis_span = 0;
+    }
+  }
 
   const T* Qp = static_cast<const T*>(a.q) + b * a.q_sb + hq * a.q_sh;
   const T* Dp = static_cast<const T*>(a.dout) + b * a.o_sb + hq * a.o_sh;
@@ -360,10 +385,12 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) 
   const int64_t t_lo = kv_lo / BN;
   const int64_t t_hi = kv_hi > kv_lo ? (kv_hi + BN - 1) / BN : t_lo;
 
-  constexpr int NL = 2 * tile_load_insts<D, BN>();
+  TileLoader<T, D, BN> kload, vload;
+  kload.init(a.k_ss);
+  vload.init(a.v_ss);
   auto issue = [&](int64_t kb0, int st) {
-    tile_load_async<T, D, BN>(Ks[st], Kp, a.k_ss, kb0, a.Skv);
-    tile_load_async<T, D, BN>(Vs[st], Vp, a.v_ss, kb0, a.Skv);
+    kload.issue(Ks[st], Kp, a.k_ss, kb0, a.Skv, kFull);
+    vload.issue(Vs[st], Vp, a.v_ss, kb0, a.Skv, kFull);
   };
 
   f32x16 dq[D / 32];
@@ -374,14 +401,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) 
   auto step = [&](auto stage_tag, int64_t t) {
     constexpr int st = decltype(stage_tag)::value;
     const int64_t kb0 = t * BN;
-    __syncthreads();
-    if (t + 1 < t_hi) {
-      issue(kb0 + BN, st ^ 1);
-      wait_vmcnt<NL>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    __syncthreads();
+    wait_vmcnt<0>();  // this wave's loads of tile t have landed
+    __syncthreads();  // ... and every wave's; all are done with the other stage
+    if (t + 1 < t_hi) issue(kb0 + BN, st ^ 1);
 
     bool skip = false, need_mask = kb0 + BN > a.Skv || qw0 + 31 >= a.Sq;
     if (a.causal) {
@@ -418,8 +440,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) 
       for (int j = 0; j < 16; ++j) {
         float p = __builtin_amdgcn_exp2f(fmaf(s[tt][j], c2, -lse2));
         if (need_mask) {
-          const int key = static_cast<int>(kb0) + 32 * tt + 8 * (j >> 2) + 4 * g + (j & 3);
-          if (!visible32(iq, key, Sq32, Skv32, a.causal, W32)) p = 0.f;
+          const int rel = static_cast<int>(kb0) - vis_lo + 32 * tt + 8 * (j >> 2) + 4 * g + (j & 3);
+          if (static_cast<unsigned>(rel) > static_cast<unsigned>(vis_span)) p = 0.f;
         }
         sb[2 * tt + (j >> 3)][j & 7] = static_cast<T>(p * (dp[tt][j] - del));
       }
@@ -584,11 +606,23 @@ extern "C" int zk_attn_bwd(const zk_attn_desc* desc, const void* q,
   const int64_t n_qt = (desc->Sq + DqCfg<128>::BM - 1) / DqCfg<128>::BM;
   const dim3 kgrid(static_cast<unsigned>(n_kt * desc->B * desc->Hkv));
   const dim3 qgrid(static_cast<unsigned>(n_qt * desc->B * desc->Hq));
-#define ZK_BWD(T, D)                                                                  \
-  do {                                                                                \
-    if (rows > 0) hipLaunchKernelGGL(attn_bwd_prep<T>, pgrid, dim3(256), 0, s, a);    \
-    if (n_kt > 0) hipLaunchKernelGGL((attn_bwd_dkdv<T, D>), kgrid, dim3(256), 0, s, a); \
-    if (n_qt > 0) hipLaunchKernelGGL((attn_bwd_dq<T, D>), qgrid, dim3(256), 0, s, a, n_qt); \
+  const bool q_full = desc->Sq % DkdvCfg<128>::MQ == 0;
+  const bool k_full = desc->Skv % DqCfg<128>::BN == 0;
+#define ZK_BWD(T, D)                                                                        \
+  do {                                                                                      \
+    if (rows > 0) hipLaunchKernelGGL(attn_bwd_prep<T>, pgrid, dim3(256), 0, s, a);          \
+    if (n_kt > 0) {                                                                         \
+      if (q_full)                                                                           \
+        hipLaunchKernelGGL((attn_bwd_dkdv<T, D, true>), kgrid, dim3(256), 0, s, a);         \
+      else                                                                                  \
+        hipLaunchKernelGGL((attn_bwd_dkdv<T, D, false>), kgrid, dim3(256), 0, s, a);        \
+    }                                                                                       \
+    if (n_qt > 0) {                                                                         \
+      if (k_full)                                                                           \
+        hipLaunchKernelGGL((attn_bwd_dq<T, D, true>), qgrid, dim3(256), 0, s, a, n_qt);     \
+      else                                                                                  \
+        hipLaunchKernelGGL((attn_bwd_dq<T, D, false>), qgrid, dim3(256), 0, s, a, n_qt);    \
+    }                                                                                       \
   } while (0)
   if (desc->dtype == ZK_BF16) {
     if (desc->d == 128) ZK_BWD(bf16, 128); else ZK_BWD(bf16, 64);
