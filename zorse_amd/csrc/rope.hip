@@ -11,7 +11,7 @@
 //     y1 = r(x1 c - x2 s)             y2 = r(x1 s + x2 c)
 // The inverse (backward) applies the transpose rotation with the same
 // rounding structure as autograd of those expressions.
-#include "zk_common.h"
+#include "vec.h"
 
 namespace zk {
 
@@ -80,6 +80,84 @@ __global__ __launch_bounds__(256) void rope_kernel(
   }
 }
 
+// Vectorised path for head_dim 64 / 128 with 16-byte aligned rows: a thread
+// rotates 8 pairs with 16-byte accesses; the grid is (position blocks,
+// heads, batch), so no index arithmetic divides.
+template <typename T, int D, int kPairing, bool kInverse>
+__global__ __launch_bounds__(256) void rope_vec_kernel(
+    T* __restrict__ q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+    T* __restrict__ k, int64_t k_sb, int64_t k_ss, int64_t k_sh, int64_t S, int64_t Hq,
+    const float* __restrict__ cosT, const float* __restrict__ sinT, int64_t n_pos,
+    const int64_t* __restrict__ positions) {
+  constexpr int HALF = D / 2;
+  constexpr int TPR = HALF / 8;        // threads per (position, head) row
+  constexpr int RPB = 256 / TPR;       // positions per workgroup
+  const int64_t s = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / TPR;
+  if (s >= S) return;
+  const int64_t h = blockIdx.y, b = blockIdx.z;
+  const int i0 = (threadIdx.x % TPR) * 8;  // first pair of this thread
+  T* row = h < Hq ? q + b * q_sb + s * q_ss + h * q_sh
+                  : k + b * k_sb + s * k_ss + (h - Hq) * k_sh;
+  int64_t pos = positions != nullptr ? positions[s] : s;
+  if (pos < 0) pos = 0;
+  if (pos >= n_pos) pos = n_pos - 1;
+  float c[8], sn[8];
+  Vec8<float>::load(cosT + pos * HALF + i0, c);
+  Vec8<float>::load(sinT + pos * HALF + i0, sn);
+  float x1[8], x2[8], y1[8], y2[8];
+  if (kPairing == ZK_ROPE_HALF) {
+    Vec8<T>::load(row + i0, x1);
+    Vec8<T>::load(row + i0 + HALF, x2);
+  } else {
+    float a[8], bb[8];
+    Vec8<T>::load(row + 2 * i0, a);
+    Vec8<T>::load(row + 2 * i0 + 8, bb);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x1[j] = a[2 * j];
+      x2[j] = a[2 * j + 1];
+      x1[j + 4] = bb[2 * j];
+      x2[j + 4] = bb[2 * j + 1];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) rotate_pair<T, kPairing, kInverse>(x1[j], x2[j], c[j], sn[j], y1[j], y2[j]);
+  if (kPairing == ZK_ROPE_HALF) {
+    Vec8<T>::store(row + i0, y1);
+    Vec8<T>::store(row + i0 + HALF, y2);
+  } else {
+    float a[8], bb[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      a[2 * j] = y1[j];
+      a[2 * j + 1] = y2[j];
+      bb[2 * j] = y1[j + 4];
+      bb[2 * j + 1] = y2[j + 4];
+    }
+    Vec8<T>::store(row + 2 * i0, a);
+    Vec8<T>::store(row + 2 * i0 + 8, bb);
+  }
+}
+
+template <typename T, int D>
+static void launch_rope_vec(int pairing, int inverse, void* q, int64_t q_sb, int64_t q_ss,
+                            int64_t q_sh, void* k, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                            int64_t B, int64_t S, int64_t Hq, int64_t Hkv, const float* c,
+                            const float* sn, int64_t n_pos, const int64_t* pos, hipStream_t st) {
+  constexpr int RPB = 256 / (D / 16);
+  const dim3 grid(static_cast<unsigned>((S + RPB - 1) / RPB),
+                  static_cast<unsigned>(Hq + (k != nullptr ? Hkv : 0)), static_cast<unsigned>(B));
+#define ZK_ROPEV(P, I)                                                                   \
+  hipLaunchKernelGGL((rope_vec_kernel<T, D, P, I>), grid, dim3(256), 0, st, (T*)q, q_sb,  \
+                     q_ss, q_sh, (T*)k, k_sb, k_ss, k_sh, S, Hq, c, sn, n_pos, pos)
+  if (pairing == ZK_ROPE_HALF) {
+    if (inverse) ZK_ROPEV(ZK_ROPE_HALF, true); else ZK_ROPEV(ZK_ROPE_HALF, false);
+  } else {
+    if (inverse) ZK_ROPEV(ZK_ROPE_INTERLEAVED, true); else ZK_ROPEV(ZK_ROPE_INTERLEAVED, false);
+  }
+#undef ZK_ROPEV
+}
+
 template <typename T>
 static void launch_rope(int pairing, int inverse, void* q, int64_t q_sb,
                         int64_t q_ss, int64_t q_sh, void* k, int64_t k_sb,
@@ -128,6 +206,24 @@ extern "C" int zk_rope(void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
   ZK_REQUIRE(n_pos > 0, ZK_EINVAL, "zk_rope: empty table");
   if (B == 0 || S == 0 || Hq + Hkv == 0) return ZK_OK;
   hipStream_t st = as_stream(stream);
+  // 16-byte vector path: 2-byte types, d 64 / 128, aligned rows and heads,
+  // grid dimensions within range
+  const int64_t H = Hq + (k != nullptr ? Hkv : 0);
+  bool vec = dtype != ZK_F32 && (d == 64 || d == 128) && aligned(q, 16) &&
+             (k == nullptr || aligned(k, 16)) && H < 65536 && B < 65536 &&
+             S / (256 / (d / 16)) < 0x7fffffff;
+  vec = vec && q_sb % 8 == 0 && q_ss % 8 == 0 && q_sh % 8 == 0;
+  if (k != nullptr) vec = vec && k_sb % 8 == 0 && k_ss % 8 == 0 && k_sh % 8 == 0;
+  if (vec) {
+#define ZK_VEC(T, D) launch_rope_vec<T, D>(pairing, inverse, q, q_sb, q_ss, q_sh, k, k_sb, k_ss, k_sh, B, S, Hq, Hkv, cos, sin, n_pos, positions, st)
+    if (dtype == ZK_BF16) {
+      if (d == 128) ZK_VEC(bf16, 128); else ZK_VEC(bf16, 64);
+    } else {
+      if (d == 128) ZK_VEC(f16, 128); else ZK_VEC(f16, 64);
+    }
+#undef ZK_VEC
+    return launch_status("zk_rope");
+  }
   if (dtype == ZK_BF16)
     launch_rope<bf16>(pairing, inverse, q, q_sb, q_ss, q_sh, k, k_sb, k_ss, k_sh, B, S, Hq, Hkv, d, cos, sin, n_pos, positions, st);
   else if (dtype == ZK_F16)
