@@ -240,8 +240,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
         }
       }
     };
-    // Software pipeline over the two halves: the VALU work of one half is
-    // issued between MFMAs that do not depend on it.
+    // Both halves in one straight-line block: the VALU work of one half can
+    // be issued between MFMAs that do not depend on it.
     auto body = [&](auto mask_tag) {
       f32x16 s0, dp0, s1, dp1;
       V8 pb0[2], sb0[2], pb1[2], sb1[2];
@@ -251,31 +251,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
       accumulate(0, pb0, sb0);
       probs(mask_tag, 1, s1, dp1, pb1, sb1);
       accumulate(1, pb1, sb1);
-      // Issue order for the scheduler (groups: DS read 0x100, MFMA 0x008,
-      // VALU 0x002): the score MFMAs of half 1 carry the softmax of half 0,
-      // the dV / dK MFMAs of half 0 carry the softmax of half 1.
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      }
+      // single-wave MFMA / LDS / VALU interleaving strategy of the compiler's
+      // instruction-group scheduler (one wave per SIMD runs this kernel)
+      __builtin_amdgcn_iglp_opt(1);
     };
     if (need_mask)
       body(std::true_type{});
