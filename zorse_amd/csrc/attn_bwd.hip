@@ -149,9 +149,11 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
   TileLoader<T, D, MQ> qload, dload;
   qload.init(a.q_ss);
   dload.init(a.o_ss);
-  auto issue = [&](int64_t it, int st) {
-    const int64_t hq = hk * n_rep + it / nqb;
-    const int64_t qb0 = (qb_lo + it % nqb) * MQ;
+  // iteration it covers query block qb_lo + it % nqb of q-head hk * n_rep +
+  // it / nqb; (qbi, hr) below track that pair without dividing
+  auto issue = [&](int64_t qbi, int64_t hr, int st) {
+    const int64_t hq = hk * n_rep + hr;
+    const int64_t qb0 = qbi * MQ;
     const T* Qp = static_cast<const T*>(a.q) + b * a.q_sb + hq * a.q_sh;
     const T* Dp = static_cast<const T*>(a.dout) + b * a.o_sb + hq * a.o_sh;
     qload.issue(Qs[st], Qp, a.q_ss, qb0, a.Sq, kFull);
@@ -164,12 +166,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
   };
 
   // One pipeline step on LDS stage ST (compile-time: immediate LDS offsets).
-  auto step = [&](auto stage_tag, int64_t it) {
+  auto step = [&](auto stage_tag, int64_t qbi, int64_t nxt_qbi, int64_t nxt_hr, bool has_next) {
     constexpr int st = decltype(stage_tag)::value;
-    const int64_t qb0 = (qb_lo + it % nqb) * MQ;
-    wait_vmcnt<0>();  // this wave's loads of block it have landed
+    const int64_t qb0 = qbi * MQ;
+    wait_vmcnt<0>();  // this wave's loads of this block have landed
     __syncthreads();  // ... and every wave's; all are done with the other stage
-    if (it + 1 < n_iter) issue(it + 1, st ^ 1);
+    if (has_next) issue(nxt_qbi, nxt_hr, st ^ 1);
 
     // wave-uniform classification of this (query block, 32 keys) tile
     bool skip = false, need_mask = kw0 + 31 >= a.Skv || qb0 + MQ > a.Sq;
@@ -261,10 +263,26 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
       body(std::false_type{});
   };
 
-  if (n_iter > 0) issue(0, 0);
+  int64_t qbi = qb_lo, hr = 0;
+  auto advance = [&](int64_t& q, int64_t& h) {
+    if (++q == qb_hi) {
+      q = qb_lo;
+      ++h;
+    }
+  };
+  if (n_iter > 0) issue(qbi, hr, 0);
   for (int64_t it = 0; it < n_iter; it += 2) {
-    step(std::integral_constant<int, 0>{}, it);
-    if (it + 1 < n_iter) step(std::integral_constant<int, 1>{}, it + 1);
+    int64_t nq = qbi, nh = hr;
+    advance(nq, nh);
+    step(std::integral_constant<int, 0>{}, qbi, nq, nh, it + 1 < n_iter);
+    qbi = nq;
+    hr = nh;
+    if (it + 1 < n_iter) {
+      advance(nq, nh);
+      step(std::integral_constant<int, 1>{}, qbi, nq, nh, it + 2 < n_iter);
+      qbi = nq;
+      hr = nh;
+    }
   }
 
   // dK = scale (Q^T dS)^T, dV = (dO^T P)^T: lane holds key my_key and
