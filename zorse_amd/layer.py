@@ -2,9 +2,9 @@
 
 One autograd node per layer: the whole of LlamaDecoderLayer.forward
 (models/llama_simple.py:456-479) -- RMSNorm, the q|k|v projection as ONE GEMM,
-RoPE, flash attention (GQA, causal / sliding window), o_proj with the residual
-add folded into the GEMM (addmm), RMSNorm, gate|up as ONE GEMM, SwiGLU, down
-with the residual folded in -- and its backward, which writes every weight
+RoPE, flash attention (GQA, causal / sliding window), o_proj, the residual
+add fused into the second RMSNorm, gate|up as ONE GEMM, SwiGLU, down with the
+residual folded into the GEMM (addmm) -- and its backward, which writes every weight
 gradient straight into one flat gradient buffer laid out like the flat
 parameter (q, k, v, o, gate, up, down, ln1, ln2 -- the registration order the
 reference's FSDP flat parameter uses, zorse_utils/pipeline.py:120-148).
@@ -113,8 +113,10 @@ def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec):
     K.rope_(q, k, cos, sin, interleaved=spec.interleaved_rope)
     o, lse = K.attn_fwd(q, k, v, causal=spec.causal, window=spec.window)
     o2 = o.view(T, spec.q_dim)
-    hdn = torch.addmm(x2, o2, w.o.t())               # residual + o_proj(attn)
-    n2, rstd2, _ = K.rmsnorm_fwd(hdn, w.ln2, spec.eps)
+    # o_proj, then residual add fused into the second RMSNorm (one pass writes
+    # hdn = x + round(o_proj) and its normalisation, the reference's order)
+    attn_out = _mm(o2, w.o.t())
+    n2, rstd2, hdn = K.rmsnorm_fwd(attn_out, w.ln2, spec.eps, residual=x2)
     gu = _mm(n2, w.gu.t())                           # [T, 2F] = gate | up
     F = spec.ffn
     z = K.swiglu_fwd(gu[:, :F], gu[:, F:])
