@@ -224,3 +224,34 @@ def test_ce_chunk_validation(lib):
     assert lib.zk_ce_fwd_chunk(p, 4, 8, 8, None, 0, p, p, p, 2, None) == -1  # null labels
     assert lib.zk_ce_bwd_chunk(p, 4, 8, 8, p, 0, p, 1.0, 9, None) == -2      # bad dtype
     assert lib.zk_ce_fwd_chunk(ctypes.c_void_p(18), 4, 8, 8, p, 0, p, p, p, 2, None) == -3
+
+
+def test_attention_cache_keys():
+    """The recompute cache hits only for the same input storage, version and
+    weights, including through detach() (how the stage runner re-feeds the
+    saved input); a modified input or weight misses."""
+    from zorse_amd.layer import AttentionCache
+    c = AttentionCache()
+    x = torch.randn(2, 8, 16)
+    w = torch.zeros(32)
+    o, lse = torch.ones(3), torch.zeros(3)
+    c.bind(x, w, w)
+    assert c.take() is None
+    c.put(o, lse)
+    assert len(c) == 1
+    c.bind(torch.randn(2, 8, 16), w, w)             # other tensor, same shape
+    assert c.take() is None
+    c.bind(x.detach(), w, w)                        # same storage and version
+    hit = c.take()
+    assert hit is not None and hit[0] is o and hit[1] is lse and len(c) == 0
+    c.bind(x, w, w)
+    c.put(o, lse)
+    x.add_(1.0)                                     # input modified in place
+    c.bind(x, w, w)
+    assert c.take() is None
+    c.clear()
+    c.bind(x, w, w)
+    c.put(o, lse)
+    torch.autograd.graph.increment_version(w)       # weights stepped
+    c.bind(x, w, w)
+    assert c.take() is None

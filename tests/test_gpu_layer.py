@@ -251,6 +251,52 @@ def test_stage_runner_optimizer_in_backwards(dev):
         assert layer.flat_param.grad is None
 
 
+def test_stage_recompute_attention_cache(dev):
+    """Recompute mode (the reference pipeline's second forward inside the
+    backward, zorse_utils/pipeline_schedule_v2.py:157-200): with the attention
+    cache the re-forward launches no attention kernel, and every layer
+    gradient is bit-identical to recompute without the cache and to the
+    single-forward path (the kernels are deterministic)."""
+    from zorse_amd import layer as L
+    from zorse_amd.stage import StageRunner
+    kw = dict(hidden_size=256, num_attention_heads=2, intermediate_size=512, rope_theta=1e4)
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(1, 256, 256, generator=g).to(dtype).to(dev)
+    dout = torch.randn(1, 256, 256, generator=g).to(dtype).to(dev)
+    calls = {"n": 0}
+    real = L.K.attn_fwd
+
+    def counting(*a, **k):
+        calls["n"] += 1
+        return real(*a, **k)
+
+    results = {}
+    try:
+        L.K.attn_fwd = counting
+        for name, rc, cache in (("plain", False, False), ("recompute", True, False),
+                                ("cached", True, True)):
+            layers = [_layer(kw, dev, param_dtype=dtype, seed=s) for s in (1, 2)]
+            grads = {}
+            for i, l in enumerate(layers):
+                l.flat_param.register_post_accumulate_grad_hook(
+                    lambda p, i=i: grads.__setitem__(i, p.grad.detach().clone()))
+            runner = StageRunner(layers, lr=1e-4, recompute=rc, cache_attention=cache)
+            calls["n"] = 0
+            runner.step(x, dout)
+            runner.wait_optimizer()
+            torch.cuda.synchronize()
+            results[name] = (grads, calls["n"], [len(c) for c in runner.attn_caches])
+    finally:
+        L.K.attn_fwd = real
+    assert results["plain"][1] == 2 and results["recompute"][1] == 4
+    assert results["cached"][1] == 2, "the recompute forward ran attention again"
+    assert results["cached"][2] == [0, 0], "cache entries left after the backward"
+    for i in (0, 1):
+        assert torch.equal(results["cached"][0][i], results["recompute"][0][i])
+        assert torch.equal(results["cached"][0][i], results["plain"][0][i])
+
+
 # ------------------------------------------------------------- llama_v2 block --
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

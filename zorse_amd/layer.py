@@ -98,8 +98,13 @@ def _mm(a, b, out=None):
     return torch.mm(a, b) if out is None else torch.mm(a, b, out=out)
 
 
-def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec):
-    """Forward on compute-dtype tensors; returns (out, saved tuple)."""
+def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=None):
+    """Forward on compute-dtype tensors; returns (out, saved tuple).
+
+    ``attn_cache`` (optional) is an AttentionCache: a hit supplies the
+    attention output and LSE of an earlier forward of the same input and
+    weights, so the attention forward is skipped (the recompute of the
+    reference's pipeline backward); a miss computes them and records them."""
     B, S, h = x.shape
     T = B * S
     d, Hq, Hkv = spec.head_dim, spec.heads, spec.kv_heads
@@ -111,7 +116,13 @@ def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec):
     v = qkv[:, spec.q_dim + spec.kv_dim:].view(B, S, Hkv, d)
     cos, sin = rope_tables(S, d, spec.rope_theta, x.dtype, x.device, spec.interleaved_rope)
     K.rope_(q, k, cos, sin, interleaved=spec.interleaved_rope)
-    o, lse = K.attn_fwd(q, k, v, causal=spec.causal, window=spec.window)
+    hit = attn_cache.take() if attn_cache is not None else None
+    if hit is not None:
+        o, lse = hit
+    else:
+        o, lse = K.attn_fwd(q, k, v, causal=spec.causal, window=spec.window)
+        if attn_cache is not None:
+            attn_cache.put(o, lse)
     o2 = o.view(T, spec.q_dim)
     # o_proj, then residual add fused into the second RMSNorm (one pass writes
     # hdn = x + round(o_proj) and its normalisation, the reference's order)
@@ -171,15 +182,57 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
     return dx.view(B, S, h)
 
 
+class AttentionCache:
+    """Attention outputs of forwards that will be recomputed.
+
+    The reference's pipeline runs every layer forward twice per micro-batch:
+    once without autograd, and again inside the backward to rebuild the
+    activations (zorse_utils/pipeline_schedule_v2.py:157-200).  Between the
+    two the input and the weights are unchanged, so the attention output O
+    and its LSE can be kept from the first forward and the second skips the
+    attention kernel.  Entries are keyed by the input's storage address,
+    offset, shape, strides and version counter plus the weights' address and
+    version counters; an entry keeps the input's storage alive, so no other
+    tensor can take that address while the entry exists.  A forward whose key
+    has no entry computes attention and records it; an entry is removed when
+    it is used."""
+
+    def __init__(self):
+        self._entries = {}
+        self._key = None
+        self._storage = None
+
+    def __len__(self):
+        return len(self._entries)
+
+    def clear(self):
+        self._entries.clear()
+
+    def bind(self, x, flat_param, w_flat):
+        st = x.untyped_storage()
+        self._storage = st
+        self._key = (st.data_ptr(), x.storage_offset(), tuple(x.shape), tuple(x.stride()),
+                     x._version, flat_param._version, w_flat.data_ptr(), w_flat._version)
+
+    def take(self):
+        hit = self._entries.pop(self._key, None)
+        return None if hit is None else hit[1:]
+
+    def put(self, o, lse):
+        self._entries[self._key] = (self._storage, o, lse)
+
+
 class DecoderLayerFunction(torch.autograd.Function):
     """autograd node of one decoder layer: inputs (x, flat_param)."""
 
     @staticmethod
-    def forward(ctx, x, flat_param, spec, weights_lowp):
+    def forward(ctx, x, flat_param, spec, weights_lowp, attn_cache=None):
         w_flat = weights_lowp if weights_lowp is not None else flat_param
         w = FlatViews(spec, w_flat)
+        if attn_cache is not None:
+            attn_cache.bind(x, flat_param, w_flat)
         with torch.autocast("cuda", enabled=False):
-            out, saved = layer_forward(x.contiguous(), w, spec)
+            out, saved = layer_forward(x.contiguous(), w, spec, attn_cache)
         ctx.spec = spec
         ctx.param_dtype = flat_param.dtype
         ctx.save_for_backward(w_flat, *saved)
@@ -196,4 +249,4 @@ class DecoderLayerFunction(torch.autograd.Function):
             dx = layer_backward(dout, saved, w, spec, grad_flat)
         if ctx.param_dtype != grad_flat.dtype:
             grad_flat = grad_flat.to(ctx.param_dtype)
-        return dx, grad_flat, None, None
+        return dx, grad_flat, None, None, None

@@ -160,6 +160,9 @@ class FlatDecoderLayer(nn.Module):
         self.flat_param = nn.Parameter(torch.empty(spec.numel, dtype=param_dtype, device=device))
         self._lowp_cache = None
         self._init_std, self._init_gen = init_std, generator
+        # AttentionCache shared by the two forwards of a recomputed micro-batch
+        # (set by the stage runner; None = always compute attention)
+        self.attn_cache = None
 
     # -- parameters -----------------------------------------------------------
     def param_view(self, name: str) -> torch.Tensor:
@@ -218,7 +221,7 @@ class FlatDecoderLayer(nn.Module):
             cdt = torch.get_autocast_dtype("cuda")
             x = x.to(cdt)
         return DecoderLayerFunction.apply(x, self.flat_param, self.spec,
-                                          self._compute_weights(cdt))
+                                          self._compute_weights(cdt), self.attn_cache)
 
 
 class LlamaDecoderLayer(FlatDecoderLayer):

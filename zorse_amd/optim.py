@@ -68,6 +68,10 @@ class FusedAdamW(torch.optim.Optimizer):
                              lr=group["lr"], beta1=b1, beta2=b2, eps=group["eps"],
                              weight_decay=group["weight_decay"], step=st["step"],
                              lowp_out=p.view(-1) if master is not None else None)
+                # the kernel wrote p through a raw pointer: advance its version
+                # counter as an in-place torch op would, so caches keyed on it
+                # (compute-dtype weight copies, attention caches) see the update
+                torch.autograd.graph.increment_version(p)
         return loss
 
     def master_param(self, p: torch.Tensor) -> torch.Tensor:

@@ -10,7 +10,10 @@ Reference behaviour reproduced (single GPU, no communication):
     ``--optimizer_in_backwards`` path built at zorse_utils/pipeline.py:
     150-181), then the gradient is released;
   * ``recompute=True`` re-runs each layer's forward inside the backward, as
-    ``_backward_layer`` does (zorse_utils/pipeline_schedule_v2.py:157-200).
+    ``_backward_layer`` does (zorse_utils/pipeline_schedule_v2.py:157-200);
+    with ``cache_attention`` (the default) the first forward keeps each
+    layer's attention output and LSE and the re-run skips the attention
+    forward kernel.
 
 All streams are created at the default priority.
 """
@@ -21,6 +24,7 @@ from typing import Sequence
 import torch
 import torch.nn as nn
 
+from .layer import AttentionCache
 from .optim import FusedAdamW
 
 
@@ -32,10 +36,19 @@ def _call(layer: nn.Module, x: torch.Tensor) -> torch.Tensor:
 
 class StageRunner:
     def __init__(self, layers: Sequence[nn.Module], lr=1e-4, betas=(0.9, 0.95), eps=1e-8,
-                 weight_decay=0.1, optimizer_in_backwards=True, recompute=False):
+                 weight_decay=0.1, optimizer_in_backwards=True, recompute=False,
+                 cache_attention=True):
         self.layers = list(layers)
         self.optimizer_in_backwards = optimizer_in_backwards
         self.recompute = recompute
+        # one attention cache per fused decoder layer (recompute mode only)
+        self.attn_caches = []
+        if recompute and cache_attention:
+            for layer in self.layers:
+                for m in layer.modules():
+                    if hasattr(m, "attn_cache") and hasattr(m, "flat_param"):
+                        m.attn_cache = AttentionCache()
+                        self.attn_caches.append(m.attn_cache)
         self.optimizers = []
         self._hooks = []
         dev = next(self.layers[0].parameters()).device
@@ -95,6 +108,8 @@ class StageRunner:
                 y.backward(g)
                 g = xr.grad
             self._inputs = []
+            for c in self.attn_caches:  # entries of forwards never recomputed
+                c.clear()
         if not self.optimizer_in_backwards:
             for opt in self.optimizers:
                 opt.step()
