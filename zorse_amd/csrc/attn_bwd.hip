@@ -26,6 +26,7 @@
 #include <type_traits>
 
 #include "attn_common.h"
+#include "vec.h"
 
 namespace zk {
 
@@ -58,6 +59,37 @@ __global__ __launch_bounds__(256) void attn_bwd_prep(AttnArgs a) {
   acc += __shfl_xor(acc, 4, 64);
   if (row < rows && sub == 0) {
     const int64_t i = (b * a.Hq + h) * a.Sq + q;
+    a.delta[i] = acc;
+    const float l = a.lse[i];
+    a.lse2[i] = l == -INFINITY ? INFINITY : l * kLog2e;
+  }
+}
+
+// Vector variant for 2-byte storage and d = 64 / 128: D / 8 lanes per row,
+// 16-byte loads, grid (query blocks, B * Hq) so that the delta / lse2 writes
+// of a workgroup are consecutive queries of one head.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_bwd_prep_vec(AttnArgs a) {
+  constexpr int LPR = D / 8;        // lanes per row
+  constexpr int RPB = 256 / LPR;    // rows per workgroup
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
+  const int64_t bh = blockIdx.y;
+  const int64_t b = bh / a.Hq, h = bh % a.Hq;
+  const int sub = threadIdx.x % LPR;
+  float acc = 0.f;
+  if (q < a.Sq) {
+    const T* Or = static_cast<const T*>(a.o) + b * a.o_sb + q * a.o_ss + h * a.o_sh + 8 * sub;
+    const T* Dr = static_cast<const T*>(a.dout) + b * a.o_sb + q * a.o_ss + h * a.o_sh + 8 * sub;
+    float ov[8], dv[8];
+    Vec8<T>::load(Or, ov);
+    Vec8<T>::load(Dr, dv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = fmaf(ov[e], dv[e], acc);
+  }
+#pragma unroll
+  for (int off = 1; off < LPR; off <<= 1) acc += __shfl_xor(acc, off, 64);
+  if (q < a.Sq && sub == 0) {
+    const int64_t i = bh * a.Sq + q;
     a.delta[i] = acc;
     const float l = a.lse[i];
     a.lse2[i] = l == -INFINITY ? INFINITY : l * kLog2e;
@@ -606,7 +638,13 @@ extern "C" int zk_attn_bwd(const zk_attn_desc* desc, const void* q,
   const bool k_full = desc->Skv % DqCfg<128>::BN == 0;
 #define ZK_BWD(T, D)                                                                        \
   do {                                                                                      \
-    if (rows > 0) hipLaunchKernelGGL(attn_bwd_prep<T>, pgrid, dim3(256), 0, s, a);          \
+    if (rows > 0 && desc->B * desc->Hq <= 65535) {                                          \
+      const dim3 vgrid(static_cast<unsigned>((desc->Sq + 256 / (D / 8) - 1) / (256 / (D / 8))), \
+                       static_cast<unsigned>(desc->B * desc->Hq));                          \
+      hipLaunchKernelGGL((attn_bwd_prep_vec<T, D>), vgrid, dim3(256), 0, s, a);            \
+    } else if (rows > 0) {                                                                  \
+      hipLaunchKernelGGL(attn_bwd_prep<T>, pgrid, dim3(256), 0, s, a);                      \
+    }                                                                                       \
     if (n_kt > 0) {                                                                         \
       if (q_full)                                                                           \
         hipLaunchKernelGGL((attn_bwd_dkdv<T, D, true>), kgrid, dim3(256), 0, s, a);         \
