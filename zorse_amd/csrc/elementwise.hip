@@ -15,11 +15,9 @@ template <typename T>
 __global__ __launch_bounds__(256) void swiglu_fwd_vec(
     const T* __restrict__ gate, const T* __restrict__ up, int64_t ld_in,
     T* __restrict__ z, int64_t ld_z, int64_t rows, int64_t cols) {
-  const int64_t nch = cols / 8, total = rows * nch;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-       t < total; t += stride) {
-    const int64_t r = t / nch, c = (t - r * nch) * 8;
+  // one workgroup per row (grid-stride over rows), 8 columns per thread-step
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x)
+  for (int64_t c = threadIdx.x * 8; c < cols; c += 256 * 8) {
     float g[8], u[8], o[8];
     Vec8<T>::load(gate + r * ld_in + c, g);
     Vec8<T>::load(up + r * ld_in + c, u);
@@ -34,11 +32,8 @@ __global__ __launch_bounds__(256) void swiglu_bwd_vec(
     const T* __restrict__ dz, int64_t ld_dz, const T* __restrict__ gate,
     const T* __restrict__ up, int64_t ld_in, T* __restrict__ dgate,
     T* __restrict__ dup, int64_t ld_out, int64_t rows, int64_t cols) {
-  const int64_t nch = cols / 8, total = rows * nch;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-       t < total; t += stride) {
-    const int64_t r = t / nch, c = (t - r * nch) * 8;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x)
+  for (int64_t c = threadIdx.x * 8; c < cols; c += 256 * 8) {
     float d[8], g[8], u[8], dg[8], du[8];
     Vec8<T>::load(dz + r * ld_dz + c, d);
     Vec8<T>::load(gate + r * ld_in + c, g);
@@ -167,7 +162,7 @@ extern "C" int zk_swiglu_fwd(const void* gate, const void* up, int64_t ld_in,
   const bool vec = cols % 8 == 0 && ld_in % 8 == 0 && ld_z % 8 == 0 &&
                    aligned(gate, 16) && aligned(up, 16) && aligned(z, 16);
   if (vec) {
-    const int grid = grid_for(rows * (cols / 8));
+    const int grid = static_cast<int>(rows < 0x7fffffff ? rows : 0x7fffffff);  // a row per workgroup
     if (dtype == ZK_BF16)
       hipLaunchKernelGGL(swiglu_fwd_vec<bf16>, dim3(grid), dim3(256), 0, s, (const bf16*)gate, (const bf16*)up, ld_in, (bf16*)z, ld_z, rows, cols);
     else if (dtype == ZK_F16)
@@ -195,7 +190,7 @@ extern "C" int zk_swiglu_bwd(const void* dz, int64_t ld_dz, const void* gate,
                    ld_out % 8 == 0 && aligned(dz, 16) && aligned(gate, 16) &&
                    aligned(up, 16) && aligned(dgate, 16) && aligned(dup, 16);
   if (vec) {
-    const int grid = grid_for(rows * (cols / 8));
+    const int grid = static_cast<int>(rows < 0x7fffffff ? rows : 0x7fffffff);  // a row per workgroup
     if (dtype == ZK_BF16)
       hipLaunchKernelGGL(swiglu_bwd_vec<bf16>, dim3(grid), dim3(256), 0, s, (const bf16*)dz, ld_dz, (const bf16*)gate, (const bf16*)up, ld_in, (bf16*)dgate, (bf16*)dup, ld_out, rows, cols);
     else if (dtype == ZK_F16)
