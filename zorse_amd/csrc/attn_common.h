@@ -210,6 +210,16 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
+// Value of lane l ^ 32 (the other half of the wave) via gfx950's
+// v_permlane32_swap: a VALU exchange, no LDS round trip.  swap(x, x) leaves
+// {x[0..31], x[0..31]} in the first result and {x[32..63], x[32..63]} in
+// the second, so lane l's partner value is the result from the other half.
+__device__ __forceinline__ float other_half(float x) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                   false, false);
+  return __uint_as_float((threadIdx.x & 32) ? sw[0] : sw[1]);
+}
+
 // True when key kj is visible from query qi (32-bit positions).
 __device__ __forceinline__ bool visible32(int qi, int kj, int Sq, int Skv, int causal,
                                           int window) {

@@ -177,7 +177,7 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
       for (int tt = 0; tt < BN / 32; ++tt)
 #pragma unroll
         for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, s[tt][j]);
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      mloc = fmaxf(mloc, other_half(mloc));
       // move the reference maximum only when it has grown past the threshold
       const bool grow = (mloc - m_ref) * c2 > kRescaleThreshold;
       if (__any(grow)) {
@@ -226,7 +226,7 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
     if (t + 1 < t_hi) step(std::integral_constant<int, 1>{}, t + 1);
   }
 
-  const float l_tot = l_i + __shfl_xor(l_i, 32, 64);
+  const float l_tot = l_i + other_half(l_i);
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   if (my_q < a.Sq) {
     T* Op = static_cast<T*>(a.out) + b * a.o_sb + hq * a.o_sh + my_q * a.o_ss;
