@@ -136,6 +136,13 @@ def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=Non
     return out.view(B, S, h), saved
 
 
+# Host callbacks run right before a layer's attention backward is enqueued
+# (the stage runner starts the previous layer's optimizer step there, so the
+# HBM-bound update runs beside the LDS-bound attention kernels rather than
+# beside the projection GEMMs).
+BEFORE_ATTENTION_BACKWARD: list = []
+
+
 def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
                    grad_flat: torch.Tensor) -> torch.Tensor:
     """Backward of layer_forward; writes weight grads into ``grad_flat``
@@ -170,6 +177,8 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
     dq = dqkv[:, :spec.q_dim].view(B, S, Hq, d)
     dk = dqkv[:, spec.q_dim:spec.q_dim + spec.kv_dim].view(B, S, Hkv, d)
     dv = dqkv[:, spec.q_dim + spec.kv_dim:].view(B, S, Hkv, d)
+    for fn in list(BEFORE_ATTENTION_BACKWARD):
+        fn()
     K.attn_bwd(q, k, v, o2.view(B, S, Hq, d), do2.view(B, S, Hq, d), lse,
                causal=spec.causal, window=spec.window, dq=dq, dk=dk, dv=dv)
     del do2

@@ -24,6 +24,7 @@ from typing import Sequence
 import torch
 import torch.nn as nn
 
+from . import layer as _layer_mod
 from .layer import AttentionCache
 from .optim import FusedAdamW
 
@@ -37,9 +38,16 @@ def _call(layer: nn.Module, x: torch.Tensor) -> torch.Tensor:
 class StageRunner:
     def __init__(self, layers: Sequence[nn.Module], lr=1e-4, betas=(0.9, 0.95), eps=1e-8,
                  weight_decay=0.1, optimizer_in_backwards=True, recompute=False,
-                 cache_attention=True):
+                 cache_attention=True, optimizer_overlap="attention"):
+        if optimizer_overlap not in ("attention", "immediate"):
+            raise ValueError(f"optimizer_overlap {optimizer_overlap!r}: 'attention' or 'immediate'")
         self.layers = list(layers)
         self.optimizer_in_backwards = optimizer_in_backwards
+        # "immediate": a layer's step is enqueued as soon as its gradient is
+        # complete; "attention": it is held until the next layer's attention
+        # backward starts, so that it overlaps that kernel instead of GEMMs
+        self.optimizer_overlap = optimizer_overlap
+        self._pending = []
         self.recompute = recompute
         # one attention cache per fused decoder layer (recompute mode only)
         self.attn_caches = []
@@ -64,8 +72,16 @@ class StageRunner:
 
     def _make_hook(self, opt: FusedAdamW):
         def hook(p: torch.Tensor):
-            self._step_on_side_stream(opt, p)
+            if self.optimizer_overlap == "attention":
+                self._pending.append((opt, p))
+            else:
+                self._step_on_side_stream(opt, p)
         return hook
+
+    def _launch_pending(self):
+        pending, self._pending = self._pending, []
+        for opt, p in pending:
+            self._step_on_side_stream(opt, p)
 
     def _step_on_side_stream(self, opt: FusedAdamW, p: torch.Tensor):
         cur = torch.cuda.current_stream(p.device)
@@ -98,18 +114,24 @@ class StageRunner:
         return x
 
     def backward(self, out: torch.Tensor, grad: torch.Tensor):
-        if not self.recompute:
-            out.backward(grad)
-        else:
-            g = grad
-            for layer, x in zip(reversed(self.layers), reversed(self._inputs)):
-                xr = x.detach().requires_grad_(True)
-                y = _call(layer, xr)
-                y.backward(g)
-                g = xr.grad
-            self._inputs = []
-            for c in self.attn_caches:  # entries of forwards never recomputed
-                c.clear()
+        hook = self._launch_pending
+        _layer_mod.BEFORE_ATTENTION_BACKWARD.append(hook)
+        try:
+            if not self.recompute:
+                out.backward(grad)
+            else:
+                g = grad
+                for layer, x in zip(reversed(self.layers), reversed(self._inputs)):
+                    xr = x.detach().requires_grad_(True)
+                    y = _call(layer, xr)
+                    y.backward(g)
+                    g = xr.grad
+                self._inputs = []
+                for c in self.attn_caches:  # entries of forwards never recomputed
+                    c.clear()
+        finally:
+            _layer_mod.BEFORE_ATTENTION_BACKWARD.remove(hook)
+        self._launch_pending()  # the last layer's step: nothing left to overlap
         if not self.optimizer_in_backwards:
             for opt in self.optimizers:
                 opt.step()
