@@ -205,6 +205,15 @@ int zk_ce_bwd_chunk(void* logits, int64_t rows, int64_t cols, int64_t ld,
 int zk_cast(const void* x, int x_dtype, void* y, int y_dtype, int64_t n,
             int accumulate, zk_stream_t stream);
 
+/* 2-D transpose, dst[c][r] = src[r][c] for r < rows, c < cols (row strides
+ * ld_src >= cols, ld_dst >= rows, elements).  Stands in for the layout the
+ * reference's autograd gives nn.Linear's weight gradient
+ * (grad_weight = grad_output^T @ input, models/llama_simple.py:206-221,
+ * 293-295, 368 and the MLP projections): the backward materialises
+ * grad_output^T so that GEMM reduces over contiguous tokens. */
+int zk_transpose(const void* src, int64_t ld_src, void* dst, int64_t ld_dst,
+                 int64_t rows, int64_t cols, int dtype, zk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

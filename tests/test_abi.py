@@ -74,6 +74,11 @@ def test_validation_codes(lib):
     assert lib.zk_swiglu_fwd(p, p, 4, p, 8, 2, 8, 2, None) == -1
     assert lib.zk_rope(p, 0, 0, 0, None, 0, 0, 0, 1, 1, 1, 0, 7, p, p, 1, None, 0, 0, 2, None) == -1
     assert lib.zk_cast(p, 5, p, 0, 8, 0, None) == -2
+    # transpose: ld_dst < rows, in place, zero-size is a no-op
+    q = ctypes.c_void_p(32)
+    assert lib.zk_transpose(p, 8, q, 4, 8, 8, 2, None) == -1
+    assert lib.zk_transpose(p, 8, p, 8, 8, 8, 2, None) == -1
+    assert lib.zk_transpose(None, 8, None, 8, 0, 8, 2, None) == 0
 
 
 def test_wrappers_reject_cpu_tensors():

@@ -308,6 +308,21 @@ def test_cast(dev):
     assert torch.equal(y, (x.to(torch.bfloat16).float() + x).to(torch.bfloat16))
 
 
+@pytest.mark.parametrize("dtype,rows,cols", [(torch.bfloat16, 4096, 12288), (torch.float16, 200, 72),
+                                             (torch.bfloat16, 65, 131), (torch.float32, 130, 67)])
+def test_transpose(dev, dtype, rows, cols):
+    """zk_transpose (the weight-gradient layout change) is an exact copy:
+    full tiles, ragged edges, the scalar path; also from a strided view."""
+    from zorse_amd import kernels as K
+    x = _rand((rows, cols), dtype, 61).to(dev)
+    assert torch.equal(K.transpose(x), x.t())
+    wide = _rand((rows, cols + 8), dtype, 62).to(dev)
+    view = wide[:, 8:]
+    out = torch.empty(cols, rows, dtype=dtype, device=dev)
+    K.transpose(view, out=out)
+    assert torch.equal(out, view.t())
+
+
 # ------------------------------------------------------ LM head + cross-entropy --
 
 @pytest.mark.parametrize("dtype,V,chunk", [(torch.float32, 1000, 384), (torch.bfloat16, 4096, 1024),

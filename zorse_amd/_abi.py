@@ -86,6 +86,7 @@ SIGNATURES = {
     "zk_ce_fwd_chunk": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr, _int,
                                _ptr]),
     "zk_ce_bwd_chunk": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _f32, _int, _ptr]),
+    "zk_transpose": (_int, [_ptr, _i64, _ptr, _i64, _i64, _i64, _int, _ptr]),
 }
 
 _lock = threading.Lock()

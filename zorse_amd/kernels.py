@@ -332,6 +332,22 @@ def cast_(src: torch.Tensor, dst: torch.Tensor, accumulate: bool = False) -> tor
     return dst
 
 
+def transpose(src: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out = src^T for a 2-D tensor with unit column stride; ``out`` (rows
+    with unit stride, shape (cols, rows)) may be supplied."""
+    dev = _require_gpu(src)
+    if src.dim() != 2 or src.stride(1) != 1:
+        raise ValueError("transpose needs a 2-D tensor with unit column stride")
+    rows, cols = src.shape
+    if out is None:
+        out = torch.empty(cols, rows, device=dev, dtype=src.dtype)
+    if out.shape != (cols, rows) or out.dtype != src.dtype or out.stride(1) != 1:
+        raise ValueError("out must be (cols, rows) of the same dtype with unit column stride")
+    check(lib().zk_transpose(ptr(src), src.stride(0), ptr(out), out.stride(0), rows, cols,
+                             dtype_code(src.dtype), stream_handle(dev)), "zk_transpose")
+    return out
+
+
 def device_info(device: int = 0) -> dict:
     import ctypes
     arch = ctypes.create_string_buffer(64)

@@ -98,6 +98,23 @@ def _mm(a, b, out=None):
     return torch.mm(a, b) if out is None else torch.mm(a, b, out=out)
 
 
+# tokens from which the weight gradient goes through an explicit transpose
+_WGRAD_TRANSPOSE_MIN_TOKENS = 1024
+
+
+def _wgrad(dy, x, out):
+    """out = dy^T x (the weight gradient of y = x W^T).  For 2-byte types and
+    long token counts dy^T is materialised first (zk_transpose): the GEMM then
+    streams both operands along the token reduction, which is faster than the
+    strided-reduction form by more than the transpose costs."""
+    if dy.dtype in (torch.bfloat16, torch.float16) and dy.shape[0] >= _WGRAD_TRANSPOSE_MIN_TOKENS:
+        dyt = K.transpose(dy)
+        torch.mm(dyt, x, out=out)
+        del dyt
+    else:
+        torch.mm(dy.t(), x, out=out)
+
+
 def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=None):
     """Forward on compute-dtype tensors; returns (out, saved tuple).
 
@@ -157,19 +174,19 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
 
     # MLP: out = hdn + z W_down^T
     dz = _mm(dout2, w.down)                          # [T, F]
-    _mm(dout2.t(), z, out=g.down)
+    _wgrad(dout2, z, g.down)
     dgu = torch.empty_like(gu)
     K.swiglu_bwd(dz, gu[:, :F], gu[:, F:], dgu[:, :F], dgu[:, F:])
     del dz
     dn2 = _mm(dgu, w.gu)                             # [T, h]
-    _mm(dgu.t(), n2, out=g.gu)
+    _wgrad(dgu, n2, g.gu)
     del dgu
     dh, _ = K.rmsnorm_bwd(dn2, hdn, w.ln2, rstd2, dres=dout2, dw=g.ln2)
     del dn2
 
     # attention: hdn = x + o W_o^T
     do2 = _mm(dh, w.o)                               # [T, Hq d]
-    _mm(dh.t(), o2, out=g.o)
+    _wgrad(dh, o2, g.o)
     q = qkv[:, :spec.q_dim].view(B, S, Hq, d)
     k = qkv[:, spec.q_dim:spec.q_dim + spec.kv_dim].view(B, S, Hkv, d)
     v = qkv[:, spec.q_dim + spec.kv_dim:].view(B, S, Hkv, d)
@@ -185,7 +202,7 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
     cos, sin = rope_tables(S, d, spec.rope_theta, dout.dtype, dout.device, spec.interleaved_rope)
     K.rope_(dq, dk, cos, sin, interleaved=spec.interleaved_rope, inverse=True)
     dn1 = _mm(dqkv, w.qkv)                           # [T, h]
-    _mm(dqkv.t(), n1, out=g.qkv)
+    _wgrad(dqkv, n1, g.qkv)
     del dqkv
     dx, _ = K.rmsnorm_bwd(dn1, x2, w.ln1, rstd1, dres=dh, dw=g.ln1)
     return dx.view(B, S, h)
