@@ -168,7 +168,7 @@ def measure_kernels(dev, spec, S):
     cases = KernelCases(dev, spec, S)
     rows = {}
     spec_of = {
-        "attn_fwd": ("attn_fwd_kernel<bf16,128>", "mfma", 20),
+        "attn_fwd": ("attn_fwd_kernel<bf16,128,full>", "mfma", 20),
         "attn_bwd": ("zk_attn_bwd (prep + attn_bwd_dkdv + attn_bwd_dq)", "mfma", 10),
         "rmsnorm_fwd": ("rmsnorm_fwd_vec<bf16,bf16,128,4>", "hbm", 32),
         "rmsnorm_bwd": ("rmsnorm_bwd_vec<bf16,bf16,256,2,2> + dw reduce", "hbm", 32),
@@ -184,7 +184,7 @@ def measure_kernels(dev, spec, S):
             ach, peak, unit = work / ms / 1e6, HBM_PEAK_GBS, "GB/s"
         rows[name] = {"kernel": kname, "bound": bound, "achieved": round(ach, 1), "peak": peak,
                       "unit": unit, "frac": round(ach / peak, 4), "avg_ms": round(ms, 4),
-                      "work_per_launch": work}
+                      "work_per_launch": work, "traffic": recorded_traffic(kname)}
         del run
         torch.cuda.empty_cache()
     return rows
@@ -215,6 +215,68 @@ def cpu_baseline(spec, S, seed=3):
             "seconds": round(dt, 2)}
 
 
+# kernel-case labels (as in the JSON line) and the rocprofv3 kernel names they cover
+TRAFFIC_CASES = {
+    "attn_fwd": ("attn_fwd_kernel<bf16,128,full>", ("attn_fwd_kernel",)),
+    "attn_bwd": ("zk_attn_bwd (prep + attn_bwd_dkdv + attn_bwd_dq)",
+                 ("attn_bwd_prep", "attn_bwd_dkdv", "attn_bwd_dq")),
+    "rmsnorm_fwd": ("rmsnorm_fwd_vec<bf16,bf16,128,4>", ("rmsnorm_fwd_vec",)),
+    "rmsnorm_bwd": ("rmsnorm_bwd_vec<bf16,bf16,256,2,2> + dw reduce",
+                    ("rmsnorm_bwd_vec", "rmsnorm_dw_reduce")),
+    "adamw": ("adamw_vec8<bf16,bf16,true>", ("adamw_vec8",)),
+}
+
+
+def summarize_traffic(root: str) -> str:
+    """Markdown summary of rocprofv3 FETCH_SIZE / WRITE_SIZE runs of the kernel
+    cases (``root/<case>_<COUNTER>/r_counter_collection.csv``), calibrated by
+    the 1 GiB device copy of the ``copy`` case; the machine-readable lines are
+    what ``recorded_traffic`` reads."""
+    import csv
+    from zorse_amd.layer import LayerSpec
+
+    def per_dispatch(case, counter, names):
+        vals = {}
+        path = os.path.join(root, f"{case}_{counter}", "r_counter_collection.csv")
+        for r in csv.DictReader(open(path)):
+            if any(n in r["Kernel_Name"] for n in names):
+                key = (r["Kernel_Name"], r["Dispatch_Id"])
+                vals[key] = vals.get(key, 0.0) + float(r["Counter_Value"])
+        by_kernel = {}
+        for (k, _), v in vals.items():
+            by_kernel.setdefault(k, []).append(v)
+        # one launch of the case = one dispatch of each of its kernels (the mean)
+        return sum(sum(v) / len(v) for v in by_kernel.values())
+
+    copy_fetch = per_dispatch("copy", "FETCH_SIZE", ("copyBuffer",))
+    copy_write = per_dispatch("copy", "WRITE_SIZE", ("copyBuffer",))
+    gib_kib = float(1 << 20)
+    f_fac, w_fac = gib_kib / copy_fetch, gib_kib / copy_write
+    from zorse_amd import flops
+    spec = LayerSpec(hidden=4096, heads=32, kv_heads=32, head_dim=128, ffn=11008)
+    T, h, H, d = 4096, spec.hidden, spec.heads, spec.head_dim
+    algo = {"attn_fwd": flops.attn_fwd_bytes(1, T, H, H, d),
+            "attn_bwd": flops.attn_bwd_bytes(1, T, H, H, d),
+            "rmsnorm_fwd": flops.rmsnorm_fwd_bytes(T, h),
+            "rmsnorm_bwd": flops.rmsnorm_bwd_bytes(T, h),
+            "adamw": flops.adamw_bytes(spec.numel, 2, True)}
+    lines = ["| kernel | FETCH_SIZE (MiB) | WRITE_SIZE (MiB) | HBM traffic (MB) | "
+             "algorithmic bytes (MB) | traffic / algorithmic |", "|---|---|---|---|---|---|"]
+    machine = []
+    for case, (label, names) in TRAFFIC_CASES.items():
+        fk = per_dispatch(case, "FETCH_SIZE", names)
+        wk = per_dispatch(case, "WRITE_SIZE", names)
+        traffic = (fk * f_fac + wk * w_fac) * 1024
+        a = algo[case]
+        lines.append(f"| `{label}` | {fk / 1024:.1f} | {wk / 1024:.1f} | {traffic / 1e6:.1f} | "
+                     f"{a / 1e6:.1f} | {traffic / a:.3f} |")
+        machine.append(f"traffic_bytes_per_launch {label} {int(round(traffic))}")
+    head = (f"Calibration (case `copy`: 1 GiB read + 1 GiB written by one device copy): "
+            f"HBM bytes = FETCH_SIZE x {f_fac:.3f} + WRITE_SIZE x {w_fac:.3f} (KiB per dispatch).")
+    return "\n".join([head, ""] + lines + ["", "Machine-readable (read by bench.py for the "
+                                                "`traffic` fields):", ""] + machine) + "\n"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -227,7 +289,13 @@ def main():
                     help="launch only this kernel case --steps times (for rocprofv3 --pmc)")
     ap.add_argument("--default-gemm", action="store_true",
                     help="use hipBLASLt's default solution heuristic instead of the recorded table")
+    ap.add_argument("--summarize-traffic", metavar="DIR",
+                    help="print the HBM-traffic table from rocprofv3 --pmc runs of the kernel "
+                         "cases under DIR and exit (no GPU needed)")
     args = ap.parse_args()
+    if args.summarize_traffic:
+        print(summarize_traffic(args.summarize_traffic), end="")
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(collectives and sharding are out of scope); run with --gpus 1", file=sys.stderr)
@@ -309,15 +377,16 @@ def main():
                    "layer_fwd_bwd_tflops": round(layer_tflops, 1)},
         "roofline": {"bound": a["bound"], "achieved": a["achieved"], "peak": a["peak"],
                      "unit": a["unit"], "frac": a["frac"],
-                     "traffic": recorded_traffic("adamw_vec8<bf16,bf16,true>"),
+                     "traffic": a["traffic"],
                      "kernel": a["kernel"], "avg_ms": a["avg_ms"],
                      "algorithmic_bytes": a["work_per_launch"]},
         "attention_roofline": {
             "fwd": {"kernel": af["kernel"], "achieved": af["achieved"], "peak": af["peak"],
                     "unit": "TFLOP/s", "frac": af["frac"], "avg_ms": af["avg_ms"],
-                    "traffic": recorded_traffic("attn_fwd_kernel<bf16,128>")},
+                    "traffic": af["traffic"]},
             "bwd": {"kernel": ab["kernel"], "achieved": ab["achieved"], "peak": ab["peak"],
-                    "unit": "TFLOP/s", "frac": ab["frac"], "avg_ms": ab["avg_ms"]}},
+                    "unit": "TFLOP/s", "frac": ab["frac"], "avg_ms": ab["avg_ms"],
+                    "traffic": ab["traffic"]}},
         "kernels": kern,
         "cpu_baseline": cpu,
     }

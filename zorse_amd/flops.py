@@ -64,3 +64,17 @@ def rmsnorm_bwd_bytes(T, h, e=2) -> int:
 
 def adamw_bytes(n, grad_bytes=4, lowp_copy=False) -> int:
     return n * (24 + grad_bytes + (2 if lowp_copy else 0))
+
+
+def attn_fwd_bytes(B, S, Hq, Hkv, d, e=2) -> int:
+    """Compulsory HBM bytes of the attention forward: read Q, K, V, write O
+    (storage type, e bytes) and the fp32 LSE."""
+    return e * B * S * d * (2 * Hq + 2 * Hkv) + 4 * B * Hq * S
+
+
+def attn_bwd_bytes(B, S, Hq, Hkv, d, e=2) -> int:
+    """Compulsory HBM bytes of the attention backward: read Q, K, V, O, dO and
+    the LSE, write dQ, dK, dV, plus the fp32 delta / log2-LSE workspace
+    (written once, read by both gradient kernels)."""
+    return e * B * S * d * (3 * Hq + 2 * Hkv) + e * B * S * d * (Hq + 2 * Hkv) \
+        + 4 * B * Hq * S + 2 * 3 * 4 * B * Hq * S
