@@ -102,6 +102,22 @@ int zk_swiglu_bwd(const void* dz, int64_t ld_dz, const void* gate,
                   int64_t ld_out, int64_t rows, int64_t cols, int dtype,
                   zk_stream_t stream);
 
+/* The same two passes with a transposed copy of the result, for the
+ * token-contiguous weight-gradient GEMMs that follow (down_proj's
+ * grad_weight = grad_output^T @ z and gate/up's = grad^T @ x, the nn.Linear
+ * backward of the LlamaMLP built at models/llama_simple.py:418): besides z the forward
+ * writes zt[c][r] = z[r][c] (row stride ld_zt >= rows); besides dgate / dup
+ * the backward writes dgate_t[c][r] and dup_t[c][r] (row stride ld_t).
+ * 2-byte dtypes; rows, cols and every leading dimension multiples of 8;
+ * operands 16-byte aligned (ZK_EUNSUPPORTED / ZK_EALIGN otherwise). */
+int zk_swiglu_fwd_t(const void* gate, const void* up, int64_t ld_in, void* z,
+                    int64_t ld_z, void* zt, int64_t ld_zt, int64_t rows,
+                    int64_t cols, int dtype, zk_stream_t stream);
+int zk_swiglu_bwd_t(const void* dz, int64_t ld_dz, const void* gate,
+                    const void* up, int64_t ld_in, void* dgate, void* dup,
+                    int64_t ld_out, void* dgate_t, void* dup_t, int64_t ld_t,
+                    int64_t rows, int64_t cols, int dtype, zk_stream_t stream);
+
 /* ------------------------------------------------------------------- RoPE --
  * Replaces apply_rotary_pos_emb / rotate_half (models/llama_simple.py:27-58,
  * HF-style half-split pairing, per-op rounding in the act dtype) and

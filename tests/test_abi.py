@@ -79,6 +79,12 @@ def test_validation_codes(lib):
     assert lib.zk_transpose(p, 8, q, 4, 8, 8, 2, None) == -1
     assert lib.zk_transpose(p, 8, p, 8, 8, 8, 2, None) == -1
     assert lib.zk_transpose(None, 8, None, 8, 0, 8, 2, None) == 0
+    # swiglu with transposed outputs: fp32, rows not a multiple of 8, misaligned
+    assert lib.zk_swiglu_fwd_t(p, p, 16, p, 8, p, 16, 16, 8, 0, None) == -2
+    assert lib.zk_swiglu_fwd_t(p, p, 16, p, 8, p, 16, 12, 8, 2, None) == -4
+    assert lib.zk_swiglu_fwd_t(ctypes.c_void_p(24), p, 16, p, 8, p, 16, 16, 8, 2, None) == -3
+    assert lib.zk_swiglu_bwd_t(p, 8, p, p, 16, p, p, 16, p, p, 4, 16, 8, 2, None) == -1
+    assert lib.zk_swiglu_bwd_t(p, 16, p, p, 16, p, p, 16, p, p, 16, 16, 12, 1, None) == -4
 
 
 def test_wrappers_reject_cpu_tensors():

@@ -91,6 +91,28 @@ def test_swiglu_fwd_bwd(dev, rows, cols, dtype):
     assert_close(dgu[:, cols:], rdu, dtype, "du")
 
 
+@pytest.mark.parametrize("rows,cols", [(4096, 11008), (72, 200), (64, 64), (8, 8)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_swiglu_transposed_outputs(dev, rows, cols, dtype):
+    """zk_swiglu_fwd_t / zk_swiglu_bwd_t: the row-major outputs are bit-equal
+    to zk_swiglu_fwd / zk_swiglu_bwd and the transposed copies are exact
+    transposes (full tiles, ragged 64-tiles, the smallest shape)."""
+    from zorse_amd import kernels as K
+    print(f"swiglu_t rows={rows} cols={cols} {dtype}", flush=True)
+    gu = _rand((rows, 2 * cols), dtype, 63, 2.0).to(dev)
+    dz = _rand((rows, cols), dtype, 64).to(dev)
+    g, u = gu[:, :cols], gu[:, cols:]
+    z, zt = K.swiglu_fwd_t(g, u)
+    assert torch.equal(z, K.swiglu_fwd(g, u))
+    assert torch.equal(zt, z.t())
+    dgu, ref = torch.empty_like(gu), torch.empty_like(gu)
+    dgut = torch.full((2 * cols, rows), float("nan"), dtype=dtype, device=dev)
+    K.swiglu_bwd_t(dz, g, u, dgu[:, :cols], dgu[:, cols:], dgut[:cols], dgut[cols:])
+    K.swiglu_bwd(dz, g, u, ref[:, :cols], ref[:, cols:])
+    assert torch.equal(dgu, ref)
+    assert torch.equal(dgut, dgu.t())
+
+
 # ------------------------------------------------------------------- RoPE --
 
 @pytest.mark.parametrize("d,theta", [(64, 5e5), (128, 1e4), (128, 1e6)])

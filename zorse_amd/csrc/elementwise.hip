@@ -5,6 +5,8 @@
 // rounding points follow the reference's bf16/fp16 op sequence, silu(g)
 // rounded to the storage type before the product, so that the fused kernel
 // reproduces what torch computes op by op.
+#include <initializer_list>
+
 #include "vec.h"
 
 namespace zk {
@@ -50,6 +52,115 @@ __global__ __launch_bounds__(256) void swiglu_bwd_vec(
     Vec8<T>::store(dgate + r * ld_out + c, dg);
     Vec8<T>::store(dup + r * ld_out + c, du);
   }
+}
+
+// SwiGLU with a transposed copy of its output (2-byte types).  The weight
+// gradient of the projection that consumes the output reduces over tokens, and
+// the GEMM is fastest with both operands token-contiguous, so the producer
+// writes out^T [cols, rows] next to out [rows, cols]: the transposed copy costs
+// one extra write instead of a separate read + write pass.
+//
+// A workgroup owns a 64-token x 64-column tile: 16-byte loads (8 columns per
+// thread, 2 chunks per thread), the row-major result stored directly, then
+// the tile is staged in LDS (row pitch 66 elements, so that the column reads
+// of the transpose spread over the banks) and written back as 64
+// rows of 64 tokens with 16-byte stores.  Requires rows % 8 == 0 and
+// cols % 8 == 0; partial tiles at the edges are masked per 8-element chunk.
+template <typename T>
+struct TTile {
+  static constexpr int R = 64, C = 64, P = C + 2;  // tile rows (tokens), cols, LDS pitch
+};
+
+// Writes the LDS tile (row-major, pitch P, R x C) transposed: out^T[c][r0 + r].
+template <typename T>
+__device__ __forceinline__ void store_tile_t(const T (*tile)[TTile<T>::P], T* __restrict__ out_t,
+                                             int64_t ld_t, int64_t r0, int64_t c0, int64_t rows,
+                                             int64_t cols) {
+  constexpr int R = TTile<T>::R;
+  // thread -> (column cc, 8-token chunk rr): 64 columns x 8 chunks = 512 items
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int item = it * 256 + threadIdx.x;
+    const int cc = item / (R / 8), rr = (item % (R / 8)) * 8;
+    if (c0 + cc < cols && r0 + rr < rows) {
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = to_f32(tile[rr + e][cc]);
+      Vec8<T>::store(out_t + (c0 + cc) * ld_t + r0 + rr, v);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_fwd_t(
+    const T* __restrict__ gate, const T* __restrict__ up, int64_t ld_in, T* __restrict__ z,
+    int64_t ld_z, T* __restrict__ zt, int64_t ld_zt, int64_t rows, int64_t cols) {
+  typedef TTile<T> TT;
+  __shared__ T tile[TT::R][TT::P];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * TT::R;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * TT::C;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int item = it * 256 + threadIdx.x;          // 64 rows x 8 chunks
+    const int rr = item / (TT::C / 8), cc = (item % (TT::C / 8)) * 8;
+    const int64_t r = r0 + rr, c = c0 + cc;
+    if (r < rows && c < cols) {
+      float g[8], u[8], o[8];
+      Vec8<T>::load(gate + r * ld_in + c, g);
+      Vec8<T>::load(up + r * ld_in + c, u);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = round_to<T>(silu_f(g[i])) * u[i];
+      Vec8<T>::store(z + r * ld_z + c, o);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) tile[rr][cc + i] = static_cast<T>(o[i]);
+    }
+  }
+  __syncthreads();
+  store_tile_t<T>(tile, zt, ld_zt, r0, c0, rows, cols);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_bwd_t(
+    const T* __restrict__ dz, int64_t ld_dz, const T* __restrict__ gate,
+    const T* __restrict__ up, int64_t ld_in, T* __restrict__ dgate, T* __restrict__ dup,
+    int64_t ld_out, T* __restrict__ dgate_t, T* __restrict__ dup_t, int64_t ld_t, int64_t rows,
+    int64_t cols) {
+  typedef TTile<T> TT;
+  __shared__ T tg[TT::R][TT::P];
+  __shared__ T tu[TT::R][TT::P];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * TT::R;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * TT::C;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int item = it * 256 + threadIdx.x;
+    const int rr = item / (TT::C / 8), cc = (item % (TT::C / 8)) * 8;
+    const int64_t r = r0 + rr, c = c0 + cc;
+    if (r < rows && c < cols) {
+      float d[8], g[8], u[8], dg[8], du[8];
+      Vec8<T>::load(dz + r * ld_dz + c, d);
+      Vec8<T>::load(gate + r * ld_in + c, g);
+      Vec8<T>::load(up + r * ld_in + c, u);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float den = 1.0f + expf(-g[i]);
+        const float sg = 1.0f / den;
+        const float sv = round_to<T>(g[i] / den);
+        du[i] = d[i] * sv;
+        const float ds = round_to<T>(d[i] * u[i]);
+        dg[i] = ds * sg * (1.0f + g[i] * (1.0f - sg));
+      }
+      Vec8<T>::store(dgate + r * ld_out + c, dg);
+      Vec8<T>::store(dup + r * ld_out + c, du);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        tg[rr][cc + i] = static_cast<T>(dg[i]);
+        tu[rr][cc + i] = static_cast<T>(du[i]);
+      }
+    }
+  }
+  __syncthreads();
+  store_tile_t<T>(tg, dgate_t, ld_t, r0, c0, rows, cols);
+  store_tile_t<T>(tu, dup_t, ld_t, r0, c0, rows, cols);
 }
 
 // Scalar fallbacks (any width / alignment).
@@ -201,6 +312,71 @@ extern "C" int zk_swiglu_bwd(const void* dz, int64_t ld_dz, const void* gate,
     hipLaunchKernelGGL(swiglu_bwd_scalar, dim3(grid_for(rows * cols)), dim3(256), 0, s, dz, ld_dz, gate, up, ld_in, dgate, dup, ld_out, rows, cols, dtype);
   }
   return launch_status("zk_swiglu_bwd");
+}
+
+// Shared checks of the transposed-output variants: 2-byte type, 16-byte
+// aligned operands, rows / cols / leading dimensions multiples of 8, grid in range.
+static int check_t_args(const char* who, int dtype, int64_t rows, int64_t cols,
+                        std::initializer_list<int64_t> lds,
+                        std::initializer_list<const void*> ptrs) {
+  ZK_REQUIRE(dtype == ZK_BF16 || dtype == ZK_F16, ZK_EDTYPE,
+             "%s: 2-byte dtypes only (got %d)", who, dtype);
+  ZK_REQUIRE(rows >= 0 && cols >= 0, ZK_EINVAL, "%s: bad shape", who);
+  ZK_REQUIRE(rows % 8 == 0 && cols % 8 == 0, ZK_EUNSUPPORTED,
+             "%s: rows and cols must be multiples of 8 (got %lld, %lld)", who,
+             (long long)rows, (long long)cols);
+  for (int64_t ld : lds)
+    ZK_REQUIRE(ld % 8 == 0, ZK_EALIGN, "%s: leading dimensions must be multiples of 8", who);
+  for (const void* p : ptrs) {
+    ZK_REQUIRE(p != nullptr, ZK_EINVAL, "%s: null pointer", who);
+    ZK_REQUIRE(aligned(p, 16), ZK_EALIGN, "%s: operands must be 16-byte aligned", who);
+  }
+  ZK_REQUIRE((rows + 63) / 64 < 65536 && (cols + 63) / 64 < 0x7fffffffLL, ZK_EINVAL,
+             "%s: grid too large", who);
+  return ZK_OK;
+}
+
+extern "C" int zk_swiglu_fwd_t(const void* gate, const void* up, int64_t ld_in, void* z,
+                               int64_t ld_z, void* zt, int64_t ld_zt, int64_t rows,
+                               int64_t cols, int dtype, zk_stream_t stream) {
+  ZK_REQUIRE(ld_in >= cols && ld_z >= cols && ld_zt >= rows, ZK_EINVAL,
+             "zk_swiglu_fwd_t: bad leading dimension");
+  if (rows == 0 || cols == 0) return ZK_OK;
+  int rc = check_t_args("zk_swiglu_fwd_t", dtype, rows, cols, {ld_in, ld_z, ld_zt},
+                        {gate, up, z, zt});
+  if (rc != ZK_OK) return rc;
+  hipStream_t s = as_stream(stream);
+  const dim3 grid(static_cast<unsigned>((cols + 63) / 64), static_cast<unsigned>((rows + 63) / 64));
+  if (dtype == ZK_BF16)
+    hipLaunchKernelGGL(swiglu_fwd_t<bf16>, grid, dim3(256), 0, s, (const bf16*)gate,
+                       (const bf16*)up, ld_in, (bf16*)z, ld_z, (bf16*)zt, ld_zt, rows, cols);
+  else
+    hipLaunchKernelGGL(swiglu_fwd_t<f16>, grid, dim3(256), 0, s, (const f16*)gate,
+                       (const f16*)up, ld_in, (f16*)z, ld_z, (f16*)zt, ld_zt, rows, cols);
+  return launch_status("zk_swiglu_fwd_t");
+}
+
+extern "C" int zk_swiglu_bwd_t(const void* dz, int64_t ld_dz, const void* gate,
+                               const void* up, int64_t ld_in, void* dgate, void* dup,
+                               int64_t ld_out, void* dgate_t, void* dup_t, int64_t ld_t,
+                               int64_t rows, int64_t cols, int dtype, zk_stream_t stream) {
+  ZK_REQUIRE(ld_in >= cols && ld_dz >= cols && ld_out >= cols && ld_t >= rows, ZK_EINVAL,
+             "zk_swiglu_bwd_t: bad leading dimension");
+  if (rows == 0 || cols == 0) return ZK_OK;
+  int rc = check_t_args("zk_swiglu_bwd_t", dtype, rows, cols, {ld_dz, ld_in, ld_out, ld_t},
+                        {dz, gate, up, dgate, dup, dgate_t, dup_t});
+  if (rc != ZK_OK) return rc;
+  hipStream_t s = as_stream(stream);
+  const dim3 grid(static_cast<unsigned>((cols + 63) / 64), static_cast<unsigned>((rows + 63) / 64));
+  if (dtype == ZK_BF16)
+    hipLaunchKernelGGL(swiglu_bwd_t<bf16>, grid, dim3(256), 0, s, (const bf16*)dz, ld_dz,
+                       (const bf16*)gate, (const bf16*)up, ld_in, (bf16*)dgate, (bf16*)dup,
+                       ld_out, (bf16*)dgate_t, (bf16*)dup_t, ld_t, rows, cols);
+  else
+    hipLaunchKernelGGL(swiglu_bwd_t<f16>, grid, dim3(256), 0, s, (const f16*)dz, ld_dz,
+                       (const f16*)gate, (const f16*)up, ld_in, (f16*)dgate, (f16*)dup,
+                       ld_out, (f16*)dgate_t, (f16*)dup_t, ld_t, rows, cols);
+  return launch_status("zk_swiglu_bwd_t");
 }
 
 extern "C" int zk_cast(const void* x, int x_dtype, void* y, int y_dtype,

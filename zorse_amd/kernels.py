@@ -176,6 +176,51 @@ def swiglu_bwd(dz: torch.Tensor, gate: torch.Tensor, up: torch.Tensor,
                               stream_handle(dev)), "zk_swiglu_bwd")
 
 
+def swiglu_fwd_t(gate: torch.Tensor, up: torch.Tensor):
+    """(z, z^T): the SwiGLU output and its transpose [cols, rows] from one pass
+    (2-byte dtypes, rows and cols multiples of 8)."""
+    dev = _require_gpu(gate, up)
+    if gate.shape != up.shape or gate.dtype != up.dtype:
+        raise ValueError("gate and up must match")
+    ld = _row_view_check("gate", gate)
+    if _row_view_check("up", up) != ld:
+        raise ValueError("gate and up must share a row stride")
+    rows, cols = gate.shape
+    z = torch.empty(rows, cols, device=dev, dtype=gate.dtype)
+    zt = torch.empty(cols, rows, device=dev, dtype=gate.dtype)
+    check(lib().zk_swiglu_fwd_t(ptr(gate), ptr(up), ld, ptr(z), cols, ptr(zt), rows, rows, cols,
+                                dtype_code(gate.dtype), stream_handle(dev)), "zk_swiglu_fwd_t")
+    return z, zt
+
+
+def swiglu_bwd_t(dz: torch.Tensor, gate: torch.Tensor, up: torch.Tensor,
+                 dgate: torch.Tensor, dup: torch.Tensor, dgate_t: torch.Tensor,
+                 dup_t: torch.Tensor) -> None:
+    """swiglu_bwd that also writes dgate^T / dup^T ([cols, rows] views sharing
+    a row stride; 2-byte dtypes, rows and cols multiples of 8)."""
+    dev = _require_gpu(dz, gate, up, dgate, dup, dgate_t, dup_t)
+    ld_in = _row_view_check("gate", gate)
+    if _row_view_check("up", up) != ld_in:
+        raise ValueError("gate and up must share a row stride")
+    ld_out = _row_view_check("dgate", dgate)
+    if _row_view_check("dup", dup) != ld_out:
+        raise ValueError("dgate and dup must share a row stride")
+    ld_t = _row_view_check("dgate_t", dgate_t)
+    if _row_view_check("dup_t", dup_t) != ld_t:
+        raise ValueError("dgate_t and dup_t must share a row stride")
+    ld_dz = _row_view_check("dz", dz)
+    rows, cols = gate.shape
+    for t in (dz, up, dgate, dup):
+        if t.shape != (rows, cols) or t.dtype != gate.dtype:
+            raise ValueError("swiglu_bwd_t operands must match gate")
+    for t in (dgate_t, dup_t):
+        if t.shape != (cols, rows) or t.dtype != gate.dtype:
+            raise ValueError("transposed outputs must be (cols, rows) of gate's dtype")
+    check(lib().zk_swiglu_bwd_t(ptr(dz), ld_dz, ptr(gate), ptr(up), ld_in, ptr(dgate), ptr(dup),
+                                ld_out, ptr(dgate_t), ptr(dup_t), ld_t, rows, cols,
+                                dtype_code(gate.dtype), stream_handle(dev)), "zk_swiglu_bwd_t")
+
+
 # ------------------------------------------------------------------- RoPE --
 
 def rope_(q: torch.Tensor, k: torch.Tensor | None, cos: torch.Tensor, sin: torch.Tensor,

@@ -109,17 +109,27 @@ def _transposing(t):
     return t.dtype in (torch.bfloat16, torch.float16) and t.shape[0] >= _TRANSPOSE_MIN_TOKENS
 
 
-def _wgrad(dy, x, out):
+def _wgrad(dy, x, out, dyt=None, xt=None):
     """out = dy^T x (the weight gradient of y = x W^T).  For 2-byte types and
-    long token counts dy^T and x^T are materialised first (zk_transpose) so
-    that the GEMM streams both operands along the token reduction."""
+    long token counts dy^T and x^T are materialised first (zk_transpose, or
+    supplied by the kernel that produced them) so that the GEMM streams both
+    operands along the token reduction.  ``x`` may be None when ``xt`` is given."""
     if _transposing(dy):
-        dyt = K.transpose(dy)
-        xt = K.transpose(x)
+        if dyt is None:
+            dyt = K.transpose(dy)
+        if xt is None:
+            xt = K.transpose(x)
         torch.mm(dyt, xt.t(), out=out)
         del dyt, xt
     else:
         torch.mm(dy.t(), x, out=out)
+
+
+def _swiglu_transposed(gu, F):
+    """True when the SwiGLU kernels also write the transposed copies the MLP's
+    weight gradients use (token-contiguous operands, 2-byte types; the fused
+    kernels need rows and columns in multiples of 8)."""
+    return _transposing(gu) and gu.shape[0] % 8 == 0 and F % 8 == 0
 
 
 def _dgrad(dy, wmat, transpose_weight):
@@ -166,9 +176,15 @@ def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=Non
     n2, rstd2, hdn = K.rmsnorm_fwd(attn_out, w.ln2, spec.eps, residual=x2)
     gu = _mm(n2, w.gu.t())                           # [T, 2F] = gate | up
     F = spec.ffn
-    z = K.swiglu_fwd(gu[:, :F], gu[:, F:])
+    if _swiglu_transposed(gu, F):
+        # z^T is what down_proj's weight gradient reads; z itself is only
+        # needed for the GEMM below
+        z, zs = K.swiglu_fwd_t(gu[:, :F], gu[:, F:])
+    else:
+        z = zs = K.swiglu_fwd(gu[:, :F], gu[:, F:])
     out = torch.addmm(hdn, z, w.down.t())            # residual + down(z)
-    saved = (x2, n1, rstd1, qkv, o2, lse, hdn, n2, rstd2, gu, z)
+    del z
+    saved = (x2, n1, rstd1, qkv, o2, lse, hdn, n2, rstd2, gu, zs)
     return out.view(B, S, h), saved
 
 
@@ -183,7 +199,7 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
                    grad_flat: torch.Tensor) -> torch.Tensor:
     """Backward of layer_forward; writes weight grads into ``grad_flat``
     (compute dtype, flat layout) and returns dx."""
-    x2, n1, rstd1, qkv, o2, lse, hdn, n2, rstd2, gu, z = saved
+    x2, n1, rstd1, qkv, o2, lse, hdn, n2, rstd2, gu, zs = saved
     T, h = x2.shape
     B = dout.shape[0]
     S = T // B
@@ -193,13 +209,22 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
 
     # MLP: out = hdn + z W_down^T
     dz = _dgrad(dout2, w.down, True)                 # [T, F]
-    _wgrad(dout2, z, g.down)
+    fused_t = _swiglu_transposed(gu, F)
+    if fused_t:                                      # zs = z^T
+        _wgrad(dout2, None, g.down, xt=zs)
+    else:                                            # zs = z
+        _wgrad(dout2, zs, g.down)
     dgu = torch.empty_like(gu)
-    K.swiglu_bwd(dz, gu[:, :F], gu[:, F:], dgu[:, :F], dgu[:, F:])
+    dgut = None
+    if fused_t:
+        dgut = torch.empty(2 * F, T, device=gu.device, dtype=gu.dtype)
+        K.swiglu_bwd_t(dz, gu[:, :F], gu[:, F:], dgu[:, :F], dgu[:, F:], dgut[:F], dgut[F:])
+    else:
+        K.swiglu_bwd(dz, gu[:, :F], gu[:, F:], dgu[:, :F], dgu[:, F:])
     del dz
     dn2 = _dgrad(dgu, w.gu, False)                   # [T, h]
-    _wgrad(dgu, n2, g.gu)
-    del dgu
+    _wgrad(dgu, n2, g.gu, dyt=dgut)
+    del dgu, dgut
     dh, _ = K.rmsnorm_bwd(dn2, hdn, w.ln2, rstd2, dres=dout2, dw=g.ln2)
     del dn2
 
