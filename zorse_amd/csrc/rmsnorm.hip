@@ -6,8 +6,9 @@
 // row: x is read once and y written once, the HBM minimum.  The backward
 // walks rows in groups of kBwdRows with a grid of at most kBwdParts
 // workgroups: the group's dy, h (and residual gradient) loads are all issued
-// before its row reductions, the row sums share one pair of barriers, each
-// thread accumulates the weight gradient of its fixed columns in registers,
+// before its row reductions (for 2-byte rows of up to 4096 elements also the
+// next group's, while this one is processed); the row sums share one pair of
+// barriers, each thread accumulates the weight gradient of its fixed columns in registers,
 // and every workgroup writes one fp32 partial row that a second kernel
 // reduces deterministically (no atomics).  Rows whose width is not a
 // multiple of 8, wider than 8192, or misaligned buffers take the scalar
@@ -135,6 +136,13 @@ __device__ __forceinline__ void block_sum_rows(float (&v)[R], float* red) {
   }
 }
 
+// The rows of one group (dy, h, dres) in packed form plus their rstd.
+template <typename T, int R, int CH, bool kRes>
+struct BwdGroup {
+  Raw8<T> d8[R][CH], h8[R][CH], g8[kRes ? R : 1][CH];
+  float r[R];
+};
+
 template <typename T, typename W, int NT, int R, int CH, bool kRes>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2)))
 void rmsnorm_bwd_vec(
@@ -142,6 +150,7 @@ void rmsnorm_bwd_vec(
     const float* __restrict__ rstd, const T* __restrict__ dres,
     T* __restrict__ dx, float* __restrict__ part, int64_t rows,
     int64_t hidden) {
+  typedef BwdGroup<T, R, CH, kRes> G;
   __shared__ float red[R * (NT / 64)];
   const int nchunk = static_cast<int>(hidden / 8);
   float wv[CH][8], dw[CH][8];
@@ -155,27 +164,29 @@ void rmsnorm_bwd_vec(
     }
     if (ch < nchunk) Vec8<W>::load(w + ch * 8, wv[c]);
   }
-  for (int64_t row0 = static_cast<int64_t>(blockIdx.x) * R; row0 < rows;
-       row0 += static_cast<int64_t>(gridDim.x) * R) {
-    Raw8<T> d8[R][CH], h8[R][CH], g8[kRes ? R : 1][CH];
-    float dot[R], r[R];
+
+  auto load = [&](G& gr, int64_t row0) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < R; ++k) {
       const int64_t row = row0 + k < rows ? row0 + k : rows - 1;
-      r[k] = row0 + k < rows ? rstd[row] : 0.f;  // r = 0: the row contributes nothing
+      gr.r[k] = row0 + k < rows ? rstd[row] : 0.f;  // r = 0: the row contributes nothing
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
         const int ch = threadIdx.x + c * NT;
         if (ch < nchunk) {
-          d8[k][c].load(dy + row * hidden + ch * 8);
-          h8[k][c].load(h + row * hidden + ch * 8);
-          if (kRes) g8[kRes ? k : 0][c].load(dres + row * hidden + ch * 8);
+          gr.d8[k][c].load(dy + row * hidden + ch * 8);
+          gr.h8[k][c].load(h + row * hidden + ch * 8);
+          if (kRes) gr.g8[kRes ? k : 0][c].load(dres + row * hidden + ch * 8);
         } else {
-          d8[k][c].zero();
-          h8[k][c].zero();
+          gr.d8[k][c].zero();
+          gr.h8[k][c].zero();
         }
       }
     }
+  };
+
+  auto process = [&](G& gr, int64_t row0) __attribute__((always_inline)) {
+    float dot[R];
 #pragma unroll
     for (int k = 0; k < R; ++k) {
       dot[k] = 0.f;
@@ -183,9 +194,9 @@ void rmsnorm_bwd_vec(
       for (int c = 0; c < CH; ++c)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float xh = h8[k][c][i] * r[k];
-          dot[k] = fmaf(d8[k][c][i] * wv[c][i], xh, dot[k]);
-          dw[c][i] = fmaf(d8[k][c][i], round_to<T>(xh), dw[c][i]);
+          const float xh = gr.h8[k][c][i] * gr.r[k];
+          dot[k] = fmaf(gr.d8[k][c][i] * wv[c][i], xh, dot[k]);
+          dw[c][i] = fmaf(gr.d8[k][c][i], round_to<T>(xh), dw[c][i]);
         }
     }
     block_sum_rows<NT, R>(dot, red);
@@ -193,8 +204,8 @@ void rmsnorm_bwd_vec(
     for (int k = 0; k < R; ++k)
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
-        d8[k][c].opaque();
-        h8[k][c].opaque();
+        gr.d8[k][c].opaque();
+        gr.h8[k][c].opaque();
       }
 #pragma unroll
     for (int k = 0; k < R; ++k) {
@@ -208,13 +219,41 @@ void rmsnorm_bwd_vec(
           float o[8];
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            const float xh = h8[k][c][i] * r[k];
-            o[i] = r[k] * (d8[k][c][i] * wv[c][i] - xh * mean);
-            if (kRes) o[i] += g8[kRes ? k : 0][c][i];
+            const float xh = gr.h8[k][c][i] * gr.r[k];
+            o[i] = gr.r[k] * (gr.d8[k][c][i] * wv[c][i] - xh * mean);
+            if (kRes) o[i] += gr.g8[kRes ? k : 0][c][i];
           }
           Vec8<T>::store(dx + row * hidden + ch * 8, o);
         }
       }
+    }
+  };
+
+  // Row groups blockIdx.x, + gridDim.x, ...  For 2-byte rows of up to 2
+  // chunks per thread the next group's loads are in flight while the current
+  // one is reduced and written (two buffers, alternated by unrolling the loop
+  // by two); wider rows have no registers for a second buffer.
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * R;
+  int64_t row0 = static_cast<int64_t>(blockIdx.x) * R;
+  if constexpr (CH <= 2 && sizeof(T) == 2) {
+    G ga, gb;
+    if (row0 < rows) load(ga, row0);
+    while (row0 < rows) {
+      int64_t nxt = row0 + stride;
+      if (nxt < rows) load(gb, nxt);
+      process(ga, row0);
+      row0 = nxt;
+      if (row0 >= rows) break;
+      nxt = row0 + stride;
+      if (nxt < rows) load(ga, nxt);
+      process(gb, row0);
+      row0 = nxt;
+    }
+  } else {
+    for (; row0 < rows; row0 += stride) {
+      G ga;
+      load(ga, row0);
+      process(ga, row0);
     }
   }
 #pragma unroll
