@@ -118,6 +118,21 @@ int zk_swiglu_bwd_t(const void* dz, int64_t ld_dz, const void* gate,
                     int64_t ld_out, void* dgate_t, void* dup_t, int64_t ld_t,
                     int64_t rows, int64_t cols, int dtype, zk_stream_t stream);
 
+/* gate|up projection with the SwiGLU epilogue: replaces gate_proj(x),
+ * up_proj(x) and act_fn(gate) * up of HF LlamaMLP.forward (the MLP built at
+ * models/llama_simple.py:418; torchtitan FeedForward.forward,
+ * models/llama_v2.py:319-320) -- two nn.Linear GEMMs and the activation.
+ *     g = x Wg^T, u = x Wu^T (fp32 accumulation, rounded), z = round(round(silu(g)) * u)
+ * x [M, K] (row stride ld_x), w_gate / w_up [F, K] (row stride ld_w; the two
+ * halves of the flat gate|up weight), g_out / u_out [M, F] (shared row stride
+ * ld_gu: the halves of one [M, 2F] buffer kept for the backward), z [M, F]
+ * (ld_z), optional zt [F, M] = z^T (ld_zt; NULL to skip).  2-byte dtypes,
+ * K a multiple of 64, M and F multiples of 8, 16-byte aligned operands. */
+int zk_gemm_swiglu(const void* x, int64_t ld_x, const void* w_gate,
+                   const void* w_up, int64_t ld_w, void* g_out, void* u_out,
+                   int64_t ld_gu, void* z, int64_t ld_z, void* zt, int64_t ld_zt,
+                   int64_t M, int64_t F, int64_t K, int dtype, zk_stream_t stream);
+
 /* ------------------------------------------------------------------- RoPE --
  * Replaces apply_rotary_pos_emb / rotate_half (models/llama_simple.py:27-58,
  * HF-style half-split pairing, per-op rounding in the act dtype) and

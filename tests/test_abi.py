@@ -85,6 +85,12 @@ def test_validation_codes(lib):
     assert lib.zk_swiglu_fwd_t(ctypes.c_void_p(24), p, 16, p, 8, p, 16, 16, 8, 2, None) == -3
     assert lib.zk_swiglu_bwd_t(p, 8, p, p, 16, p, p, 16, p, p, 4, 16, 8, 2, None) == -1
     assert lib.zk_swiglu_bwd_t(p, 16, p, p, 16, p, p, 16, p, p, 16, 16, 12, 1, None) == -4
+    # gemm_swiglu: fp32, K not a multiple of 64, misaligned x, ld_x < K
+    assert lib.zk_gemm_swiglu(p, 64, p, p, 64, p, p, 8, p, 8, None, 0, 8, 8, 64, 0, None) == -2
+    assert lib.zk_gemm_swiglu(p, 64, p, p, 64, p, p, 8, p, 8, None, 0, 8, 8, 32, 2, None) == -4
+    assert lib.zk_gemm_swiglu(ctypes.c_void_p(24), 64, p, p, 64, p, p, 8, p, 8, None, 0, 8, 8, 64,
+                              2, None) == -3
+    assert lib.zk_gemm_swiglu(p, 32, p, p, 64, p, p, 8, p, 8, None, 0, 8, 8, 64, 2, None) == -1
 
 
 def test_wrappers_reject_cpu_tensors():

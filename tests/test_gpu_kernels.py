@@ -113,6 +113,41 @@ def test_swiglu_transposed_outputs(dev, rows, cols, dtype):
     assert torch.equal(dgut, dgu.t())
 
 
+@pytest.mark.parametrize("M,F,K,dtype", [(200, 72, 128, torch.bfloat16), (136, 200, 192, torch.float16),
+                                          (8, 8, 64, torch.bfloat16), (1024, 704, 512, torch.bfloat16)])
+def test_gemm_swiglu(dev, M, F, K, dtype):
+    """zk_gemm_swiglu (gate|up GEMM + SwiGLU epilogue) vs the fp64 oracle on
+    the same rounded inputs: g, u within the bf16/fp16 bar, z bit-equal to the
+    SwiGLU kernel applied to the returned g, u, z^T an exact transpose; ragged
+    128 x 64 tiles and both dtypes."""
+    from zorse_amd import kernels as K_
+    print(f"gemm_swiglu M={M} F={F} K={K} {dtype}", flush=True)
+    x = _rand((M, K), dtype, 71)
+    w = _rand((2 * F, K), dtype, 72, 0.05)
+    xd, wd = x.to(dev), w.to(dev)
+    gu, z, zt = K_.gemm_swiglu(xd, wd[:F], wd[F:], transposed=True)
+    ref = x.double() @ w.double().t()
+    assert_close(gu[:, :F], ref[:, :F], dtype, "g")
+    assert_close(gu[:, F:], ref[:, F:], dtype, "u")
+    assert_close(z, O.swiglu(ref[:, :F].to(dtype).double(), ref[:, F:].to(dtype).double()), dtype, "z")
+    assert torch.equal(z, K_.swiglu_fwd(gu[:, :F], gu[:, F:]))
+    assert torch.equal(zt, z.t())
+
+
+def test_gemm_swiglu_llama7b_shape(dev):
+    """The 7B layer shape (4096 tokens, F = 11008, K = 4096) against a plain
+    PyTorch fp32 GEMM of the same rounded inputs; the epilogue as above."""
+    from zorse_amd import kernels as K_
+    M, F, K = 4096, 11008, 4096
+    g = torch.Generator(device="cpu").manual_seed(73)
+    x = torch.randn(M, K, generator=g).to(dev, torch.bfloat16)
+    w = (0.02 * torch.randn(2 * F, K, generator=g)).to(dev, torch.bfloat16)
+    gu, z = K_.gemm_swiglu(x, w[:F], w[F:])
+    ref = torch.mm(x.float(), w.float().t())
+    assert_close(gu, ref, torch.bfloat16, "gu")
+    assert torch.equal(z, K_.swiglu_fwd(gu[:, :F], gu[:, F:]))
+
+
 # ------------------------------------------------------------------- RoPE --
 
 @pytest.mark.parametrize("d,theta", [(64, 5e5), (128, 1e4), (128, 1e6)])

@@ -72,6 +72,8 @@ SIGNATURES = {
     "zk_swiglu_fwd": (_int, [_ptr, _ptr, _i64, _ptr, _i64, _i64, _i64, _int, _ptr]),
     "zk_swiglu_bwd": (_int, [_ptr, _i64, _ptr, _ptr, _i64, _ptr, _ptr, _i64,
                              _i64, _i64, _int, _ptr]),
+    "zk_gemm_swiglu": (_int, [_ptr, _i64, _ptr, _ptr, _i64, _ptr, _ptr, _i64, _ptr, _i64, _ptr,
+                               _i64, _i64, _i64, _i64, _int, _ptr]),
     "zk_swiglu_fwd_t": (_int, [_ptr, _ptr, _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _int,
                                 _ptr]),
     "zk_swiglu_bwd_t": (_int, [_ptr, _i64, _ptr, _ptr, _i64, _ptr, _ptr, _i64, _ptr, _ptr,

@@ -176,6 +176,36 @@ def swiglu_bwd(dz: torch.Tensor, gate: torch.Tensor, up: torch.Tensor,
                               stream_handle(dev)), "zk_swiglu_bwd")
 
 
+def gemm_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
+                gu_out: torch.Tensor | None = None, transposed: bool = False):
+    """(gu, z[, z^T]) with gu = [x Wg^T | x Wu^T] ([M, 2F], kept for the
+    backward) and z = SwiGLU(g, u), from one hand-written GEMM with the
+    activation in its epilogue.  x [M, K], w_gate / w_up [F, K] with unit
+    column stride; 2-byte dtypes, K % 64 == 0, M and F multiples of 8."""
+    dev = _require_gpu(x, w_gate, w_up, gu_out)
+    if x.dim() != 2 or w_gate.dim() != 2 or w_gate.shape != w_up.shape:
+        raise ValueError("gemm_swiglu: x [M, K] and two [F, K] weights expected")
+    M, K = x.shape
+    F = w_gate.shape[0]
+    if w_gate.shape[1] != K or x.dtype != w_gate.dtype or w_up.dtype != x.dtype:
+        raise ValueError("gemm_swiglu: operands must share K and dtype")
+    ld_x = _row_view_check("x", x)
+    ld_w = _row_view_check("w_gate", w_gate)
+    if _row_view_check("w_up", w_up) != ld_w:
+        raise ValueError("w_gate and w_up must share a row stride")
+    if gu_out is None:
+        gu_out = torch.empty(M, 2 * F, device=dev, dtype=x.dtype)
+    if gu_out.shape != (M, 2 * F) or gu_out.dtype != x.dtype or gu_out.stride(1) != 1:
+        raise ValueError("gu_out must be [M, 2F] with unit column stride")
+    z = torch.empty(M, F, device=dev, dtype=x.dtype)
+    zt = torch.empty(F, M, device=dev, dtype=x.dtype) if transposed else None
+    check(lib().zk_gemm_swiglu(ptr(x), ld_x, ptr(w_gate), ptr(w_up), ld_w, ptr(gu_out),
+                               ptr(gu_out[:, F:]), gu_out.stride(0), ptr(z), F,
+                               ptr(zt) if zt is not None else None, M, M, F, K,
+                               dtype_code(x.dtype), stream_handle(dev)), "zk_gemm_swiglu")
+    return (gu_out, z, zt) if transposed else (gu_out, z)
+
+
 def swiglu_fwd_t(gate: torch.Tensor, up: torch.Tensor):
     """(z, z^T): the SwiGLU output and its transpose [cols, rows] from one pass
     (2-byte dtypes, rows and cols multiples of 8)."""
