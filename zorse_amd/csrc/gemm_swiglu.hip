@@ -18,7 +18,7 @@
 // not alias reads of the other).  The epilogue stages g, u, z through the
 // then idle LDS (same swizzle) and writes 16-byte row chunks; the optional
 // transposed copy z^T [F, M] (for down_proj's weight gradient) is written
-// from the same staged tile.  Workgroups are ordered in groups of 8 token
+// from the same staged tile.  Workgroups are ordered in groups of 16 token
 // tiles per feature tile so that the blocks running together share their x
 // and weight rows in the caches.
 #include "attn_common.h"
@@ -30,7 +30,7 @@ struct GemmSwigluCfg {
   static constexpr int BM = 128;  // tokens per workgroup
   static constexpr int BF = 64;   // features per workgroup (g and u each)
   static constexpr int BK = 64;   // reduction step
-  static constexpr int GROUP_M = 8;
+  static constexpr int GROUP_M = 16;
 };
 
 template <typename T>
@@ -106,6 +106,8 @@ void gemm_swiglu_kernel(const T* __restrict__ x, int64_t ld_x, const T* __restri
         accu[mi] = Mm::mma(a[mi], bu, accu[mi]);
       }
     }
+    // the compiler's single-wave MFMA / LDS interleaving strategy
+    __builtin_amdgcn_iglp_opt(1);
   };
 
   const int64_t n_k = K / BK;
