@@ -5,7 +5,8 @@ backward GEMMs) run through torch.mm / torch.addmm, i.e. hipBLASLt.  Its
 default heuristic does not always pick the fastest solution for these shapes
 on gfx950; ``tunableop_gfx950.csv`` records, per GEMM shape, the solution
 PyTorch's TunableOp measured fastest on an MI355X for the Llama-2-7B layer
-(bf16, 4096 tokens).  ``use_tuned_gemms()`` loads that table with tuning
+(bf16, 4096 tokens), tuned with a 1 GiB rotating input buffer so that the
+operands are not cache-resident, as in a stage step.  ``use_tuned_gemms()`` loads that table with tuning
 switched OFF, so nothing is benchmarked at run time; shapes not in the table
 use the library default.  The table is validated by TunableOp against the
 torch / HIP / hipBLASLt versions it was recorded with and ignored on a
