@@ -314,6 +314,35 @@ def test_adamw_kernel_vs_oracle(dev, gdt, n):
     assert torch.equal(lowp.cpu(), p.cpu().to(torch.bfloat16))
 
 
+@pytest.mark.parametrize("rows,cols,gdt,ldt", [(4096, 4096, torch.bfloat16, torch.bfloat16),
+                                              (72, 200, torch.float32, torch.bfloat16),
+                                              (200, 136, torch.float16, torch.float16),
+                                              (8, 8, torch.bfloat16, torch.bfloat16)])
+def test_adamw_step_transposed_copy(dev, rows, cols, gdt, ldt):
+    """zk_adamw_step_t: master, m, v and the compute copy bit-equal to
+    zk_adamw_step on the same inputs, and the transposed copy an exact
+    transpose of the compute copy (full and ragged 64 x 64 tiles)."""
+    from zorse_amd import kernels as K
+    print(f"adamw_t rows={rows} cols={cols} {gdt} -> {ldt}", flush=True)
+    g = torch.Generator().manual_seed(52)
+    n = rows * cols
+    p0 = torch.randn(n, generator=g)
+    m0 = 0.01 * torch.randn(n, generator=g)
+    v0 = 0.001 * torch.rand(n, generator=g)
+    gr = torch.randn(n, generator=g).to(gdt).to(dev)
+    hyper = dict(lr=1e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, step=4)
+    p, m, v = p0.to(dev), m0.to(dev), v0.to(dev)
+    low = torch.empty(n, dtype=ldt, device=dev)
+    K.adamw_step(p, gr, m, v, lowp_out=low, **hyper)
+    pt, mt, vt = p0.to(dev), m0.to(dev), v0.to(dev)
+    lowt = torch.empty(n, dtype=ldt, device=dev)
+    tr = torch.full((cols, rows), float("nan"), dtype=ldt, device=dev)
+    K.adamw_step_t(pt, gr, mt, vt, lowt, tr, rows=rows, cols=cols, **hyper)
+    for a, b, what in ((p, pt, "master"), (m, mt, "m"), (v, vt, "v"), (low, lowt, "copy")):
+        assert torch.equal(a, b), what
+    assert torch.equal(tr, lowt.view(rows, cols).t())
+
+
 def test_fused_adamw_matches_torch_adamw_and_adam(dev):
     from zorse_amd.optim import FusedAdam, FusedAdamW
     g = torch.Generator().manual_seed(51)

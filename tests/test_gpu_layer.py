@@ -251,6 +251,67 @@ def test_stage_runner_optimizer_in_backwards(dev):
         assert layer.flat_param.grad is None
 
 
+def test_stage_transposed_weights(dev):
+    """The optimizer step keeps W^T of the projections next to the bf16 weights
+    (StageRunner(transposed_weights=True)): after each step the copies are
+    exact transposes of the weights; the next backward reads them instead of
+    transposing W_o / W_down (two fewer transposes per layer) and its
+    gradients and updated weights agree with the run without them (only the
+    GEMMs' summation order differs).  1024 tokens, so the backward takes its
+    transposed-operand GEMM path."""
+    from zorse_amd import layer as L
+    from zorse_amd.stage import StageRunner
+    kw = dict(hidden_size=256, num_attention_heads=2, intermediate_size=512, rope_theta=1e4)
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(1, 1024, 256, generator=g).to(dtype).to(dev)
+    dout = torch.randn(1, 1024, 256, generator=g).to(dtype).to(dev)
+    real = L.K.transpose
+    counts = {}
+
+    def counting(*a, **k):
+        counts["n"] = counts.get("n", 0) + 1
+        return real(*a, **k)
+
+    out = {}
+    try:
+        L.K.transpose = counting
+        for use_wt in (False, True):
+            layers = [_layer(kw, dev, param_dtype=dtype, seed=s) for s in (1, 2)]
+            grads = {}
+            for i, l in enumerate(layers):
+                l.flat_param.register_post_accumulate_grad_hook(
+                    lambda p, i=i: grads.__setitem__(i, p.grad.detach().clone()))
+            runner = StageRunner(layers, lr=1e-4, transposed_weights=use_wt)
+            per_step = []
+            for _ in range(2):
+                counts["n"] = 0
+                runner.step(x, dout)
+                runner.wait_optimizer()
+                torch.cuda.synchronize()
+                per_step.append(counts["n"])
+                if use_wt:
+                    for l in layers:
+                        assert l._transposed_weights() is not None
+                        for name, view in (("qkv", l.param_view("q")), ("o", l.param_view("o")),
+                                           ("down", l.param_view("down"))):
+                            if name == "qkv":
+                                a, b = l._offsets["q"][0], l._offsets["v"][1]
+                                view = l.flat_param[a:b].view(-1, 256)
+                            assert torch.equal(l._wt[name], view.t()), name
+                        a, b = l._offsets["gate"][0], l._offsets["up"][1]
+                        assert torch.equal(l._wt["gu"], l.flat_param[a:b].view(-1, 256).t())
+            out[use_wt] = (grads, [l.flat_param.detach().clone() for l in layers], per_step)
+    finally:
+        L.K.transpose = real
+    # step 1 has no copies yet; step 2 uses them: 2 transposes fewer per layer
+    assert out[True][2][0] == out[False][2][0]
+    assert out[True][2][1] == out[False][2][1] - 4
+    for i in (0, 1):
+        assert_close(out[True][0][i], out[False][0][i].double(), dtype, f"layer {i} grad")
+        assert_close(out[True][1][i], out[False][1][i].double(), dtype, f"layer {i} weights")
+
+
 def test_stage_recompute_attention_cache(dev):
     """Recompute mode (the reference pipeline's second forward inside the
     backward, zorse_utils/pipeline_schedule_v2.py:157-200): with the attention

@@ -177,6 +177,82 @@ __global__ __launch_bounds__(256) void adamw_vec8(
   }
 }
 
+// The same update on one row-major [rows, cols] matrix of the shard, also
+// writing the rounded parameter transposed (lowp_t[c][r], row stride ld_t):
+// the compute copy the backward's input-gradient GEMM reads along its
+// reduction.  A workgroup owns a 64 x 64 tile: 16-byte accesses on every
+// stream (rows of 64 elements), the rounded values staged in a padded LDS
+// tile (pitch 66) and written back as 16-byte chunks of 8 consecutive rows.
+// rows and cols are multiples of 8.
+template <typename G, typename L>
+__global__ __launch_bounds__(256) void adamw_tile_t(
+    float* __restrict__ p, const G* __restrict__ g, float* __restrict__ m,
+    float* __restrict__ v, L* __restrict__ lowp, L* __restrict__ lowp_t, int64_t ld_t,
+    int64_t rows, int64_t cols, AdamScalars s) {
+  __shared__ L tile[64][66];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const int tid = threadIdx.x;
+  float4 pa[2][2], ma[2][2], va[2][2];
+  float gv[2][8];
+  bool in[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {  // rows k * 32 + tid / 8, columns 8 (tid % 8)
+    const int r = k * 32 + (tid >> 3), ch = tid & 7;
+    const int64_t gr = r0 + r, gc = c0 + 8 * ch;
+    in[k] = gr < rows && gc < cols;
+    if (in[k]) {
+      const int64_t i = gr * cols + gc;
+      pa[k][0] = *reinterpret_cast<const float4*>(p + i);
+      pa[k][1] = *reinterpret_cast<const float4*>(p + i + 4);
+      ma[k][0] = *reinterpret_cast<const float4*>(m + i);
+      ma[k][1] = *reinterpret_cast<const float4*>(m + i + 4);
+      va[k][0] = *reinterpret_cast<const float4*>(v + i);
+      va[k][1] = *reinterpret_cast<const float4*>(v + i + 4);
+      load_grad8<G>(g, i, gv[k]);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    if (!in[k]) continue;
+    const int r = k * 32 + (tid >> 3), ch = tid & 7;
+    const int64_t i = (r0 + r) * cols + c0 + 8 * ch;
+    float4 &p0 = pa[k][0], &p1 = pa[k][1], &m0 = ma[k][0], &m1 = ma[k][1];
+    float4 &v0 = va[k][0], &v1 = va[k][1];
+    adam_one(p0.x, gv[k][0], m0.x, v0.x, s);
+    adam_one(p0.y, gv[k][1], m0.y, v0.y, s);
+    adam_one(p0.z, gv[k][2], m0.z, v0.z, s);
+    adam_one(p0.w, gv[k][3], m0.w, v0.w, s);
+    adam_one(p1.x, gv[k][4], m1.x, v1.x, s);
+    adam_one(p1.y, gv[k][5], m1.y, v1.y, s);
+    adam_one(p1.z, gv[k][6], m1.z, v1.z, s);
+    adam_one(p1.w, gv[k][7], m1.w, v1.w, s);
+    *reinterpret_cast<float4*>(p + i) = p0;
+    *reinterpret_cast<float4*>(p + i + 4) = p1;
+    *reinterpret_cast<float4*>(m + i) = m0;
+    *reinterpret_cast<float4*>(m + i + 4) = m1;
+    *reinterpret_cast<float4*>(v + i) = v0;
+    *reinterpret_cast<float4*>(v + i + 4) = v1;
+    store8<L>(lowp + i, p0, p1);
+    const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[r][8 * ch + e] = static_cast<L>(pv[e]);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {  // transposed rows c: 8-row chunks
+    const int c = k * 32 + (tid >> 3), ch = tid & 7;
+    const int64_t gc = c0 + c, gr = r0 + 8 * ch;
+    if (gc < cols && gr < rows) {
+      typedef L L8 __attribute__((ext_vector_type(8)));
+      L8 w;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w[e] = tile[8 * ch + e][c];
+      *reinterpret_cast<L8*>(lowp_t + gc * ld_t + gr) = w;
+    }
+  }
+}
+
 // groups of 8 elements one workgroup of adamw_vec8 covers
 static constexpr int64_t kAdamGroupsPerBlock = 512;
 
@@ -216,6 +292,21 @@ static void launch_vec(float* p, const void* g, float* m, float* v, void* lowp,
                        st, p, (const G*)g, m, v, (float*)lowp, n8, s);
 }
 
+static AdamScalars adam_scalars(double lr, double beta1, double beta2, double eps,
+                                double weight_decay, int64_t step) {
+  AdamScalars s;
+  s.decay = static_cast<float>(1.0 - lr * weight_decay);
+  s.one_minus_b1 = static_cast<float>(1.0 - beta1);
+  s.b2 = static_cast<float>(beta2);
+  s.one_minus_b2 = static_cast<float>(1.0 - beta2);
+  const double bc1 = 1.0 - std::pow(beta1, static_cast<double>(step));
+  const double bc2 = 1.0 - std::pow(beta2, static_cast<double>(step));
+  s.step_size = static_cast<float>(lr / bc1);
+  s.bc2_sqrt = static_cast<float>(std::sqrt(bc2));
+  s.eps = static_cast<float>(eps);
+  return s;
+}
+
 }  // namespace zk
 
 using namespace zk;
@@ -239,16 +330,7 @@ extern "C" int zk_adamw_step(float* param, const void* grad, int grad_dtype,
                  eps >= 0 && weight_decay >= 0,
              ZK_EINVAL, "zk_adamw_step: hyper-parameter out of range");
   if (n == 0) return ZK_OK;
-  AdamScalars s;
-  s.decay = static_cast<float>(1.0 - lr * weight_decay);
-  s.one_minus_b1 = static_cast<float>(1.0 - beta1);
-  s.b2 = static_cast<float>(beta2);
-  s.one_minus_b2 = static_cast<float>(1.0 - beta2);
-  const double bc1 = 1.0 - std::pow(beta1, static_cast<double>(step));
-  const double bc2 = 1.0 - std::pow(beta2, static_cast<double>(step));
-  s.step_size = static_cast<float>(lr / bc1);
-  s.bc2_sqrt = static_cast<float>(std::sqrt(bc2));
-  s.eps = static_cast<float>(eps);
+  const AdamScalars s = adam_scalars(lr, beta1, beta2, eps, weight_decay, step);
 
   hipStream_t st = as_stream(stream);
   const int gbytes = dtype_bytes(grad_dtype);
@@ -280,4 +362,48 @@ extern "C" int zk_adamw_step(float* param, const void* grad, int grad_dtype,
                        begin, n, s);
   }
   return launch_status("zk_adamw_step");
+}
+
+extern "C" int zk_adamw_step_t(float* param, const void* grad, int grad_dtype, float* exp_avg,
+                               float* exp_avg_sq, void* param_lowp, void* lowp_t, int64_t ld_t,
+                               int lowp_dtype, int64_t rows, int64_t cols, double lr,
+                               double beta1, double beta2, double eps, double weight_decay,
+                               int64_t step, zk_stream_t stream) {
+  ZK_REQUIRE(valid_dtype(grad_dtype), ZK_EDTYPE, "zk_adamw_step_t: bad grad dtype %d",
+             grad_dtype);
+  ZK_REQUIRE(lowp_dtype == ZK_BF16 || lowp_dtype == ZK_F16, ZK_EDTYPE,
+             "zk_adamw_step_t: the copies must be bf16 or fp16 (got %d)", lowp_dtype);
+  ZK_REQUIRE(rows >= 0 && cols >= 0 && ld_t >= rows, ZK_EINVAL, "zk_adamw_step_t: bad shape");
+  ZK_REQUIRE(step >= 1, ZK_EINVAL, "zk_adamw_step_t: step must be >= 1 (got %lld)",
+             (long long)step);
+  ZK_REQUIRE(lr >= 0 && beta1 >= 0 && beta1 < 1 && beta2 >= 0 && beta2 < 1 &&
+                 eps >= 0 && weight_decay >= 0,
+             ZK_EINVAL, "zk_adamw_step_t: hyper-parameter out of range");
+  if (rows == 0 || cols == 0) return ZK_OK;
+  ZK_REQUIRE(rows % 8 == 0 && cols % 8 == 0 && ld_t % 8 == 0, ZK_EUNSUPPORTED,
+             "zk_adamw_step_t: rows, cols and ld_t must be multiples of 8");
+  ZK_REQUIRE((rows + 63) / 64 < 65536 && (cols + 63) / 64 < 0x7fffffffLL, ZK_EINVAL,
+             "zk_adamw_step_t: matrix too large");
+  const void* ptrs[] = {param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_t};
+  for (const void* p : ptrs) {
+    ZK_REQUIRE(p != nullptr, ZK_EINVAL, "zk_adamw_step_t: null pointer");
+    ZK_REQUIRE(aligned(p, 16), ZK_EALIGN, "zk_adamw_step_t: operands must be 16-byte aligned");
+  }
+  const AdamScalars s = adam_scalars(lr, beta1, beta2, eps, weight_decay, step);
+  hipStream_t st = as_stream(stream);
+  const dim3 grid(static_cast<unsigned>((cols + 63) / 64), static_cast<unsigned>((rows + 63) / 64));
+#define ZK_T(G, L)                                                                          \
+  hipLaunchKernelGGL((adamw_tile_t<G, L>), grid, dim3(256), 0, st, param, (const G*)grad,  \
+                     exp_avg, exp_avg_sq, (L*)param_lowp, (L*)lowp_t, ld_t, rows, cols, s)
+  if (lowp_dtype == ZK_BF16) {
+    if (grad_dtype == ZK_BF16) ZK_T(bf16, bf16);
+    else if (grad_dtype == ZK_F16) ZK_T(f16, bf16);
+    else ZK_T(float, bf16);
+  } else {
+    if (grad_dtype == ZK_BF16) ZK_T(bf16, f16);
+    else if (grad_dtype == ZK_F16) ZK_T(f16, f16);
+    else ZK_T(float, f16);
+  }
+#undef ZK_T
+  return launch_status("zk_adamw_step_t");
 }

@@ -397,6 +397,30 @@ def adamw_step(param: torch.Tensor, grad: torch.Tensor, exp_avg: torch.Tensor,
           "zk_adamw_step")
 
 
+def adamw_step_t(param: torch.Tensor, grad: torch.Tensor, exp_avg: torch.Tensor,
+                 exp_avg_sq: torch.Tensor, lowp_out: torch.Tensor, lowp_t: torch.Tensor, *,
+                 rows: int, cols: int, lr: float, beta1: float, beta2: float, eps: float,
+                 weight_decay: float, step: int) -> None:
+    """adamw_step on one row-major [rows, cols] matrix (flat contiguous slices of
+    rows * cols elements) that also writes the rounded parameter transposed into
+    ``lowp_t`` ([cols, rows], unit column stride, bf16 / fp16)."""
+    dev = _require_gpu(param, grad, exp_avg, exp_avg_sq, lowp_out, lowp_t)
+    n = rows * cols
+    for name, t in (("param", param), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq)):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != n:
+            raise ValueError(f"{name} must be contiguous fp32 with {n} elements")
+    for name, t in (("grad", grad), ("lowp_out", lowp_out)):
+        if t.numel() != n or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous with {n} elements")
+    if lowp_t.shape != (cols, rows) or lowp_t.stride(1) != 1 or lowp_t.dtype != lowp_out.dtype:
+        raise ValueError("lowp_t must be [cols, rows] with unit column stride, lowp_out's dtype")
+    check(lib().zk_adamw_step_t(ptr(param), ptr(grad), dtype_code(grad.dtype), ptr(exp_avg),
+                                ptr(exp_avg_sq), ptr(lowp_out), ptr(lowp_t), lowp_t.stride(0),
+                                dtype_code(lowp_out.dtype), rows, cols, float(lr), float(beta1),
+                                float(beta2), float(eps), float(weight_decay), int(step),
+                                stream_handle(dev)), "zk_adamw_step_t")
+
+
 def cast_(src: torch.Tensor, dst: torch.Tensor, accumulate: bool = False) -> torch.Tensor:
     """dst = round(src) (or dst = round(dst + src)); contiguous, same numel."""
     dev = _require_gpu(src, dst)

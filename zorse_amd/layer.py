@@ -132,15 +132,19 @@ def _swiglu_transposed(gu, F):
     return _transposing(gu) and gu.shape[0] % 8 == 0 and F % 8 == 0
 
 
-def _dgrad(dy, wmat, transpose_weight):
-    """dy W (the input gradient of y = x W^T).  With ``transpose_weight`` (and
-    2-byte types, long token counts) W^T is materialised first so that both
-    operands are read along the reduction; the layer uses it where the
-    reduction is over the hidden size (o_proj, down_proj), for which the
-    transpose is cheap relative to the GEMM it speeds up."""
-    if transpose_weight and _transposing(dy):
-        wt = K.transpose(wmat)
-        return torch.mm(dy, wt.t())
+def _dgrad(dy, wmat, transpose_weight, wt=None):
+    """dy W (the input gradient of y = x W^T).  For 2-byte types and long
+    token counts the GEMM reads W^T [in, out] so that both operands stream
+    along the reduction: ``wt`` when the optimizer keeps it current, else, with
+    ``transpose_weight``, a transpose made here -- the layer asks for that
+    where the reduction is over the hidden size (o_proj, down_proj), for which
+    the transpose is cheap relative to the GEMM it speeds up."""
+    if _transposing(dy):
+        if wt is not None:
+            return torch.mm(dy, wt.t())
+        if transpose_weight:
+            wt = K.transpose(wmat)
+            return torch.mm(dy, wt.t())
     return torch.mm(dy, wmat)
 
 
@@ -196,9 +200,11 @@ BEFORE_ATTENTION_BACKWARD: list = []
 
 
 def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
-                   grad_flat: torch.Tensor) -> torch.Tensor:
+                   grad_flat: torch.Tensor, wt: dict | None = None) -> torch.Tensor:
     """Backward of layer_forward; writes weight grads into ``grad_flat``
-    (compute dtype, flat layout) and returns dx."""
+    (compute dtype, flat layout) and returns dx.  ``wt`` (optional): W^T of
+    the qkv, o, gu and down weights, current with ``w``."""
+    wt = wt or {}
     x2, n1, rstd1, qkv, o2, lse, hdn, n2, rstd2, gu, zs = saved
     T, h = x2.shape
     B = dout.shape[0]
@@ -208,7 +214,7 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
     dout2 = dout.reshape(T, h)
 
     # MLP: out = hdn + z W_down^T
-    dz = _dgrad(dout2, w.down, True)                 # [T, F]
+    dz = _dgrad(dout2, w.down, True, wt.get("down"))  # [T, F]
     fused_t = _swiglu_transposed(gu, F)
     if fused_t:                                      # zs = z^T
         _wgrad(dout2, None, g.down, xt=zs)
@@ -222,14 +228,14 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
     else:
         K.swiglu_bwd(dz, gu[:, :F], gu[:, F:], dgu[:, :F], dgu[:, F:])
     del dz
-    dn2 = _dgrad(dgu, w.gu, False)                   # [T, h]
+    dn2 = _dgrad(dgu, w.gu, False, wt.get("gu"))     # [T, h]
     _wgrad(dgu, n2, g.gu, dyt=dgut)
     del dgu, dgut
     dh, _ = K.rmsnorm_bwd(dn2, hdn, w.ln2, rstd2, dres=dout2, dw=g.ln2)
     del dn2
 
     # attention: hdn = x + o W_o^T
-    do2 = _dgrad(dh, w.o, True)                      # [T, Hq d]
+    do2 = _dgrad(dh, w.o, True, wt.get("o"))         # [T, Hq d]
     _wgrad(dh, o2, g.o)
     q = qkv[:, :spec.q_dim].view(B, S, Hq, d)
     k = qkv[:, spec.q_dim:spec.q_dim + spec.kv_dim].view(B, S, Hkv, d)
@@ -245,7 +251,7 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
     del do2
     cos, sin = rope_tables(S, d, spec.rope_theta, dout.dtype, dout.device, spec.interleaved_rope)
     K.rope_(dq, dk, cos, sin, interleaved=spec.interleaved_rope, inverse=True)
-    dn1 = _dgrad(dqkv, w.qkv, False)                 # [T, h]
+    dn1 = _dgrad(dqkv, w.qkv, False, wt.get("qkv"))  # [T, h]
     _wgrad(dqkv, n1, g.qkv)
     del dqkv
     dx, _ = K.rmsnorm_bwd(dn1, x2, w.ln1, rstd1, dres=dh, dw=g.ln1)
@@ -296,7 +302,7 @@ class DecoderLayerFunction(torch.autograd.Function):
     """autograd node of one decoder layer: inputs (x, flat_param)."""
 
     @staticmethod
-    def forward(ctx, x, flat_param, spec, weights_lowp, attn_cache=None):
+    def forward(ctx, x, flat_param, spec, weights_lowp, attn_cache=None, wt=None):
         w_flat = weights_lowp if weights_lowp is not None else flat_param
         w = FlatViews(spec, w_flat)
         if attn_cache is not None:
@@ -304,6 +310,7 @@ class DecoderLayerFunction(torch.autograd.Function):
         with torch.autocast("cuda", enabled=False):
             out, saved = layer_forward(x.contiguous(), w, spec, attn_cache)
         ctx.spec = spec
+        ctx.wt = wt
         ctx.param_dtype = flat_param.dtype
         ctx.save_for_backward(w_flat, *saved)
         return out
@@ -316,7 +323,7 @@ class DecoderLayerFunction(torch.autograd.Function):
         dout = dout.to(w_flat.dtype).contiguous()
         grad_flat = torch.empty(spec.numel, device=dout.device, dtype=w_flat.dtype)
         with torch.autocast("cuda", enabled=False):
-            dx = layer_backward(dout, saved, w, spec, grad_flat)
+            dx = layer_backward(dout, saved, w, spec, grad_flat, ctx.wt)
         if ctx.param_dtype != grad_flat.dtype:
             grad_flat = grad_flat.to(ctx.param_dtype)
-        return dx, grad_flat, None, None, None
+        return dx, grad_flat, None, None, None, None

@@ -30,6 +30,28 @@ class FusedAdamW(torch.optim.Optimizer):
             raise ValueError(f"invalid betas {betas}")
         super().__init__(params, dict(lr=lr, betas=tuple(betas), eps=eps,
                                       weight_decay=weight_decay))
+        self._tcopies = {}      # param -> [(offset, rows, cols, out)]
+        self._step_hooks = {}   # param -> [callable(param)]
+
+    def add_transposed_copy(self, p: torch.Tensor, offset: int, rows: int, cols: int,
+                            out: torch.Tensor) -> None:
+        """Each step also writes the updated elements offset .. offset + rows * cols
+        of ``p`` (a row-major [rows, cols] matrix), rounded to ``p``'s dtype,
+        transposed into ``out`` ([cols, rows]) -- in the same kernel pass that
+        updates them.  ``p`` must be a bf16 / fp16 compute copy (fp32 master in
+        the optimizer state); regions must not overlap."""
+        if p.dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("transposed copies are kept for bf16 / fp16 parameters only")
+        if out.shape != (cols, rows) or out.dtype != p.dtype or out.stride(1) != 1:
+            raise ValueError("out must be [cols, rows] of the parameter's dtype")
+        if offset < 0 or offset + rows * cols > p.numel():
+            raise ValueError("matrix region outside the parameter")
+        self._tcopies.setdefault(p, []).append((int(offset), int(rows), int(cols), out))
+        self._tcopies[p].sort(key=lambda r: r[0])
+
+    def add_step_hook(self, p: torch.Tensor, fn) -> None:
+        """``fn(p)`` runs after every step of ``p`` (after its version bump)."""
+        self._step_hooks.setdefault(p, []).append(fn)
 
     def _init_state(self, p: torch.Tensor) -> dict:
         st = self.state[p]
@@ -63,16 +85,42 @@ class FusedAdamW(torch.optim.Optimizer):
                             st[k] = st[k].to(p.device)
                 st["step"] += 1
                 master = st.get("master")
-                K.adamw_step(master if master is not None else p.view(-1),
-                             p.grad.view(-1), st["exp_avg"], st["exp_avg_sq"],
-                             lr=group["lr"], beta1=b1, beta2=b2, eps=group["eps"],
-                             weight_decay=group["weight_decay"], step=st["step"],
-                             lowp_out=p.view(-1) if master is not None else None)
+                hyper = dict(lr=group["lr"], beta1=b1, beta2=b2, eps=group["eps"],
+                             weight_decay=group["weight_decay"], step=st["step"])
+                regions = self._tcopies.get(p) if master is not None else None
+                if not regions:
+                    K.adamw_step(master if master is not None else p.view(-1),
+                                 p.grad.view(-1), st["exp_avg"], st["exp_avg_sq"],
+                                 lowp_out=p.view(-1) if master is not None else None, **hyper)
+                else:
+                    self._step_regions(p, st, master, regions, hyper)
                 # the kernel wrote p through a raw pointer: advance its version
                 # counter as an in-place torch op would, so caches keyed on it
                 # (compute-dtype weight copies, attention caches) see the update
                 torch.autograd.graph.increment_version(p)
+                for fn in self._step_hooks.get(p, ()):
+                    fn(p)
         return loss
+
+    @staticmethod
+    def _step_regions(p, st, master, regions, hyper):
+        """The step as one launch per registered matrix (with its transposed
+        copy) plus flat launches for the elements between them."""
+        flat, grad = p.view(-1), p.grad.view(-1)
+        m, v = st["exp_avg"], st["exp_avg_sq"]
+        pos, n = 0, p.numel()
+
+        def plain(a, b):
+            if b > a:
+                K.adamw_step(master[a:b], grad[a:b], m[a:b], v[a:b], lowp_out=flat[a:b], **hyper)
+
+        for off, rows, cols, out in regions:
+            plain(pos, off)
+            e = off + rows * cols
+            K.adamw_step_t(master[off:e], grad[off:e], m[off:e], v[off:e], flat[off:e], out,
+                           rows=rows, cols=cols, **hyper)
+            pos = e
+        plain(pos, n)
 
     def master_param(self, p: torch.Tensor) -> torch.Tensor:
         """fp32 master of ``p`` (``p`` itself when it is fp32)."""
