@@ -94,7 +94,7 @@ class KernelCases:
     Cache.  ``copy`` is a plain device copy of 1 GiB (read 1 GiB, write
     1 GiB), the calibration for the FETCH_SIZE / WRITE_SIZE counters."""
 
-    NAMES = ("attn_fwd", "attn_bwd", "rmsnorm_fwd", "rmsnorm_bwd", "adamw", "copy")
+    NAMES = ("attn_fwd", "attn_bwd", "rmsnorm_fwd", "rmsnorm_bwd", "adamw", "adamw_t", "copy")
 
     def __init__(self, dev, spec, S):
         self.dev, self.spec, self.S = dev, spec, S
@@ -155,6 +155,30 @@ class KernelCases:
                 K.adamw_step(p, gr, m, vv, lr=1e-4, beta1=0.9, beta2=0.95, eps=1e-8,
                              weight_decay=0.1, step=step[0], lowp_out=lowp)
             return run, flops.adamw_bytes(n, 2, True)
+        if name == "adamw_t":
+            # the step as the stage runs it: one launch over the layer's four
+            # projection matrices (each also written transposed) and the norms
+            n, o, sp = spec.numel, spec.offsets(), spec
+            p = torch.randn(n, device=dev)
+            m = torch.zeros(n, device=dev)
+            vv = torch.zeros(n, device=dev)
+            gr = torch.randn(n, device=dev, dtype=torch.bfloat16)
+            lowp = torch.empty(n, device=dev, dtype=torch.bfloat16)
+            mats = [(o["q"][0], sp.q_dim + 2 * sp.kv_dim, sp.hidden),
+                    (o["o"][0], sp.hidden, sp.q_dim), (o["gate"][0], 2 * sp.ffn, sp.hidden),
+                    (o["down"][0], sp.hidden, sp.ffn)]
+            regions = [(off, r, c, torch.empty(c, r, device=dev, dtype=torch.bfloat16))
+                       for off, r, c in mats]
+            tail = o["ln1"][0]
+            regions.append((tail, 8, (n - tail) // 8, None))
+            n_t = sum(r * c for _, r, c in mats)
+            step = [0]
+
+            def run():
+                step[0] += 1
+                K.adamw_step_t(p, gr, m, vv, lowp, regions, lr=1e-4, beta1=0.9, beta2=0.95,
+                               eps=1e-8, weight_decay=0.1, step=step[0])
+            return run, flops.adamw_bytes(n, 2, True) + 2 * n_t
         if name == "copy":
             src = torch.empty(1 << 28, device=dev, dtype=torch.float32).normal_()
             dst = torch.empty_like(src)
@@ -173,6 +197,7 @@ def measure_kernels(dev, spec, S):
         "rmsnorm_fwd": ("rmsnorm_fwd_vec<bf16,bf16,128,4>", "hbm", 32),
         "rmsnorm_bwd": ("rmsnorm_bwd_vec<bf16,bf16,256,2,2> + dw reduce", "hbm", 32),
         "adamw": ("adamw_vec8<bf16,bf16,true>", "hbm", 10),
+        "adamw_t": ("adamw_tile_t<bf16,bf16> (layer step with W^T copies)", "hbm", 10),
         "copy": ("device copy 1 GiB (HBM reference)", "hbm", 5),
     }
     for name, (kname, bound, iters) in spec_of.items():
@@ -224,6 +249,7 @@ TRAFFIC_CASES = {
     "rmsnorm_bwd": ("rmsnorm_bwd_vec<bf16,bf16,256,2,2> + dw reduce",
                     ("rmsnorm_bwd_vec", "rmsnorm_dw_reduce")),
     "adamw": ("adamw_vec8<bf16,bf16,true>", ("adamw_vec8",)),
+    "adamw_t": ("adamw_tile_t<bf16,bf16> (layer step with W^T copies)", ("adamw_tile_t",)),
 }
 
 
@@ -259,7 +285,9 @@ def summarize_traffic(root: str) -> str:
             "attn_bwd": flops.attn_bwd_bytes(1, T, H, H, d),
             "rmsnorm_fwd": flops.rmsnorm_fwd_bytes(T, h),
             "rmsnorm_bwd": flops.rmsnorm_bwd_bytes(T, h),
-            "adamw": flops.adamw_bytes(spec.numel, 2, True)}
+            "adamw": flops.adamw_bytes(spec.numel, 2, True),
+            "adamw_t": flops.adamw_bytes(spec.numel, 2, True)
+            + 2 * (spec.numel - 2 * spec.hidden)}
     lines = ["| kernel | FETCH_SIZE (MiB) | WRITE_SIZE (MiB) | HBM traffic (MB) | "
              "algorithmic bytes (MB) | traffic / algorithmic |", "|---|---|---|---|---|---|"]
     machine = []
@@ -347,8 +375,9 @@ def main():
     kern = measure_kernels(dev, spec, S)
     print("kernel timings done", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline(spec, S)
-    # the dominant hand-written kernel of the step (by time): the AdamW pass
-    a = kern["adamw"]
+    # the dominant hand-written kernel of the step (by time): the AdamW pass as
+    # the stage runs it (one tiled launch per layer, writing W^T copies too)
+    a = kern["adamw_t"]
     af, ab = kern["attn_fwd"], kern["attn_bwd"]
     line = {
         "metric": "decoder-layer fwd+bwd tokens/s at 1 GPU; attention TFLOP/s vs MFMA peak",

@@ -208,21 +208,26 @@ int zk_adamw_step(float* param, const void* grad, int grad_dtype,
                   double beta2, double eps, double weight_decay, int64_t step,
                   zk_stream_t stream);
 
-/* The same update on one row-major [rows, cols] weight matrix of the shard
- * (param / grad / exp_avg / exp_avg_sq / param_lowp point at its first
- * element), additionally writing the rounded parameter transposed,
+/* The same update over a shard given as up to 8 row-major [rows, cols]
+ * regions (element offset into the shard; in increasing order, not
+ * overlapping; elements outside every region are not touched), in one
+ * launch.  param_lowp (bf16 / fp16) receives the rounded update as in
+ * zk_adamw_step; a region with lowp_t != NULL also receives it transposed,
  * lowp_t[c][r] (row stride ld_t >= rows): the weight layout the input-gradient
  * GEMM of the layer's backward reads along its reduction (grad_input =
  * grad_output @ W of the nn.Linear projections, models/llama_simple.py:
  * 206-221, 293-295, 368 and the MLP at :418), kept current by the optimizer
- * step that already rewrites the compute copy.  param_lowp and lowp_t are
- * required (bf16 / fp16); rows, cols, ld_t multiples of 8; 16-byte aligned. */
+ * step that already rewrites the compute copy.  Offsets, rows, cols, ld_t
+ * multiples of 8; 16-byte aligned buffers. */
+typedef struct zk_adamw_region {
+  int64_t offset, rows, cols, ld_t;
+  void* lowp_t;
+} zk_adamw_region;
 int zk_adamw_step_t(float* param, const void* grad, int grad_dtype,
                     float* exp_avg, float* exp_avg_sq, void* param_lowp,
-                    void* lowp_t, int64_t ld_t, int lowp_dtype, int64_t rows,
-                    int64_t cols, double lr, double beta1, double beta2,
-                    double eps, double weight_decay, int64_t step,
-                    zk_stream_t stream);
+                    int lowp_dtype, const zk_adamw_region* regions, int n_regions,
+                    double lr, double beta1, double beta2, double eps,
+                    double weight_decay, int64_t step, zk_stream_t stream);
 
 /* ------------------------------------------------- LM head cross-entropy --
  * Replaces the last stage's loss, F.cross_entropy(out.flatten(0, 1),

@@ -85,6 +85,16 @@ def test_validation_codes(lib):
     assert lib.zk_swiglu_fwd_t(ctypes.c_void_p(24), p, 16, p, 8, p, 16, 16, 8, 2, None) == -3
     assert lib.zk_swiglu_bwd_t(p, 8, p, p, 16, p, p, 16, p, p, 4, 16, 8, 2, None) == -1
     assert lib.zk_swiglu_bwd_t(p, 16, p, p, 16, p, p, 16, p, p, 16, 16, 12, 1, None) == -4
+    # adamw_step_t: overlapping regions, rows not a multiple of 8, too many regions
+    R = _abi.AdamwRegion * 2
+    regs = R(_abi.AdamwRegion(0, 8, 8, 0, None), _abi.AdamwRegion(32, 8, 8, 0, None))
+    assert lib.zk_adamw_step_t(p, p, 2, p, p, p, 2, ctypes.cast(regs, ctypes.c_void_p), 2, 1e-3,
+                               0.9, 0.999, 1e-8, 0.0, 1, None) == -1
+    regs = R(_abi.AdamwRegion(0, 12, 8, 0, None), _abi.AdamwRegion(96, 8, 8, 0, None))
+    assert lib.zk_adamw_step_t(p, p, 2, p, p, p, 2, ctypes.cast(regs, ctypes.c_void_p), 2, 1e-3,
+                               0.9, 0.999, 1e-8, 0.0, 1, None) == -4
+    assert lib.zk_adamw_step_t(p, p, 2, p, p, p, 2, ctypes.cast(regs, ctypes.c_void_p), 9, 1e-3,
+                               0.9, 0.999, 1e-8, 0.0, 1, None) == -1
     # gemm_swiglu: fp32, K not a multiple of 64, misaligned x, ld_x < K
     assert lib.zk_gemm_swiglu(p, 64, p, p, 64, p, p, 8, p, 8, None, 0, 8, 8, 64, 0, None) == -2
     assert lib.zk_gemm_swiglu(p, 64, p, p, 64, p, p, 8, p, 8, None, 0, 8, 8, 32, 2, None) == -4

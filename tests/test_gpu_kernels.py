@@ -319,13 +319,16 @@ def test_adamw_kernel_vs_oracle(dev, gdt, n):
                                               (200, 136, torch.float16, torch.float16),
                                               (8, 8, torch.bfloat16, torch.bfloat16)])
 def test_adamw_step_transposed_copy(dev, rows, cols, gdt, ldt):
-    """zk_adamw_step_t: master, m, v and the compute copy bit-equal to
-    zk_adamw_step on the same inputs, and the transposed copy an exact
-    transpose of the compute copy (full and ragged 64 x 64 tiles)."""
+    """zk_adamw_step_t over a shard of two matrices with transposed copies and
+    a region without one, around an element range no region covers: master,
+    m, v and the compute copy bit-equal to zk_adamw_step on the covered
+    elements and untouched elsewhere; the transposed copies exact transposes
+    (full and ragged 64 x 64 tiles)."""
     from zorse_amd import kernels as K
     print(f"adamw_t rows={rows} cols={cols} {gdt} -> {ldt}", flush=True)
     g = torch.Generator().manual_seed(52)
-    n = rows * cols
+    a = rows * cols
+    n = 2 * a + 64 + 128          # matrix, matrix, 64-element hole, 8 x 16 region
     p0 = torch.randn(n, generator=g)
     m0 = 0.01 * torch.randn(n, generator=g)
     v0 = 0.001 * torch.rand(n, generator=g)
@@ -335,12 +338,20 @@ def test_adamw_step_transposed_copy(dev, rows, cols, gdt, ldt):
     low = torch.empty(n, dtype=ldt, device=dev)
     K.adamw_step(p, gr, m, v, lowp_out=low, **hyper)
     pt, mt, vt = p0.to(dev), m0.to(dev), v0.to(dev)
-    lowt = torch.empty(n, dtype=ldt, device=dev)
-    tr = torch.full((cols, rows), float("nan"), dtype=ldt, device=dev)
-    K.adamw_step_t(pt, gr, mt, vt, lowt, tr, rows=rows, cols=cols, **hyper)
-    for a, b, what in ((p, pt, "master"), (m, mt, "m"), (v, vt, "v"), (low, lowt, "copy")):
-        assert torch.equal(a, b), what
-    assert torch.equal(tr, lowt.view(rows, cols).t())
+    lowt = torch.zeros(n, dtype=ldt, device=dev)
+    t1 = torch.full((cols, rows), float("nan"), dtype=ldt, device=dev)
+    t2 = torch.full((rows, cols), float("nan"), dtype=ldt, device=dev)
+    regions = [(0, rows, cols, t1), (a, cols, rows, t2), (2 * a + 64, 8, 16, None)]
+    K.adamw_step_t(pt, gr, mt, vt, lowt, regions, **hyper)
+    cov = torch.ones(n, dtype=torch.bool, device=dev)
+    cov[2 * a:2 * a + 64] = False
+    for x, y, x0, what in ((p, pt, p0, "master"), (m, mt, m0, "m"), (v, vt, v0, "v")):
+        assert torch.equal(x[cov], y[cov]), what
+        assert torch.equal(y[~cov], x0.to(dev)[~cov]), what + " outside the regions"
+    assert torch.equal(low[cov], lowt[cov])
+    assert torch.equal(lowt[~cov], torch.zeros(64, dtype=ldt, device=dev))
+    assert torch.equal(t1, lowt[:a].view(rows, cols).t())
+    assert torch.equal(t2, lowt[a:2 * a].view(cols, rows).t())
 
 
 def test_fused_adamw_matches_torch_adamw_and_adam(dev):

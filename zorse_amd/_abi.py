@@ -58,6 +58,13 @@ class AttnDesc(ctypes.Structure):
     ]
 
 
+class AdamwRegion(ctypes.Structure):
+    """Mirror of ``zk_adamw_region``."""
+
+    _fields_ = [("offset", _i64), ("rows", _i64), ("cols", _i64), ("ld_t", _i64),
+                ("lowp_t", _ptr)]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "zk_last_error": (ctypes.c_char_p, []),
@@ -88,7 +95,7 @@ SIGNATURES = {
                            _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr]),
     "zk_adamw_step": (_int, [_ptr, _ptr, _int, _ptr, _ptr, _ptr, _int, _i64,
                              _f64, _f64, _f64, _f64, _f64, _i64, _ptr]),
-    "zk_adamw_step_t": (_int, [_ptr, _ptr, _int, _ptr, _ptr, _ptr, _ptr, _i64, _int, _i64, _i64,
+    "zk_adamw_step_t": (_int, [_ptr, _ptr, _int, _ptr, _ptr, _ptr, _int, _ptr, _int,
                                 _f64, _f64, _f64, _f64, _f64, _i64, _ptr]),
     "zk_cast": (_int, [_ptr, _int, _ptr, _int, _i64, _int, _ptr]),
     "zk_ce_fwd_chunk": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr, _int,

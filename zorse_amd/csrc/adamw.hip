@@ -177,32 +177,59 @@ __global__ __launch_bounds__(256) void adamw_vec8(
   }
 }
 
-// The same update on one row-major [rows, cols] matrix of the shard, also
-// writing the rounded parameter transposed (lowp_t[c][r], row stride ld_t):
-// the compute copy the backward's input-gradient GEMM reads along its
-// reduction.  A workgroup owns a 64 x 64 tile: 16-byte accesses on every
-// stream (rows of 64 elements), the rounded values staged in a padded LDS
-// tile (pitch 66) and written back as 16-byte chunks of 8 consecutive rows.
-// rows and cols are multiples of 8.
+// The same update over a shard described as row-major [rows, cols] regions
+// (one launch per shard): for each region with a transposed-copy target the
+// rounded parameter is also written transposed (lowp_t[c][r], row stride
+// ld_t) -- the compute copy the backward's input-gradient GEMM reads along
+// its reduction.  A workgroup owns a kTileR x kTileC tile of one region:
+// 16-byte accesses on every stream (tile rows of kTileC elements), the
+// rounded values staged in a padded LDS tile and written back as 16-byte
+// chunks of 8 consecutive rows.  rows and cols are multiples of 8.
+static constexpr int kMaxAdamRegions = 8;
+struct AdamRegions {
+  int64_t offset[kMaxAdamRegions];
+  int64_t rows[kMaxAdamRegions];
+  int64_t cols[kMaxAdamRegions];
+  int64_t ld_t[kMaxAdamRegions];
+  void* lowp_t[kMaxAdamRegions];
+  int64_t tiles_x[kMaxAdamRegions];      // column tiles per region
+  int64_t first_tile[kMaxAdamRegions + 1];  // prefix sums of the tile counts
+  int n;
+};
+
+// tile of the region kernel: kTileR rows x kTileC columns per workgroup
+static constexpr int kTileR = 64, kTileC = 128;
+
 template <typename G, typename L>
 __global__ __launch_bounds__(256) void adamw_tile_t(
     float* __restrict__ p, const G* __restrict__ g, float* __restrict__ m,
-    float* __restrict__ v, L* __restrict__ lowp, L* __restrict__ lowp_t, int64_t ld_t,
-    int64_t rows, int64_t cols, AdamScalars s) {
-  __shared__ L tile[64][66];
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64;
-  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 64;
-  const int tid = threadIdx.x;
-  float4 pa[2][2], ma[2][2], va[2][2];
-  float gv[2][8];
-  bool in[2];
+    float* __restrict__ v, L* __restrict__ lowp, AdamRegions reg, AdamScalars s) {
+  constexpr int TR = kTileR, TC = kTileC;
+  constexpr int CPR = TC / 8;              // 8-element chunks per tile row
+  constexpr int NG = TR * CPR / 256;       // chunks per thread
+  constexpr int RPP = 256 / CPR;           // tile rows per pass
+  __shared__ L tile[TR][TC + 2];
+  const int64_t bid = blockIdx.x;
+  int ri = 0;
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {  // rows k * 32 + tid / 8, columns 8 (tid % 8)
-    const int r = k * 32 + (tid >> 3), ch = tid & 7;
+  for (int k = 1; k < kMaxAdamRegions; ++k)
+    if (k < reg.n && bid >= reg.first_tile[k]) ri = k;
+  const int64_t local = bid - reg.first_tile[ri];
+  const int64_t rows = reg.rows[ri], cols = reg.cols[ri];
+  const int64_t r0 = local / reg.tiles_x[ri] * TR;
+  const int64_t c0 = local % reg.tiles_x[ri] * TC;
+  const int64_t base = reg.offset[ri];
+  const int tid = threadIdx.x;
+  float4 pa[NG][2], ma[NG][2], va[NG][2];
+  float gv[NG][8];
+  bool in[NG];
+#pragma unroll
+  for (int k = 0; k < NG; ++k) {  // rows k * RPP + tid / CPR, columns 8 (tid % CPR)
+    const int r = k * RPP + tid / CPR, ch = tid % CPR;
     const int64_t gr = r0 + r, gc = c0 + 8 * ch;
     in[k] = gr < rows && gc < cols;
     if (in[k]) {
-      const int64_t i = gr * cols + gc;
+      const int64_t i = base + gr * cols + gc;
       pa[k][0] = *reinterpret_cast<const float4*>(p + i);
       pa[k][1] = *reinterpret_cast<const float4*>(p + i + 4);
       ma[k][0] = *reinterpret_cast<const float4*>(m + i);
@@ -213,10 +240,10 @@ __global__ __launch_bounds__(256) void adamw_tile_t(
     }
   }
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
+  for (int k = 0; k < NG; ++k) {
     if (!in[k]) continue;
-    const int r = k * 32 + (tid >> 3), ch = tid & 7;
-    const int64_t i = (r0 + r) * cols + c0 + 8 * ch;
+    const int r = k * RPP + tid / CPR, ch = tid % CPR;
+    const int64_t i = base + (r0 + r) * cols + c0 + 8 * ch;
     float4 &p0 = pa[k][0], &p1 = pa[k][1], &m0 = ma[k][0], &m1 = ma[k][1];
     float4 &v0 = va[k][0], &v1 = va[k][1];
     adam_one(p0.x, gv[k][0], m0.x, v0.x, s);
@@ -238,17 +265,22 @@ __global__ __launch_bounds__(256) void adamw_tile_t(
 #pragma unroll
     for (int e = 0; e < 8; ++e) tile[r][8 * ch + e] = static_cast<L>(pv[e]);
   }
+  L* lt = static_cast<L*>(reg.lowp_t[ri]);
+  if (lt == nullptr) return;  // region without a transposed copy (uniform)
+  const int64_t ld_t = reg.ld_t[ri];
   __syncthreads();
+  constexpr int RC = TR / 8;               // 8-row chunks per transposed row
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {  // transposed rows c: 8-row chunks
-    const int c = k * 32 + (tid >> 3), ch = tid & 7;
+  for (int k = 0; k < TC * RC / 256; ++k) {
+    const int q = k * 256 + tid;
+    const int c = q / RC, ch = q % RC;
     const int64_t gc = c0 + c, gr = r0 + 8 * ch;
     if (gc < cols && gr < rows) {
       typedef L L8 __attribute__((ext_vector_type(8)));
       L8 w;
 #pragma unroll
       for (int e = 0; e < 8; ++e) w[e] = tile[8 * ch + e][c];
-      *reinterpret_cast<L8*>(lowp_t + gc * ld_t + gr) = w;
+      *reinterpret_cast<L8*>(lt + gc * ld_t + gr) = w;
     }
   }
 }
@@ -365,36 +397,60 @@ extern "C" int zk_adamw_step(float* param, const void* grad, int grad_dtype,
 }
 
 extern "C" int zk_adamw_step_t(float* param, const void* grad, int grad_dtype, float* exp_avg,
-                               float* exp_avg_sq, void* param_lowp, void* lowp_t, int64_t ld_t,
-                               int lowp_dtype, int64_t rows, int64_t cols, double lr,
+                               float* exp_avg_sq, void* param_lowp, int lowp_dtype,
+                               const zk_adamw_region* regions, int n_regions, double lr,
                                double beta1, double beta2, double eps, double weight_decay,
                                int64_t step, zk_stream_t stream) {
   ZK_REQUIRE(valid_dtype(grad_dtype), ZK_EDTYPE, "zk_adamw_step_t: bad grad dtype %d",
              grad_dtype);
   ZK_REQUIRE(lowp_dtype == ZK_BF16 || lowp_dtype == ZK_F16, ZK_EDTYPE,
-             "zk_adamw_step_t: the copies must be bf16 or fp16 (got %d)", lowp_dtype);
-  ZK_REQUIRE(rows >= 0 && cols >= 0 && ld_t >= rows, ZK_EINVAL, "zk_adamw_step_t: bad shape");
+             "zk_adamw_step_t: the compute copy must be bf16 or fp16 (got %d)", lowp_dtype);
+  ZK_REQUIRE(n_regions >= 0 && n_regions <= kMaxAdamRegions, ZK_EINVAL,
+             "zk_adamw_step_t: 0 .. %d regions (got %d)", kMaxAdamRegions, n_regions);
+  ZK_REQUIRE(n_regions == 0 || regions != nullptr, ZK_EINVAL, "zk_adamw_step_t: null regions");
   ZK_REQUIRE(step >= 1, ZK_EINVAL, "zk_adamw_step_t: step must be >= 1 (got %lld)",
              (long long)step);
   ZK_REQUIRE(lr >= 0 && beta1 >= 0 && beta1 < 1 && beta2 >= 0 && beta2 < 1 &&
                  eps >= 0 && weight_decay >= 0,
              ZK_EINVAL, "zk_adamw_step_t: hyper-parameter out of range");
-  if (rows == 0 || cols == 0) return ZK_OK;
-  ZK_REQUIRE(rows % 8 == 0 && cols % 8 == 0 && ld_t % 8 == 0, ZK_EUNSUPPORTED,
-             "zk_adamw_step_t: rows, cols and ld_t must be multiples of 8");
-  ZK_REQUIRE((rows + 63) / 64 < 65536 && (cols + 63) / 64 < 0x7fffffffLL, ZK_EINVAL,
-             "zk_adamw_step_t: matrix too large");
-  const void* ptrs[] = {param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_t};
+  AdamRegions reg = {};
+  int64_t tiles = 0, prev_end = 0;
+  for (int i = 0; i < n_regions; ++i) {
+    const zk_adamw_region& r = regions[i];
+    ZK_REQUIRE(r.offset >= prev_end && r.rows >= 0 && r.cols >= 0, ZK_EINVAL,
+               "zk_adamw_step_t: region %d overlaps or has a bad shape", i);
+    ZK_REQUIRE(r.offset % 8 == 0 && r.rows % 8 == 0 && r.cols % 8 == 0, ZK_EUNSUPPORTED,
+               "zk_adamw_step_t: region %d: offset, rows and cols must be multiples of 8", i);
+    ZK_REQUIRE(r.lowp_t == nullptr || (r.ld_t >= r.rows && r.ld_t % 8 == 0 && aligned(r.lowp_t, 16)),
+               ZK_EALIGN, "zk_adamw_step_t: region %d: bad transposed target", i);
+    ZK_REQUIRE((r.rows + kTileR - 1) / kTileR * ((r.cols + kTileC - 1) / kTileC) < 0x40000000LL, ZK_EINVAL,
+               "zk_adamw_step_t: region %d too large", i);
+    reg.offset[i] = r.offset;
+    reg.rows[i] = r.rows;
+    reg.cols[i] = r.cols;
+    reg.ld_t[i] = r.ld_t;
+    reg.lowp_t[i] = r.lowp_t;
+    const int64_t tx = (r.cols + kTileC - 1) / kTileC, ty = (r.rows + kTileR - 1) / kTileR;
+    reg.tiles_x[i] = tx > 0 ? tx : 1;
+    reg.first_tile[i] = tiles;
+    tiles += tx * ty;
+    prev_end = r.offset + r.rows * r.cols;
+  }
+  reg.first_tile[n_regions] = tiles;
+  reg.n = n_regions;
+  if (tiles == 0) return ZK_OK;
+  ZK_REQUIRE(tiles < 0x7fffffffLL, ZK_EINVAL, "zk_adamw_step_t: shard too large");
+  const void* ptrs[] = {param, grad, exp_avg, exp_avg_sq, param_lowp};
   for (const void* p : ptrs) {
     ZK_REQUIRE(p != nullptr, ZK_EINVAL, "zk_adamw_step_t: null pointer");
     ZK_REQUIRE(aligned(p, 16), ZK_EALIGN, "zk_adamw_step_t: operands must be 16-byte aligned");
   }
   const AdamScalars s = adam_scalars(lr, beta1, beta2, eps, weight_decay, step);
   hipStream_t st = as_stream(stream);
-  const dim3 grid(static_cast<unsigned>((cols + 63) / 64), static_cast<unsigned>((rows + 63) / 64));
+  const dim3 grid(static_cast<unsigned>(tiles));
 #define ZK_T(G, L)                                                                          \
   hipLaunchKernelGGL((adamw_tile_t<G, L>), grid, dim3(256), 0, st, param, (const G*)grad,  \
-                     exp_avg, exp_avg_sq, (L*)param_lowp, (L*)lowp_t, ld_t, rows, cols, s)
+                     exp_avg, exp_avg_sq, (L*)param_lowp, reg, s)
   if (lowp_dtype == ZK_BF16) {
     if (grad_dtype == ZK_BF16) ZK_T(bf16, bf16);
     else if (grad_dtype == ZK_F16) ZK_T(f16, bf16);

@@ -398,27 +398,39 @@ def adamw_step(param: torch.Tensor, grad: torch.Tensor, exp_avg: torch.Tensor,
 
 
 def adamw_step_t(param: torch.Tensor, grad: torch.Tensor, exp_avg: torch.Tensor,
-                 exp_avg_sq: torch.Tensor, lowp_out: torch.Tensor, lowp_t: torch.Tensor, *,
-                 rows: int, cols: int, lr: float, beta1: float, beta2: float, eps: float,
-                 weight_decay: float, step: int) -> None:
-    """adamw_step on one row-major [rows, cols] matrix (flat contiguous slices of
-    rows * cols elements) that also writes the rounded parameter transposed into
-    ``lowp_t`` ([cols, rows], unit column stride, bf16 / fp16)."""
-    dev = _require_gpu(param, grad, exp_avg, exp_avg_sq, lowp_out, lowp_t)
-    n = rows * cols
+                 exp_avg_sq: torch.Tensor, lowp_out: torch.Tensor, regions, *, lr: float,
+                 beta1: float, beta2: float, eps: float, weight_decay: float,
+                 step: int) -> None:
+    """adamw_step over the regions of a flat shard, in one launch.  ``regions``:
+    up to 8 ``(offset, rows, cols, lowp_t)`` in increasing offset order -- a
+    row-major [rows, cols] matrix at ``offset`` whose rounded update also goes,
+    transposed, into ``lowp_t`` ([cols, rows], unit column stride, lowp_out's
+    dtype) unless it is None.  Elements outside every region are left alone."""
+    import ctypes
+    from ._abi import AdamwRegion
+    dev = _require_gpu(param, grad, exp_avg, exp_avg_sq, lowp_out)
+    n = param.numel()
     for name, t in (("param", param), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq)):
         if t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != n:
             raise ValueError(f"{name} must be contiguous fp32 with {n} elements")
     for name, t in (("grad", grad), ("lowp_out", lowp_out)):
         if t.numel() != n or not t.is_contiguous():
             raise ValueError(f"{name} must be contiguous with {n} elements")
-    if lowp_t.shape != (cols, rows) or lowp_t.stride(1) != 1 or lowp_t.dtype != lowp_out.dtype:
-        raise ValueError("lowp_t must be [cols, rows] with unit column stride, lowp_out's dtype")
+    arr = (AdamwRegion * max(1, len(regions)))()
+    for i, (off, rows, cols, lt) in enumerate(regions):
+        if off < 0 or off + rows * cols > n:
+            raise ValueError("region outside the shard")
+        if lt is not None:
+            _require_gpu(lt)
+            if lt.shape != (cols, rows) or lt.stride(1) != 1 or lt.dtype != lowp_out.dtype:
+                raise ValueError("lowp_t must be [cols, rows] with unit column stride")
+        arr[i] = AdamwRegion(off, rows, cols, lt.stride(0) if lt is not None else 0,
+                             ptr(lt) if lt is not None else None)
     check(lib().zk_adamw_step_t(ptr(param), ptr(grad), dtype_code(grad.dtype), ptr(exp_avg),
-                                ptr(exp_avg_sq), ptr(lowp_out), ptr(lowp_t), lowp_t.stride(0),
-                                dtype_code(lowp_out.dtype), rows, cols, float(lr), float(beta1),
-                                float(beta2), float(eps), float(weight_decay), int(step),
-                                stream_handle(dev)), "zk_adamw_step_t")
+                                ptr(exp_avg_sq), ptr(lowp_out), dtype_code(lowp_out.dtype),
+                                ctypes.cast(arr, ctypes.c_void_p), len(regions), float(lr),
+                                float(beta1), float(beta2), float(eps), float(weight_decay),
+                                int(step), stream_handle(dev)), "zk_adamw_step_t")
 
 
 def cast_(src: torch.Tensor, dst: torch.Tensor, accumulate: bool = False) -> torch.Tensor:

@@ -104,23 +104,27 @@ class FusedAdamW(torch.optim.Optimizer):
 
     @staticmethod
     def _step_regions(p, st, master, regions, hyper):
-        """The step as one launch per registered matrix (with its transposed
-        copy) plus flat launches for the elements between them."""
+        """The step as one launch over the registered matrices (with their
+        transposed copies) and the elements between them (as regions without
+        a copy when they tile into rows of 8, else by the flat kernel)."""
         flat, grad = p.view(-1), p.grad.view(-1)
         m, v = st["exp_avg"], st["exp_avg_sq"]
-        pos, n = 0, p.numel()
+        table, pos, n = [], 0, p.numel()
 
-        def plain(a, b):
-            if b > a:
+        def gap(a, b):
+            if b <= a:
+                return
+            if (b - a) % 64 == 0 and a % 8 == 0:
+                table.append((a, 8, (b - a) // 8, None))
+            else:
                 K.adamw_step(master[a:b], grad[a:b], m[a:b], v[a:b], lowp_out=flat[a:b], **hyper)
 
         for off, rows, cols, out in regions:
-            plain(pos, off)
-            e = off + rows * cols
-            K.adamw_step_t(master[off:e], grad[off:e], m[off:e], v[off:e], flat[off:e], out,
-                           rows=rows, cols=cols, **hyper)
-            pos = e
-        plain(pos, n)
+            gap(pos, off)
+            table.append((off, rows, cols, out))
+            pos = off + rows * cols
+        gap(pos, n)
+        K.adamw_step_t(master, grad, m, v, flat, table, **hyper)
 
     def master_param(self, p: torch.Tensor) -> torch.Tensor:
         """fp32 master of ``p`` (``p`` itself when it is fp32)."""
