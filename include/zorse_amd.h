@@ -266,6 +266,23 @@ int zk_cast(const void* x, int x_dtype, void* y, int y_dtype, int64_t n,
 int zk_transpose(const void* src, int64_t ld_src, void* dst, int64_t ld_dst,
                  int64_t rows, int64_t cols, int dtype, zk_stream_t stream);
 
+/* Device -> pinned-host copy of `bytes` bytes (host_dst from hipHostMalloc,
+ * both pointers 16-byte aligned, both ranges inside their allocations;
+ * ZK_EINVAL / ZK_EALIGN otherwise), issued from at most `blocks` workgroups
+ * so that it leaves the CUs to the compute it overlaps.  Replaces the
+ * activation store of the reference's pipeline schedule,
+ * zorse_utils/pipeline_schedule_v2.py:127-136 (store_to_cpu_buffer: a
+ * non_blocking .to("cpu") into a pinned buffer on mem_copy_stream). */
+int zk_copy_to_host(void* host_dst, const void* src, int64_t bytes, int blocks,
+                    zk_stream_t stream);
+
+/* Pinned-host -> device copy, the same rules with the roles swapped.
+ * Replaces the activation load of the reference's pipeline schedule,
+ * zorse_utils/pipeline_schedule_v2.py:119-126 (load_from_cpu_buffer: a
+ * non_blocking .to(device) on mem_copy_stream). */
+int zk_copy_from_host(void* dst, const void* host_src, int64_t bytes, int blocks,
+                      zk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -101,6 +101,14 @@ def test_validation_codes(lib):
     assert lib.zk_gemm_swiglu(ctypes.c_void_p(24), 64, p, p, 64, p, p, 8, p, 8, None, 0, 8, 8, 64,
                               2, None) == -3
     assert lib.zk_gemm_swiglu(p, 32, p, p, 64, p, p, 8, p, 8, None, 0, 8, 8, 64, 2, None) == -1
+    # copy_to_host: negative size, zero size, null, block count, misaligned
+    assert lib.zk_copy_to_host(p, p, -1, 16, None) == -1
+    assert lib.zk_copy_to_host(None, None, 0, 16, None) == 0
+    assert lib.zk_copy_to_host(None, p, 64, 16, None) == -1
+    assert lib.zk_copy_to_host(p, p, 64, 0, None) == -1
+    assert lib.zk_copy_to_host(ctypes.c_void_p(24), p, 64, 16, None) == -3
+    assert lib.zk_copy_from_host(p, None, 64, 16, None) == -1
+    assert lib.zk_copy_from_host(p, ctypes.c_void_p(24), 64, 16, None) == -3
 
 
 def test_wrappers_reject_cpu_tensors():
@@ -281,4 +289,30 @@ def test_attention_cache_keys():
     c.put(o, lse)
     torch.autograd.graph.increment_version(w)       # weights stepped
     c.bind(x, w, w)
+    assert c.take() is None
+
+
+def test_attention_cache_token_keys():
+    """With a token set (the stage's host offload brings the input back in a
+    new device buffer) the key is the token, shape and weights: another
+    buffer with the same token hits, another token or stepped weights miss."""
+    from zorse_amd.layer import AttentionCache
+    c = AttentionCache()
+    w = torch.zeros(32)
+    o, lse = torch.ones(3), torch.zeros(3)
+    c.token = (1, 0)
+    c.bind(torch.randn(2, 8, 16), w, w)
+    c.put(o, lse)
+    c.bind(torch.randn(2, 8, 16), w, w)             # the input's round trip
+    hit = c.take()
+    assert hit is not None and hit[0] is o
+    c.put(o, lse)
+    c.token = (2, 0)                                # next step
+    c.bind(torch.randn(2, 8, 16), w, w)
+    assert c.take() is None
+    c.token = (1, 0)
+    c.bind(torch.randn(2, 8, 8), w, w)              # other shape
+    assert c.take() is None
+    torch.autograd.graph.increment_version(w)
+    c.bind(torch.randn(2, 8, 16), w, w)
     assert c.take() is None

@@ -448,3 +448,61 @@ def test_lm_head_cross_entropy_chunked(dev, dtype, V, chunk):
         assert abs(loss.item() - ref.item()) <= 1e-4 * abs(ref.item())
     assert_close(xd.grad, xr.grad, dtype, "dx")
     assert_close(wd.grad, wr.grad, dtype, "dW")
+
+
+@pytest.mark.parametrize("nbytes,blocks", [(16, 1), (1000003, 16), (32 << 20, 16),
+                                           (32 << 20, 1), (5 << 20, 64)])
+def test_copy_host_round_trip(dev, nbytes, blocks):
+    """zk_copy_to_host (the stage's D2H activation store, the reference's
+    store_to_cpu_buffer, zorse_utils/pipeline_schedule_v2.py:127-136) lands
+    every byte, ragged tails included, on a side stream."""
+    from zorse_amd import kernels as K
+    g = torch.Generator().manual_seed(nbytes % 997)
+    src_cpu = torch.randint(0, 256, (nbytes,), generator=g, dtype=torch.uint8)
+    src = src_cpu.to(dev)
+    dst = torch.full((nbytes,), 7, dtype=torch.uint8, pin_memory=True)
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        K.copy_to_host(dst, src, blocks=blocks)
+    side.synchronize()
+    assert torch.equal(dst, src_cpu)
+    # and back (the reference's load_from_cpu_buffer, pipeline_schedule_v2.py:119-126)
+    back = torch.zeros_like(src)
+    with torch.cuda.stream(side):
+        K.copy_from_host(back, dst, blocks=blocks)
+    side.synchronize()
+    assert torch.equal(back, src)
+    # a bf16 view round trip, as the stage stores layer inputs
+    x = torch.randn(64, 4096, generator=g).to(torch.bfloat16).to(dev)
+    h = torch.empty(x.shape, dtype=x.dtype, pin_memory=True)
+    K.copy_to_host(h, x, blocks=blocks)
+    torch.cuda.synchronize()
+    assert torch.equal(h, x.cpu())
+
+
+def test_copy_to_host_rejects(dev):
+    """Pageable destinations, device destinations and ranges past the end
+    of an allocation are refused before any launch."""
+    import ctypes
+    from zorse_amd import kernels as K
+    from zorse_amd._abi import lib
+    src = torch.zeros(4096, dtype=torch.uint8, device=dev)
+    pageable = torch.zeros(4096, dtype=torch.uint8)
+    pinned = torch.zeros(4096, dtype=torch.uint8, pin_memory=True)
+    L = lib()
+    assert L.zk_copy_to_host(ctypes.c_void_p(pageable.data_ptr()), ctypes.c_void_p(src.data_ptr()),
+                             4096, 16, None) == -1
+    assert L.zk_copy_to_host(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(src.data_ptr()),
+                             4096, 16, None) == -1
+    assert L.zk_copy_to_host(ctypes.c_void_p(pinned.data_ptr()), ctypes.c_void_p(src.data_ptr()),
+                             8192, 16, None) == -1
+    assert L.zk_copy_from_host(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(pageable.data_ptr()),
+                               4096, 16, None) == -1
+    assert L.zk_copy_from_host(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(pinned.data_ptr()),
+                               8192, 16, None) == -1
+    with pytest.raises(ValueError):
+        K.copy_to_host(pageable, src)
+    with pytest.raises(ValueError):
+        K.copy_from_host(src, pageable)
+    torch.cuda.synchronize()

@@ -358,6 +358,77 @@ def test_stage_recompute_attention_cache(dev):
         assert torch.equal(results["cached"][0][i], results["plain"][0][i])
 
 
+def test_stage_offload_inputs(dev):
+    """Host offload in recompute mode (the reference pipeline's CPU activation
+    buffers on mem_copy_stream, zorse_utils/pipeline_schedule_v2.py:119-136):
+    each layer input goes D2H to pinned memory in the forward and returns H2D
+    one layer ahead in the backward.  Over two steps the gradients and weights
+    are bit-identical to recompute without offload, and the attention cache
+    still hits across the round trip (one attention forward per layer)."""
+    from zorse_amd import layer as L
+    from zorse_amd.stage import StageRunner
+    kw = dict(hidden_size=256, num_attention_heads=2, intermediate_size=512, rope_theta=1e4)
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(15)
+    xs = [torch.randn(1, 256, 256, generator=g).to(dtype).to(dev) for _ in range(2)]
+    douts = [torch.randn(1, 256, 256, generator=g).to(dtype).to(dev) for _ in range(2)]
+    calls = {"n": 0}
+    real = L.K.attn_fwd
+
+    def counting(*a, **k):
+        calls["n"] += 1
+        return real(*a, **k)
+
+    results = {}
+    try:
+        L.K.attn_fwd = counting
+        for name, off in (("recompute", False), ("offload", True)):
+            layers = [_layer(kw, dev, param_dtype=dtype, seed=s) for s in (1, 2, 3)]
+            grads = {}
+            for i, l in enumerate(layers):
+                l.flat_param.register_post_accumulate_grad_hook(
+                    lambda p, i=i: grads.__setitem__(i, p.grad.detach().clone()))
+            runner = StageRunner(layers, lr=1e-4, recompute=True, cache_attention=True,
+                                 offload_inputs=off)
+            per_step = []
+            for x, dout in zip(xs, douts):
+                calls["n"] = 0
+                torch.cuda.synchronize()
+                before = torch.cuda.memory_allocated()
+                y = runner.forward(x)
+                torch.cuda.synchronize()
+                held = torch.cuda.memory_allocated() - before
+                runner.backward(y.detach(), dout)
+                del y
+                runner.wait_optimizer()
+                torch.cuda.synchronize()
+                per_step.append(({i: t.clone() for i, t in grads.items()}, calls["n"], held))
+            weights = [l.flat_param.detach().clone() for l in layers]
+            results[name] = (per_step, weights, runner)
+    finally:
+        L.K.attn_fwd = real
+    off = results["offload"][2]
+    # the first two inputs went to the host; the last layer's stays resident
+    assert len(off._host) == 2 and all(h.is_pinned() and h.device.type == "cpu"
+                                      for h in off._host)
+    assert [len(c) for c in off.attn_caches] == [0, 0, 0]
+    assert all(c.token is None for c in off.attn_caches)
+    nbytes = xs[0].numel() * xs[0].element_size()
+    for step in range(2):
+        (g_ref, n_ref, held_ref), (g_off, n_off, held_off) = (results["recompute"][0][step],
+                                                              results["offload"][0][step])
+        assert n_ref == 3 and n_off == 3, (n_ref, n_off)
+        # between the forwards the input of layer 1 lives on the host (layer 0's
+        # is the caller's tensor, layer 2's stays for the backward's start)
+        assert held_ref - held_off >= nbytes, (held_ref, held_off, nbytes)
+        for i in range(3):
+            assert torch.equal(g_off[i], g_ref[i]), (step, i)
+    for a, b in zip(results["offload"][1], results["recompute"][1]):
+        assert torch.equal(a, b)
+    with pytest.raises(ValueError):
+        StageRunner([_layer(kw, dev, param_dtype=dtype, seed=1)], offload_inputs=True)
+
+
 # ------------------------------------------------------------- llama_v2 block --
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

@@ -102,6 +102,8 @@ SIGNATURES = {
                                _ptr]),
     "zk_ce_bwd_chunk": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _f32, _int, _ptr]),
     "zk_transpose": (_int, [_ptr, _i64, _ptr, _i64, _i64, _i64, _int, _ptr]),
+    "zk_copy_to_host": (_int, [_ptr, _ptr, _i64, _int, _ptr]),
+    "zk_copy_from_host": (_int, [_ptr, _ptr, _i64, _int, _ptr]),
 }
 
 _lock = threading.Lock()

@@ -459,6 +459,37 @@ def transpose(src: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tenso
     return out
 
 
+def _host_copy_check(name, host, devt):
+    if host.device.type != "cpu" or not host.is_pinned():
+        raise ValueError(f"{name}: the host tensor must be pinned")
+    _require_contig("host tensor", host)
+    _require_contig("device tensor", devt)
+    nbytes = devt.numel() * devt.element_size()
+    if host.numel() * host.element_size() != nbytes:
+        raise ValueError(f"{name}: the tensors hold different numbers of bytes")
+    return nbytes
+
+
+def copy_to_host(dst: torch.Tensor, src: torch.Tensor, blocks: int = 16) -> torch.Tensor:
+    """dst (pinned host tensor) <- src (device tensor), both contiguous with
+    the same number of bytes, on the current stream from at most ``blocks``
+    workgroups."""
+    dev = _require_gpu(src)
+    nbytes = _host_copy_check("copy_to_host", dst, src)
+    check(lib().zk_copy_to_host(ptr(dst), ptr(src), nbytes, blocks, stream_handle(dev)),
+          "zk_copy_to_host")
+    return dst
+
+
+def copy_from_host(dst: torch.Tensor, src: torch.Tensor, blocks: int = 16) -> torch.Tensor:
+    """dst (device tensor) <- src (pinned host tensor), as copy_to_host."""
+    dev = _require_gpu(dst)
+    nbytes = _host_copy_check("copy_from_host", src, dst)
+    check(lib().zk_copy_from_host(ptr(dst), ptr(src), nbytes, blocks, stream_handle(dev)),
+          "zk_copy_from_host")
+    return dst
+
+
 def device_info(device: int = 0) -> dict:
     import ctypes
     arch = ctypes.create_string_buffer(64)

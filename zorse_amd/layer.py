@@ -269,30 +269,45 @@ class AttentionCache:
     attention kernel.  Entries are keyed by the input's storage address,
     offset, shape, strides and version counter plus the weights' address and
     version counters; an entry keeps the input's storage alive, so no other
-    tensor can take that address while the entry exists.  A forward whose key
-    has no entry computes attention and records it; an entry is removed when
-    it is used."""
+    tensor can take that address while the entry exists.  A caller that moves
+    the input between the two forwards (host offload) sets ``token`` to an
+    identifier of the micro-batch and layer instead.  A forward whose key has
+    no entry computes attention and records it; an entry is removed when it
+    is used."""
 
     def __init__(self):
         self._entries = {}
         self._key = None
         self._storage = None
+        # Set by a caller that moves the input between the two forwards (the
+        # stage runner's host offload): identifies the micro-batch and layer
+        # in place of the input's storage.
+        self.token = None
 
     def __len__(self):
         return len(self._entries)
 
     def clear(self):
         self._entries.clear()
+        self._key = self._storage = None
 
     def bind(self, x, flat_param, w_flat):
+        wkey = (flat_param._version, w_flat.data_ptr(), w_flat._version)
+        if self.token is not None:
+            self._storage = None
+            self._key = ("token", self.token, tuple(x.shape)) + wkey
+            return
         st = x.untyped_storage()
         self._storage = st
         self._key = (st.data_ptr(), x.storage_offset(), tuple(x.shape), tuple(x.stride()),
-                     x._version, flat_param._version, w_flat.data_ptr(), w_flat._version)
+                     x._version) + wkey
 
     def take(self):
         hit = self._entries.pop(self._key, None)
-        return None if hit is None else hit[1:]
+        if hit is None:
+            return None
+        self._storage = None  # the input's storage is no longer needed here
+        return hit[1:]
 
     def put(self, o, lse):
         self._entries[self._key] = (self._storage, o, lse)
