@@ -199,13 +199,13 @@ def repeat_kv(x: torch.Tensor, n_rep: int) -> torch.Tensor:
     return x[:, :, :, None, :].expand(B, S, H, n_rep, d).reshape(B, S, H * n_rep, d)
 
 
-def attn_mask(sq: int, skv: int, causal: bool, window: int) -> torch.Tensor:
+def attn_mask(sq: int, skv: int, causal: bool, window: int, device=None) -> torch.Tensor:
     """Boolean [Sq, Skv] visibility: causal keeps key j <= query i; a sliding
     window W additionally keeps j > i - W (W keys including self), the
     convention of HF's sliding-window mask (transformers masking_utils)."""
-    i = torch.arange(sq)[:, None]
-    j = torch.arange(skv)[None, :]
-    vis = torch.ones(sq, skv, dtype=torch.bool)
+    i = torch.arange(sq, device=device)[:, None]
+    j = torch.arange(skv, device=device)[None, :]
+    vis = torch.ones(sq, skv, dtype=torch.bool, device=device)
     if causal:
         vis &= j <= i
     if window and window > 0:
@@ -229,7 +229,7 @@ def attention(q, k, v, causal=True, window=0, scale=None):
     s = torch.matmul(qq, kk.transpose(-1, -2)) * scale
     acc = torch.float64 if q.dtype == torch.float64 else torch.float32
     s = s.to(acc)
-    vis = attn_mask(Sq, k.shape[1], causal, window)
+    vis = attn_mask(Sq, k.shape[1], causal, window, q.device)
     s = s.masked_fill(~vis, float("-inf"))
     lse = torch.logsumexp(s, dim=-1)
     p = torch.softmax(s, dim=-1)
@@ -251,7 +251,7 @@ def attention_bwd(q, k, v, do, causal=True, window=0, scale=None):
     qq = q.transpose(1, 2)
     dd = do.transpose(1, 2)
     s = torch.matmul(qq, kk.transpose(-1, -2)) * scale
-    vis = attn_mask(Sq, k.shape[1], causal, window)
+    vis = attn_mask(Sq, k.shape[1], causal, window, q.device)
     s = s.masked_fill(~vis, float("-inf"))
     p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)
     o = torch.matmul(p, vv)
@@ -309,9 +309,9 @@ def decoder_layer(x: torch.Tensor, p: dict[str, torch.Tensor], s: LayerShape,
     v = F.linear(n1, p["v"]).view(B, S, s.kv_heads, s.head_dim)
     if rope == "half":
         cos, sin = rope_cos_sin(S, s.head_dim, s.theta, x.dtype, positions)
-        q, k = apply_rope_half(q, k, cos, sin)
+        q, k = apply_rope_half(q, k, cos.to(x.device), sin.to(x.device))
     else:
-        q, k = apply_rope_interleaved(q, k, rope_freqs_cis(s.head_dim, S, s.theta))
+        q, k = apply_rope_interleaved(q, k, rope_freqs_cis(s.head_dim, S, s.theta).to(x.device))
     a, _ = attention(q, k, v, s.causal, s.window)
     hdn = x + F.linear(a.reshape(B, S, s.heads * s.head_dim), p["o"])
     n2 = rmsnorm(hdn, p["ln2"], s.eps)

@@ -3,7 +3,7 @@ AdamW-in-backward, against the oracle and the transformers golden fixtures.
 
 Layer configs are the BASELINE configs scaled down so the fp64 oracle
 finishes in seconds (same head_dim, GQA ratio, RoPE theta, dtype and mask
-kind); the full-size shapes are exercised by test_gpu_fullsize.py.
+kind); the full-size shapes are exercised by tests/test_gpu_fullsize.py.
 """
 import os
 
