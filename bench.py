@@ -94,7 +94,8 @@ class KernelCases:
     Cache.  ``copy`` is a plain device copy of 1 GiB (read 1 GiB, write
     1 GiB), the calibration for the FETCH_SIZE / WRITE_SIZE counters."""
 
-    NAMES = ("attn_fwd", "attn_bwd", "rmsnorm_fwd", "rmsnorm_bwd", "adamw", "adamw_t", "copy")
+    NAMES = ("attn_fwd", "attn_bwd", "rmsnorm_fwd", "rmsnorm_bwd", "adamw", "adamw_t", "copy",
+             "gemm_gu", "gemm_wgrad_gu")
 
     def __init__(self, dev, spec, S):
         self.dev, self.spec, self.S = dev, spec, S
@@ -179,6 +180,20 @@ class KernelCases:
                 K.adamw_step_t(p, gr, m, vv, lowp, regions, lr=1e-4, beta1=0.9, beta2=0.95,
                                eps=1e-8, weight_decay=0.1, step=step[0])
             return run, flops.adamw_bytes(n, 2, True) + 2 * n_t
+        if name in ("gemm_gu", "gemm_wgrad_gu"):
+            # the layer's largest projection GEMM as the stage runs it (hipBLASLt
+            # through torch.mm with the recorded solutions): forward gate|up =
+            # n2 [T, h] x W_gu^T, and its weight gradient dgu^T [2F, T] x n2^T^T
+            F2 = 2 * spec.ffn
+            a = torch.randn(T, h, device=dev, dtype=torch.bfloat16)
+            if name == "gemm_gu":
+                w = 0.02 * torch.randn(F2, h, device=dev, dtype=torch.bfloat16)
+                y = torch.empty(T, F2, device=dev, dtype=torch.bfloat16)
+                return (lambda: torch.mm(a, w.t(), out=y)), 2 * T * h * F2
+            dyt = torch.randn(F2, T, device=dev, dtype=torch.bfloat16)
+            at = a.t().contiguous()
+            dw = torch.empty(F2, h, device=dev, dtype=torch.bfloat16)
+            return (lambda: torch.mm(dyt, at.t(), out=dw)), 2 * T * h * F2
         if name == "copy":
             src = torch.empty(1 << 28, device=dev, dtype=torch.float32).normal_()
             dst = torch.empty_like(src)
@@ -188,7 +203,8 @@ class KernelCases:
 
 def measure_kernels(dev, spec, S):
     """Live HIP-event timings of the hand-written kernels at the stage's
-    shapes (see KernelCases)."""
+    shapes (see KernelCases), plus the layer's largest library GEMM as the
+    reference point for the MFMA-bound ones."""
     cases = KernelCases(dev, spec, S)
     rows = {}
     spec_of = {
@@ -199,6 +215,8 @@ def measure_kernels(dev, spec, S):
         "adamw": ("adamw_vec8<bf16,bf16,true>", "hbm", 10),
         "adamw_t": ("adamw_tile_t<bf16,bf16> (layer step with W^T copies)", "hbm", 10),
         "copy": ("device copy 1 GiB (HBM reference)", "hbm", 5),
+        "gemm_gu": ("hipBLASLt gate|up GEMM 4096 x 22016 x 4096 (reference point)", "mfma", 10),
+        "gemm_wgrad_gu": ("hipBLASLt gate|up weight-gradient GEMM (reference point)", "mfma", 10),
     }
     for name, (kname, bound, iters) in spec_of.items():
         run, work = cases.make(name)
@@ -251,6 +269,51 @@ TRAFFIC_CASES = {
     "adamw": ("adamw_vec8<bf16,bf16,true>", ("adamw_vec8",)),
     "adamw_t": ("adamw_tile_t<bf16,bf16> (layer step with W^T copies)", ("adamw_tile_t",)),
 }
+
+
+MFMA_COUNTERS = ("SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CYCLES",
+                 "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "GRBM_GUI_ACTIVE")
+
+
+def summarize_mfma(root: str) -> str:
+    """Markdown summary of one rocprofv3 ``--pmc`` pass of MFMA_COUNTERS per
+    MFMA-bound kernel case (``root/<case>/r_counter_collection.csv``):
+    executed MFMA FLOPs (MOPS x 512), the clock the kernel ran at
+    (GRBM_GUI_ACTIVE per XCC / duration), MFMA busy cycles per SIMD as a
+    fraction of the kernel's active cycles (rocprof's MfmaUtil), and LDS bank
+    conflicts per LDS access cycle."""
+    import collections
+    import csv
+    simds, xccs = 1024, 8
+    lines = ["| kernel | dispatches | avg duration (us) | clock (GHz) | MFMA FLOPs executed (GF) "
+             "| MFMA busy / active cycles | LDS conflict cycles / access cycles |",
+             "|---|---|---|---|---|---|---|"]
+    for case in ("attn_fwd", "attn_bwd", "gemm_gu", "gemm_wgrad_gu"):
+        path = os.path.join(root, case, "r_counter_collection.csv")
+        if not os.path.exists(path):
+            continue
+        disp, meta = collections.defaultdict(dict), {}
+        for r in csv.DictReader(open(path)):
+            d = int(r["Dispatch_Id"])
+            disp[d][r["Counter_Name"]] = float(r["Counter_Value"])
+            meta[d] = (r["Kernel_Name"], int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        groups = collections.defaultdict(list)
+        for d, c in disp.items():
+            name, dur = meta[d]
+            if c.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0) > 0:
+                groups[name.split("(")[0][:60]].append((dur, c))
+        for name, items in groups.items():
+            n = len(items)
+            dur = sum(t for t, _ in items) / n
+            avg = {k: sum(c[k] for _, c in items) / n for k in MFMA_COUNTERS}
+            cycles = avg["GRBM_GUI_ACTIVE"] / xccs
+            busy = avg["SQ_VALU_MFMA_BUSY_CYCLES"] / simds
+            lds = avg["SQ_LDS_IDX_ACTIVE"] - avg["SQ_LDS_BANK_CONFLICT"]
+            conf = avg["SQ_LDS_BANK_CONFLICT"] / lds if lds > 0 else 0.0
+            lines.append(f"| `{name}` ({case}) | {n} | {dur / 1e3:.1f} | {cycles / dur:.2f} "
+                         f"| {avg['SQ_INSTS_VALU_MFMA_MOPS_BF16'] * 512 / 1e9:.1f} "
+                         f"| {100 * busy / cycles:.1f} % | {conf:.3f} |")
+    return "\n".join(lines) + "\n"
 
 
 def summarize_traffic(root: str) -> str:
@@ -317,10 +380,15 @@ def main():
                     help="launch only this kernel case --steps times (for rocprofv3 --pmc)")
     ap.add_argument("--default-gemm", action="store_true",
                     help="use hipBLASLt's default solution heuristic instead of the recorded table")
+    ap.add_argument("--summarize-mfma", metavar="DIR",
+                    help="print the MFMA-counter summary of rocprofv3 runs under DIR and exit")
     ap.add_argument("--summarize-traffic", metavar="DIR",
                     help="print the HBM-traffic table from rocprofv3 --pmc runs of the kernel "
                          "cases under DIR and exit (no GPU needed)")
     args = ap.parse_args()
+    if args.summarize_mfma:
+        print(summarize_mfma(args.summarize_mfma), end="")
+        return
     if args.summarize_traffic:
         print(summarize_traffic(args.summarize_traffic), end="")
         return
