@@ -150,12 +150,14 @@ def test_gemm_swiglu_llama7b_shape(dev):
 
 # ------------------------------------------------------------------- RoPE --
 
+@pytest.mark.parametrize("heads", [(4, 2), (32, 8)])  # per-head and position-major kernels
 @pytest.mark.parametrize("d,theta", [(64, 5e5), (128, 1e4), (128, 1e6)])
 @pytest.mark.parametrize("dtype", ALL)
-def test_rope_half(dev, d, theta, dtype):
+def test_rope_half(dev, d, theta, dtype, heads):
     from zorse_amd import kernels as K
     from zorse_amd.functional import rope_tables
-    B, S, Hq, Hkv = 2, 77, 4, 2
+    B, S = 2, 77
+    Hq, Hkv = heads
     q = _rand((B, S, Hq, d), dtype, 10)
     k = _rand((B, S, Hkv, d), dtype, 11)
     cos, sin = rope_tables(S, d, theta, dtype, dev)

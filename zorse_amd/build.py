@@ -34,6 +34,13 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source extra flags.  rope.hip: with packed fp32 disabled, the SLP
+# vectoriser forms two-wide fp32 negations that this compiler cannot select
+# (a backend "Cannot select: v2f32 bitcast" crash in the position-major
+# kernel); the kernels there are memory-bound, so scalar code costs nothing.
+FILE_FLAGS = {"rope.hip": ["-fno-slp-vectorize"]}
+
+
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if cand and os.path.exists(cand):
@@ -69,7 +76,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
 
     def compile_one(pair):
         src, obj = pair
-        cmd = [hipcc, *HIPCC_FLAGS, "-c", src, "-o", obj]
+        cmd = [hipcc, *HIPCC_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src,
+               "-o", obj]
         if verbose:
             print(" ".join(cmd), file=sys.stderr)
         _run(cmd)

@@ -83,27 +83,11 @@ __global__ __launch_bounds__(256) void rope_kernel(
 // Vectorised path for head_dim 64 / 128 with 16-byte aligned rows: a thread
 // rotates 8 pairs with 16-byte accesses; the grid is (position blocks,
 // heads, batch), so no index arithmetic divides.
+// One thread's 8 pairs of one (position, head) row, 16-byte accesses.
 template <typename T, int D, int kPairing, bool kInverse>
-__global__ __launch_bounds__(256) void rope_vec_kernel(
-    T* __restrict__ q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
-    T* __restrict__ k, int64_t k_sb, int64_t k_ss, int64_t k_sh, int64_t S, int64_t Hq,
-    const float* __restrict__ cosT, const float* __restrict__ sinT, int64_t n_pos,
-    const int64_t* __restrict__ positions) {
+__device__ __forceinline__ void rope_chunk8(T* row, int i0, const float (&c)[8],
+                                            const float (&sn)[8]) {
   constexpr int HALF = D / 2;
-  constexpr int TPR = HALF / 8;        // threads per (position, head) row
-  constexpr int RPB = 256 / TPR;       // positions per workgroup
-  const int64_t s = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / TPR;
-  if (s >= S) return;
-  const int64_t h = blockIdx.y, b = blockIdx.z;
-  const int i0 = (threadIdx.x % TPR) * 8;  // first pair of this thread
-  T* row = h < Hq ? q + b * q_sb + s * q_ss + h * q_sh
-                  : k + b * k_sb + s * k_ss + (h - Hq) * k_sh;
-  int64_t pos = positions != nullptr ? positions[s] : s;
-  if (pos < 0) pos = 0;
-  if (pos >= n_pos) pos = n_pos - 1;
-  float c[8], sn[8];
-  Vec8<float>::load(cosT + pos * HALF + i0, c);
-  Vec8<float>::load(sinT + pos * HALF + i0, sn);
   float x1[8], x2[8], y1[8], y2[8];
   if (kPairing == ZK_ROPE_HALF) {
     Vec8<T>::load(row + i0, x1);
@@ -139,17 +123,84 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(
   }
 }
 
+// Vectorised path for head_dim 64 / 128 with 16-byte aligned rows and few
+// heads: a thread rotates 8 pairs of one row; the grid is (position blocks,
+// heads, batch), so no index arithmetic divides.
+template <typename T, int D, int kPairing, bool kInverse>
+__global__ __launch_bounds__(256) void rope_vec_kernel(
+    T* __restrict__ q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+    T* __restrict__ k, int64_t k_sb, int64_t k_ss, int64_t k_sh, int64_t S, int64_t Hq,
+    const float* __restrict__ cosT, const float* __restrict__ sinT, int64_t n_pos,
+    const int64_t* __restrict__ positions) {
+  constexpr int HALF = D / 2;
+  constexpr int TPR = HALF / 8;        // threads per (position, head) row
+  constexpr int RPB = 256 / TPR;       // positions per workgroup
+  const int64_t s = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / TPR;
+  if (s >= S) return;
+  const int64_t h = blockIdx.y, b = blockIdx.z;
+  const int i0 = (threadIdx.x % TPR) * 8;  // first pair of this thread
+  T* row = h < Hq ? q + b * q_sb + s * q_ss + h * q_sh
+                  : k + b * k_sb + s * k_ss + (h - Hq) * k_sh;
+  int64_t pos = positions != nullptr ? positions[s] : s;
+  if (pos < 0) pos = 0;
+  if (pos >= n_pos) pos = n_pos - 1;
+  float c[8], sn[8];
+  Vec8<float>::load(cosT + pos * HALF + i0, c);
+  Vec8<float>::load(sinT + pos * HALF + i0, sn);
+  rope_chunk8<T, D, kPairing, kInverse>(row, i0, c, sn);
+}
+
+// Position-major path for many heads: a workgroup rotates every q and k head
+// of one (batch, position) -- with heads contiguous in memory, one run of
+// (Hq + Hkv) d elements -- and each thread reads its cos / sin values once
+// (256 threads and HALF / 8 chunks per row: a thread's pair offset is the
+// same in every head it visits).
+template <typename T, int D, int kPairing, bool kInverse>
+__global__ __launch_bounds__(256) void rope_pos_kernel(
+    T* __restrict__ q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+    T* __restrict__ k, int64_t k_sb, int64_t k_ss, int64_t k_sh, int64_t Hq, int64_t H,
+    const float* __restrict__ cosT, const float* __restrict__ sinT, int64_t n_pos,
+    const int64_t* __restrict__ positions) {
+  constexpr int HALF = D / 2;
+  constexpr int CPH = HALF / 8;  // 8-pair chunks per head row
+  static_assert(256 % CPH == 0, "chunk offset must be fixed per thread");
+  const int64_t s = blockIdx.x, b = blockIdx.y;
+  const int i0 = (threadIdx.x % CPH) * 8;
+  int64_t pos = positions != nullptr ? positions[s] : s;
+  if (pos < 0) pos = 0;
+  if (pos >= n_pos) pos = n_pos - 1;
+  float c[8], sn[8];
+  Vec8<float>::load(cosT + pos * HALF + i0, c);
+  Vec8<float>::load(sinT + pos * HALF + i0, sn);
+  T* qrow = q + b * q_sb + s * q_ss;
+  T* krow = k != nullptr ? k + b * k_sb + s * k_ss : nullptr;
+  for (int64_t h = threadIdx.x / CPH; h < H; h += 256 / CPH) {
+    T* row = h < Hq ? qrow + h * q_sh : krow + (h - Hq) * k_sh;
+    rope_chunk8<T, D, kPairing, kInverse>(row, i0, c, sn);
+  }
+}
+
 template <typename T, int D>
 static void launch_rope_vec(int pairing, int inverse, void* q, int64_t q_sb, int64_t q_ss,
                             int64_t q_sh, void* k, int64_t k_sb, int64_t k_ss, int64_t k_sh,
                             int64_t B, int64_t S, int64_t Hq, int64_t Hkv, const float* c,
                             const float* sn, int64_t n_pos, const int64_t* pos, hipStream_t st) {
   constexpr int RPB = 256 / (D / 16);
-  const dim3 grid(static_cast<unsigned>((S + RPB - 1) / RPB),
-                  static_cast<unsigned>(Hq + (k != nullptr ? Hkv : 0)), static_cast<unsigned>(B));
-#define ZK_ROPEV(P, I)                                                                   \
-  hipLaunchKernelGGL((rope_vec_kernel<T, D, P, I>), grid, dim3(256), 0, st, (T*)q, q_sb,  \
-                     q_ss, q_sh, (T*)k, k_sb, k_ss, k_sh, S, Hq, c, sn, n_pos, pos)
+  const int64_t H = Hq + (k != nullptr ? Hkv : 0);
+  // position-major once a position's rows fill half a workgroup's threads
+  const bool by_pos = H * (D / 16) >= 128 && S < 0x7fffffff;
+  const dim3 grid = by_pos ? dim3(static_cast<unsigned>(S), static_cast<unsigned>(B))
+                           : dim3(static_cast<unsigned>((S + RPB - 1) / RPB),
+                                  static_cast<unsigned>(H), static_cast<unsigned>(B));
+#define ZK_ROPEV(P, I)                                                                       \
+  do {                                                                                       \
+    if (by_pos)                                                                              \
+      hipLaunchKernelGGL((rope_pos_kernel<T, D, P, I>), grid, dim3(256), 0, st, (T*)q, q_sb,  \
+                         q_ss, q_sh, (T*)k, k_sb, k_ss, k_sh, Hq, H, c, sn, n_pos, pos);     \
+    else                                                                                     \
+      hipLaunchKernelGGL((rope_vec_kernel<T, D, P, I>), grid, dim3(256), 0, st, (T*)q, q_sb,  \
+                         q_ss, q_sh, (T*)k, k_sb, k_ss, k_sh, S, Hq, c, sn, n_pos, pos);     \
+  } while (0)
   if (pairing == ZK_ROPE_HALF) {
     if (inverse) ZK_ROPEV(ZK_ROPE_HALF, true); else ZK_ROPEV(ZK_ROPE_HALF, false);
   } else {
