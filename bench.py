@@ -95,7 +95,7 @@ class KernelCases:
     1 GiB), the calibration for the FETCH_SIZE / WRITE_SIZE counters."""
 
     NAMES = ("attn_fwd", "attn_bwd", "rmsnorm_fwd", "rmsnorm_bwd", "adamw", "adamw_t", "copy",
-             "gemm_gu", "gemm_wgrad_gu")
+             "gemm_gu", "gemm_wgrad_gu", "rope")
 
     def __init__(self, dev, spec, S):
         self.dev, self.spec, self.S = dev, spec, S
@@ -180,6 +180,23 @@ class KernelCases:
                 K.adamw_step_t(p, gr, m, vv, lowp, regions, lr=1e-4, beta1=0.9, beta2=0.95,
                                eps=1e-8, weight_decay=0.1, step=step[0])
             return run, flops.adamw_bytes(n, 2, True) + 2 * n_t
+        if name == "rope":
+            # q and k rotated in place in the layer's q|k|v buffer (4 rotating
+            # buffers, 1.2 GB: outside the Infinity Cache); bytes: q and k read
+            # and written
+            from zorse_amd.functional import rope_tables
+            nbuf = 4
+            bufs = [torch.randn(T, 3 * H * d, device=dev, dtype=torch.bfloat16)
+                    for _ in range(nbuf)]
+            cos, sin = rope_tables(S, d, spec.rope_theta, torch.bfloat16, dev)
+            it = [0]
+
+            def run():
+                qkv = bufs[it[0] % nbuf]
+                it[0] += 1
+                K.rope_(qkv[:, :H * d].view(B, S, H, d), qkv[:, H * d:2 * H * d].view(B, S, H, d),
+                        cos, sin)
+            return run, 2 * 2 * T * H * d * 2
         if name in ("gemm_gu", "gemm_wgrad_gu"):
             # the layer's largest projection GEMM as the stage runs it (hipBLASLt
             # through torch.mm with the recorded solutions): forward gate|up =
@@ -214,6 +231,7 @@ def measure_kernels(dev, spec, S):
         "rmsnorm_bwd": ("rmsnorm_bwd_vec<bf16,bf16,256,2,2> + dw reduce", "hbm", 32),
         "adamw": ("adamw_vec8<bf16,bf16,true>", "hbm", 10),
         "adamw_t": ("adamw_tile_t<bf16,bf16> (layer step with W^T copies)", "hbm", 10),
+        "rope": ("rope_pos_kernel<bf16,128,half> (q and k of the q|k|v buffer)", "hbm", 20),
         "copy": ("device copy 1 GiB (HBM reference)", "hbm", 5),
         "gemm_gu": ("hipBLASLt gate|up GEMM 4096 x 22016 x 4096 (reference point)", "mfma", 10),
         "gemm_wgrad_gu": ("hipBLASLt gate|up weight-gradient GEMM (reference point)", "mfma", 10),

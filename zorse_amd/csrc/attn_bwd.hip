@@ -96,6 +96,35 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_vec(AttnArgs a) {
   }
 }
 
+// Position-major variant for many heads: a workgroup takes every q-head row
+// of one (batch, query) -- with heads contiguous, one run of Hq d elements of
+// O and of dO -- D / 8 lanes per row, 256 / (D / 8) rows per pass.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_bwd_prep_pos(AttnArgs a) {
+  constexpr int LPR = D / 8;
+  constexpr int RPP = 256 / LPR;  // head rows per pass
+  const int64_t q = blockIdx.x, b = blockIdx.y;
+  const int sub = threadIdx.x % LPR;
+  const T* Ob = static_cast<const T*>(a.o) + b * a.o_sb + q * a.o_ss + 8 * sub;
+  const T* Db = static_cast<const T*>(a.dout) + b * a.o_sb + q * a.o_ss + 8 * sub;
+  for (int64_t h = threadIdx.x / LPR; h < a.Hq; h += RPP) {
+    float ov[8], dv[8];
+    Vec8<T>::load(Ob + h * a.o_sh, ov);
+    Vec8<T>::load(Db + h * a.o_sh, dv);
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = fmaf(ov[e], dv[e], acc);
+#pragma unroll
+    for (int off = 1; off < LPR; off <<= 1) acc += __shfl_xor(acc, off, 64);
+    if (sub == 0) {
+      const int64_t i = (b * a.Hq + h) * a.Sq + q;
+      a.delta[i] = acc;
+      const float l = a.lse[i];
+      a.lse2[i] = l == -INFINITY ? INFINITY : l * kLog2e;
+    }
+  }
+}
+
 // ------------------------------------------------------------- dK / dV -----
 template <int D>
 struct DkdvCfg {
@@ -638,7 +667,11 @@ extern "C" int zk_attn_bwd(const zk_attn_desc* desc, const void* q,
   const bool k_full = desc->Skv % DqCfg<128>::BN == 0;
 #define ZK_BWD(T, D)                                                                        \
   do {                                                                                      \
-    if (rows > 0 && desc->B * desc->Hq <= 65535) {                                          \
+    if (rows > 0 && desc->Hq * (D / 8) >= 128 && desc->B <= 65535 &&                    \
+        desc->Sq < 0x7fffffff) {                                                            \
+      const dim3 pos_grid(static_cast<unsigned>(desc->Sq), static_cast<unsigned>(desc->B)); \
+      hipLaunchKernelGGL((attn_bwd_prep_pos<T, D>), pos_grid, dim3(256), 0, s, a);         \
+    } else if (rows > 0 && desc->B * desc->Hq <= 65535) {                                   \
       const dim3 vgrid(static_cast<unsigned>((desc->Sq + 256 / (D / 8) - 1) / (256 / (D / 8))), \
                        static_cast<unsigned>(desc->B * desc->Hq));                          \
       hipLaunchKernelGGL((attn_bwd_prep_vec<T, D>), vgrid, dim3(256), 0, s, a);            \
