@@ -43,9 +43,11 @@ def recorded_traffic(kernel: str):
     try:
         with open(TRAFFIC_FILE) as f:
             for line in f:
-                parts = line.split()
-                if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
-                    return int(parts[2])
+                # "traffic_bytes_per_launch <kernel name, may contain spaces> <bytes>"
+                head, _, rest = line.strip().partition(" ")
+                name, _, value = rest.rpartition(" ")
+                if head == "traffic_bytes_per_launch" and name == kernel and value.isdigit():
+                    return int(value)
     except OSError:
         return None
     return None

@@ -316,3 +316,22 @@ def test_attention_cache_token_keys():
     torch.autograd.graph.increment_version(w)
     c.bind(torch.randn(2, 8, 16), w, w)
     assert c.take() is None
+
+
+def test_bench_reads_recorded_traffic():
+    """bench.py's roofline `traffic` comes from the committed rocprofv3
+    summary; every kernel it reports an HBM roofline for (names with spaces
+    included) must be found there."""
+    import bench
+    names = {
+        "adamw_tile_t<bf16,bf16> (layer step with W^T copies)": 6_071_484_416,
+        "adamw_vec8<bf16,bf16,true>": 5_666_734_080,
+        "rmsnorm_bwd_vec<bf16,bf16,256,2,2> + dw reduce": 100_683_776,
+        "zk_attn_bwd (prep + attn_bwd_dkdv + attn_bwd_dq)": None,
+    }
+    for name, algorithmic in names.items():
+        t = bench.recorded_traffic(name)
+        assert isinstance(t, int) and t > 0, name
+        if algorithmic:
+            assert 0.95 * algorithmic <= t <= 1.5 * algorithmic, (name, t)
+    assert bench.recorded_traffic("no such kernel") is None
