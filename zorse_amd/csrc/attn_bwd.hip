@@ -3,10 +3,11 @@
 // Three kernels, all on the caller's stream:
 //  1. attn_bwd_prep: delta[b,h,i] = sum_d dO[i,d] * O[i,d] (fp32).
 //  2. attn_bwd_dkdv: KV-stationary.  A workgroup owns 128 keys of one
-//     (batch, kv-head) -- 32 keys per wave, that wave's K and V rows held in
-//     registers as MFMA B operands -- and loops over 64-query blocks of every
-//     q-head in the GQA group (the group reduction of dK / dV happens in the
-//     accumulators; repeat_kv is never materialised).  Per block:
+//     (batch, kv-head) -- 32 keys per wave, that wave's K rows held in
+//     registers and its V rows in LDS as MFMA B operands -- and loops over
+//     32-query blocks of every q-head in the GQA group (the group reduction of
+//     dK / dV happens in the accumulators; repeat_kv is never materialised).
+//     Within 256 registers, two workgroups share a CU.  Per block:
 //       S  = Q K^T,  dP = dO V^T      (A = Q / dO rows from LDS)
 //       P  = exp2(S scale log2e - lse log2e),  dS = P (dP - delta)
 //       dV^T += dO^T P,  dK^T += Q^T dS
@@ -129,22 +130,25 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_pos(AttnArgs a) {
 template <int D>
 struct DkdvCfg {
   static constexpr int BK = 128;              // keys per workgroup (32 per wave)
-  static constexpr int MQ = 64;               // queries per block
+  static constexpr int MQ = 32;               // queries per block
   static constexpr int MB = MQ / 32;          // 32-row MFMA blocks per query block
 };
 
 // kFull: Sq is a multiple of the query block, so no block runs past the end.
 template <typename T, int D, bool kFull>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
+__global__ __launch_bounds__(256, 2) void attn_bwd_dkdv(AttnArgs a) {
   typedef DkdvCfg<D> C;
   typedef Mfma<T> M;
   typedef typename M::vec8 V8;
   constexpr int BK = C::BK, MQ = C::MQ;
   // Q / dO tiles double-buffered (swizzled rows); each wave keeps its own copy
   // of the block's lse2 / delta vectors so every wave issues the same loads.
-  __shared__ __attribute__((aligned(16))) T Qs[2][MQ * D];
-  __shared__ __attribute__((aligned(16))) T dOs[2][MQ * D];
+  // Q / dO tiles of the two stages in one array (stage st: Q at 2 st, dO at
+  // 2 st + 1), so every LDS operand address is a per-lane offset plus an immediate
+  __shared__ __attribute__((aligned(16))) T QD[4][MQ * D];
   __shared__ __attribute__((aligned(16))) float lse2s[2][4][64];  // 64 lanes load, MQ used
+  // V rows of each wave's 32 keys (the B operand of dP), swizzled like the tiles
+  __shared__ __attribute__((aligned(16))) T Vw[4][32 * D];
   __shared__ __attribute__((aligned(16))) float dels[2][4][64];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -178,17 +182,22 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
   const T* Kp = static_cast<const T*>(a.k) + b * a.k_sb + hk * a.k_sh;
   const T* Vp = static_cast<const T*>(a.v) + b * a.v_sb + hk * a.v_sh;
 
-  // B operands of S = Q K^T and dP = dO V^T: lane holds row my_key.
-  V8 kreg[D / 16], vreg[D / 16];
+  // B operands of S = Q K^T and dP = dO V^T: lane holds row my_key.  K stays
+  // in registers; V goes to this wave's LDS rows (read back per step), which
+  // keeps the kernel within 256 registers (two waves per SIMD).
+  V8 kreg[D / 16];
+  T* Vme = Vw[wave];
 #pragma unroll
   for (int ks = 0; ks < D / 16; ++ks) {
+    V8 vv;
     if (my_key < a.Skv) {
       kreg[ks] = *reinterpret_cast<const V8*>(Kp + my_key * a.k_ss + 16 * ks + 8 * g);
-      vreg[ks] = *reinterpret_cast<const V8*>(Vp + my_key * a.v_ss + 16 * ks + 8 * g);
+      vv = *reinterpret_cast<const V8*>(Vp + my_key * a.v_ss + 16 * ks + 8 * g);
     } else {
       kreg[ks] = V8{};
-      vreg[ks] = V8{};
+      vv = V8{};
     }
+    *reinterpret_cast<V8*>(&Vme[tile_off<D>(l32, 16 * ks + 8 * g)]) = vv;
   }
 
   f32x16 dk[D / 32], dv[D / 32];
@@ -196,6 +205,19 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
   for (int nt = 0; nt < D / 32; ++nt) {
     dk[nt] = f32x16{};
     dv[nt] = f32x16{};
+  }
+  // byte offsets of this lane's transposed-read chunks (ds_read_tr16_b64) for
+  // the 16-query step kk = 0: per 32-column block, keys 4 g .. and 8 + 4 g ..;
+  // step kk adds kk * 16 rows
+  int troff[D / 32][2];
+  {
+    const int q = lane & 15, G = lane >> 4;
+#pragma unroll
+    for (int nt = 0; nt < D / 32; ++nt) {
+      const int col = 32 * nt + 16 * (G & 1) + 4 * (q & 3);
+      troff[nt][0] = 2 * tile_off<D>(4 * g + (q >> 2), col);
+      troff[nt][1] = 2 * tile_off<D>(8 + 4 * g + (q >> 2), col);
+    }
   }
 
   // queries that can see keys [k0, k0 + BK)
@@ -217,13 +239,25 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
     const int64_t qb0 = qbi * MQ;
     const T* Qp = static_cast<const T*>(a.q) + b * a.q_sb + hq * a.q_sh;
     const T* Dp = static_cast<const T*>(a.dout) + b * a.o_sb + hq * a.o_sh;
-    qload.issue(Qs[st], Qp, a.q_ss, qb0, a.Sq, kFull);
-    dload.issue(dOs[st], Dp, a.o_ss, qb0, a.Sq, kFull);
+    qload.issue(QD[2 * st], Qp, a.q_ss, qb0, a.Sq, kFull);
+    dload.issue(QD[2 * st + 1], Dp, a.o_ss, qb0, a.Sq, kFull);
     int64_t qi = qb0 + lane;
     if (qi > a.Sq - 1) qi = a.Sq - 1;
     const int64_t ri = (b * a.Hq + hq) * a.Sq + qi;
     __builtin_amdgcn_global_load_lds((gmem_void*)(a.lse2 + ri), (lds_void*)&lse2s[st][wave][0], 4, 0, 0);
     __builtin_amdgcn_global_load_lds((gmem_void*)(a.delta + ri), (lds_void*)&dels[st][wave][0], 4, 0, 0);
+  };
+
+  // transposed MFMA operand of tile X for 16-query step kk (see lds_tr_operand)
+  auto tr_at = [&](const T* X, const int (&off)[2], int kk) __attribute__((always_inline)) {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    const char* base = reinterpret_cast<const char*>(X) + kk * 16 * D * 2;
+    const s16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off[0]));
+    const s16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off[1]));
+    const s16x8 w = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+    return __builtin_bit_cast(V8, w);
   };
 
   // One pipeline step on LDS stage ST (compile-time: immediate LDS offsets).
@@ -245,8 +279,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
       if (kw0 <= qb0 + MQ - 1 - a.window) need_mask = true;
     }
     if (skip) return;
-    const T* Qt = Qs[st];
-    const T* dOt = dOs[st];
+    const T* Qt = QD[2 * st];
+    const T* dOt = QD[2 * st + 1];
     const float* l2v = lse2s[st][wave];
     const float* dlv = dels[st][wave];
     const int qb32 = static_cast<int>(qb0);
@@ -260,7 +294,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
         const V8 qa = *reinterpret_cast<const V8*>(&Qt[tile_off<D>(32 * mb + l32, 16 * ks + 8 * g)]);
         sv = M::mma(qa, kreg[ks], sv);
         const V8 da = *reinterpret_cast<const V8*>(&dOt[tile_off<D>(32 * mb + l32, 16 * ks + 8 * g)]);
-        dpv = M::mma(da, vreg[ks], dpv);
+        const V8 vb = *reinterpret_cast<const V8*>(&Vme[tile_off<D>(l32, 16 * ks + 8 * g)]);
+        dpv = M::mma(da, vb, dpv);
       }
     };
     // P and dS of half mb, packed as the B operands of two 16-query MFMA steps;
@@ -293,30 +328,23 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs a) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int kk = 2 * mb + h;
-        const int klo = 16 * kk + 4 * g, khi = 16 * kk + 8 + 4 * g;
 #pragma unroll
         for (int nt = 0; nt < D / 32; ++nt) {
-          const V8 dA = lds_tr_operand<T, D>(dOt, 32 * nt, klo, khi);
+          const V8 dA = tr_at(dOt, troff[nt], kk);
           dv[nt] = M::mma(dA, pb[h], dv[nt]);
-          const V8 qA = lds_tr_operand<T, D>(Qt, 32 * nt, klo, khi);
+          const V8 qA = tr_at(Qt, troff[nt], kk);
           dk[nt] = M::mma(qA, sb[h], dk[nt]);
         }
       }
     };
-    // Both halves in one straight-line block: the VALU work of one half can
-    // be issued between MFMAs that do not depend on it.
+    // One 32-query block per step; the other wave on the SIMD (two
+    // workgroups per CU) covers this wave's VALU and LDS latencies.
     auto body = [&](auto mask_tag) {
-      f32x16 s0, dp0, s1, dp1;
-      V8 pb0[2], sb0[2], pb1[2], sb1[2];
+      f32x16 s0, dp0;
+      V8 pb0[2], sb0[2];
       scores(0, s0, dp0);
-      scores(1, s1, dp1);
       probs(mask_tag, 0, s0, dp0, pb0, sb0);
       accumulate(0, pb0, sb0);
-      probs(mask_tag, 1, s1, dp1, pb1, sb1);
-      accumulate(1, pb1, sb1);
-      // single-wave MFMA / LDS / VALU interleaving strategy of the compiler's
-      // instruction-group scheduler (one wave per SIMD runs this kernel)
-      __builtin_amdgcn_iglp_opt(1);
     };
     if (need_mask)
       body(std::true_type{});
