@@ -143,9 +143,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv(AttnArgs a) {
   constexpr int BK = C::BK, MQ = C::MQ;
   // Q / dO tiles double-buffered (swizzled rows); each wave keeps its own copy
   // of the block's lse2 / delta vectors so every wave issues the same loads.
-  // Q / dO tiles of the two stages in one array (stage st: Q at 2 st, dO at
-  // 2 st + 1), so every LDS operand address is a per-lane offset plus an immediate
-  __shared__ __attribute__((aligned(16))) T QD[4][MQ * D];
+  // Q / dO tiles of the two stages, each its own array: the compiler then sees
+  // that the next stage's asynchronous loads do not alias this stage's reads
+  // (and adds no wait for them)
+  __shared__ __attribute__((aligned(16))) T Q0[MQ * D], Q1[MQ * D], dO0[MQ * D], dO1[MQ * D];
   __shared__ __attribute__((aligned(16))) float lse2s[2][4][64];  // 64 lanes load, MQ used
   // V rows of each wave's 32 keys (the B operand of dP), swizzled like the tiles
   __shared__ __attribute__((aligned(16))) T Vw[4][32 * D];
@@ -206,19 +207,17 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv(AttnArgs a) {
     dk[nt] = f32x16{};
     dv[nt] = f32x16{};
   }
-  // byte offsets of this lane's transposed-read chunks (ds_read_tr16_b64) for
-  // the 16-query step kk = 0: per 32-column block, keys 4 g .. and 8 + 4 g ..;
-  // step kk adds kk * 16 rows
-  int troff[D / 32][2];
-  {
-    const int q = lane & 15, G = lane >> 4;
-#pragma unroll
-    for (int nt = 0; nt < D / 32; ++nt) {
-      const int col = 32 * nt + 16 * (G & 1) + 4 * (q & 3);
-      troff[nt][0] = 2 * tile_off<D>(4 * g + (q >> 2), col);
-      troff[nt][1] = 2 * tile_off<D>(8 + 4 * g + (q >> 2), col);
-    }
-  }
+  // LDS byte offsets, derived on the fly from two per-lane bases (the swizzle
+  // XORs chunk indices, and a row's chunk bits never overlap its row bits, so
+  // moving to another chunk is an XOR by a constant):
+  //  * row reads of this lane's row l32, chunk 2 ks + g: rbase ^ (ks << 5);
+  //  * transposed reads (ds_read_tr16_b64) of 32-column block nt for the
+  //    16-query step kk = 0: keys 4 g .. at tbase ^ (nt << 6), keys 8 + 4 g ..
+  //    at that ^ 32 (their swizzle differs by 2 chunks) plus 8 rows.
+  // Two registers instead of one per operand slot keep the kernel within 256.
+  static_assert(MQ == 32, "one 32-row block per step");
+  const int rbase = 2 * tile_off<D>(l32, 8 * g);
+  const int tbase = 2 * tile_off<D>(4 * g + ((lane & 15) >> 2), 16 * ((lane >> 4) & 1) + 4 * (lane & 3));
 
   // queries that can see keys [k0, k0 + BK)
   int64_t q_lo = 0, q_hi = a.Sq;
@@ -239,8 +238,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv(AttnArgs a) {
     const int64_t qb0 = qbi * MQ;
     const T* Qp = static_cast<const T*>(a.q) + b * a.q_sb + hq * a.q_sh;
     const T* Dp = static_cast<const T*>(a.dout) + b * a.o_sb + hq * a.o_sh;
-    qload.issue(QD[2 * st], Qp, a.q_ss, qb0, a.Sq, kFull);
-    dload.issue(QD[2 * st + 1], Dp, a.o_ss, qb0, a.Sq, kFull);
+    qload.issue(st ? Q1 : Q0, Qp, a.q_ss, qb0, a.Sq, kFull);
+    dload.issue(st ? dO1 : dO0, Dp, a.o_ss, qb0, a.Sq, kFull);
     int64_t qi = qb0 + lane;
     if (qi > a.Sq - 1) qi = a.Sq - 1;
     const int64_t ri = (b * a.Hq + hq) * a.Sq + qi;
@@ -249,13 +248,14 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv(AttnArgs a) {
   };
 
   // transposed MFMA operand of tile X for 16-query step kk (see lds_tr_operand)
-  auto tr_at = [&](const T* X, const int (&off)[2], int kk) __attribute__((always_inline)) {
+  auto tr_at = [&](const T* X, int off, int kk) __attribute__((always_inline)) {
     typedef short s16x4 __attribute__((ext_vector_type(4)));
     typedef short s16x8 __attribute__((ext_vector_type(8)));
     typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
     const char* base = reinterpret_cast<const char*>(X) + kk * 16 * D * 2;
-    const s16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off[0]));
-    const s16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off[1]));
+    const s16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off));
+    const s16x4 x1 =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + 8 * D * 2 + (off ^ 32)));
     const s16x8 w = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
     return __builtin_bit_cast(V8, w);
   };
@@ -279,8 +279,12 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv(AttnArgs a) {
       if (kw0 <= qb0 + MQ - 1 - a.window) need_mask = true;
     }
     if (skip) return;
-    const T* Qt = QD[2 * st];
-    const T* dOt = QD[2 * st + 1];
+    const T* Qt = st ? Q1 : Q0;
+    const T* dOt = st ? dO1 : dO0;
+    // opaque per-step copies of the bases: the addresses derived from them are
+    // recomputed in the step instead of being kept live across the loop
+    int rb = rbase, tb = tbase;
+    asm volatile("" : "+v"(rb), "+v"(tb));
     const float* l2v = lse2s[st][wave];
     const float* dlv = dels[st][wave];
     const int qb32 = static_cast<int>(qb0);
@@ -291,10 +295,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv(AttnArgs a) {
       dpv = f32x16{};
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
-        const V8 qa = *reinterpret_cast<const V8*>(&Qt[tile_off<D>(32 * mb + l32, 16 * ks + 8 * g)]);
+        const int ro = rb ^ (ks << 5);
+        const V8 qa = *reinterpret_cast<const V8*>(reinterpret_cast<const char*>(Qt) + ro);
         sv = M::mma(qa, kreg[ks], sv);
-        const V8 da = *reinterpret_cast<const V8*>(&dOt[tile_off<D>(32 * mb + l32, 16 * ks + 8 * g)]);
-        const V8 vb = *reinterpret_cast<const V8*>(&Vme[tile_off<D>(l32, 16 * ks + 8 * g)]);
+        const V8 da = *reinterpret_cast<const V8*>(reinterpret_cast<const char*>(dOt) + ro);
+        const V8 vb = *reinterpret_cast<const V8*>(reinterpret_cast<const char*>(Vme) + ro);
         dpv = M::mma(da, vb, dpv);
       }
     };
@@ -330,9 +335,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv(AttnArgs a) {
         const int kk = 2 * mb + h;
 #pragma unroll
         for (int nt = 0; nt < D / 32; ++nt) {
-          const V8 dA = tr_at(dOt, troff[nt], kk);
+          const V8 dA = tr_at(dOt, tb ^ (nt << 6), kk);
           dv[nt] = M::mma(dA, pb[h], dv[nt]);
-          const V8 qA = tr_at(Qt, troff[nt], kk);
+          const V8 qA = tr_at(Qt, tb ^ (nt << 6), kk);
           dk[nt] = M::mma(qA, sb[h], dk[nt]);
         }
       }
