@@ -55,8 +55,9 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
   typedef Mfma<T> M;
   typedef typename M::vec8 V8;
   constexpr int BM = C::BM, BN = C::BN;
-  __shared__ __attribute__((aligned(16))) T Ks[2][BN * D];
-  __shared__ __attribute__((aligned(16))) T Vs[2][BN * D];
+  // each stage its own array: the compiler then sees that the next tile's
+  // asynchronous loads do not alias this tile's reads (and adds no wait)
+  __shared__ __attribute__((aligned(16))) T K0[BN * D], K1[BN * D], V0[BN * D], V1[BN * D];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, g = lane >> 5;
@@ -95,9 +96,16 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
   kload.init(a.k_ss);
   vload.init(a.v_ss);
   auto issue = [&](int64_t k0, int st) {
-    kload.issue(Ks[st], Kp, a.k_ss, k0, a.Skv, kFull);
-    vload.issue(Vs[st], Vp, a.v_ss, k0, a.Skv, kFull);
+    kload.issue(st ? K1 : K0, Kp, a.k_ss, k0, a.Skv, kFull);
+    vload.issue(st ? V1 : V0, Vp, a.v_ss, k0, a.Skv, kFull);
   };
+  // LDS byte offsets from two per-lane bases (the swizzle XORs chunk indices,
+  // and a row's chunk bits never overlap its row bits): K row l32 + 32 tt,
+  // chunk 2 ks + g at (rbase ^ (ks << 5)) + tt rows; the transposed V reads
+  // of 32-column block nt, keys 16 kk + 4 g .. at (tbase ^ (nt << 6)) + kk
+  // rows and keys 16 kk + 8 + 4 g .. at that ^ 32 plus 8 rows
+  const int rbase = 2 * tile_off<D>(l32, 8 * g);
+  const int tbase = 2 * tile_off<D>(4 * g + ((lane & 15) >> 2), 16 * ((lane >> 4) & 1) + 4 * (lane & 3));
 
   f32x16 o[D / 32];
 #pragma unroll
@@ -129,8 +137,11 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
     wait_vmcnt<0>();  // this wave's loads of tile t have landed
     __syncthreads();  // ... and every other wave's; all are done with the other stage
     if (t + 1 < t_hi) issue(k0 + BN, st ^ 1);
-    const T* Kt = Ks[st];
-    const T* Vt = Vs[st];
+    const T* Kt = st ? K1 : K0;
+    const T* Vt = st ? V1 : V0;
+    // opaque per-step copies: the derived addresses are recomputed in the step
+    int rb = rbase, tb = tbase;
+    asm volatile("" : "+v"(rb), "+v"(tb));
 
     // wave-uniform tile classification
     bool skip = false, need_mask = k0 + BN > a.Skv;
@@ -157,7 +168,8 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
         s[tt] = f32x16{};
 #pragma unroll
         for (int ks = 0; ks < D / 16; ++ks) {
-          const V8 kv = *reinterpret_cast<const V8*>(&Kt[tile_off<D>(32 * tt + l32, 16 * ks + 8 * g)]);
+          const V8 kv = *reinterpret_cast<const V8*>(reinterpret_cast<const char*>(Kt) +
+                                                     (rb ^ (ks << 5)) + tt * 32 * D * 2);
           s[tt] = M::mma(kv, qreg[ks], s[tt]);
         }
       }
@@ -206,11 +218,18 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
       // O^T += V^T P^T (V^T read transposed from the row-major V tile)
 #pragma unroll
       for (int kk = 0; kk < BN / 16; ++kk) {
-        const int klo = 16 * kk + 4 * g, khi = 16 * kk + 8 + 4 * g;
 #pragma unroll
         for (int nt = 0; nt < D / 32; ++nt) {
-          const V8 vA = lds_tr_operand<T, D>(Vt, 32 * nt, klo, khi);
-          o[nt] = M::mma(vA, pb[kk], o[nt]);
+          typedef short s16x4 __attribute__((ext_vector_type(4)));
+          typedef short s16x8 __attribute__((ext_vector_type(8)));
+          typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+          const char* vb = reinterpret_cast<const char*>(Vt) + kk * 16 * D * 2;
+          const int off = tb ^ (nt << 6);
+          const s16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + off));
+          const s16x4 x1 =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + 8 * D * 2 + (off ^ 32)));
+          const s16x8 w = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+          o[nt] = M::mma(__builtin_bit_cast(V8, w), pb[kk], o[nt]);
         }
       }
     };
