@@ -416,8 +416,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) 
   typedef Mfma<T> M;
   typedef typename M::vec8 V8;
   constexpr int BM = C::BM, BN = C::BN;
-  __shared__ __attribute__((aligned(16))) T Ks[2][BN * D];  // swizzled rows
-  __shared__ __attribute__((aligned(16))) T Vs[2][BN * D];
+  // swizzled rows; each stage its own array, so the compiler sees that the
+  // next tile's asynchronous loads do not alias this tile's reads
+  __shared__ __attribute__((aligned(16))) T K0[BN * D], K1[BN * D], V0[BN * D], V1[BN * D];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, g = lane >> 5;
@@ -479,9 +480,15 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) 
   kload.init(a.k_ss);
   vload.init(a.v_ss);
   auto issue = [&](int64_t kb0, int st) {
-    kload.issue(Ks[st], Kp, a.k_ss, kb0, a.Skv, kFull);
-    vload.issue(Vs[st], Vp, a.v_ss, kb0, a.Skv, kFull);
+    kload.issue(st ? K1 : K0, Kp, a.k_ss, kb0, a.Skv, kFull);
+    vload.issue(st ? V1 : V0, Vp, a.v_ss, kb0, a.Skv, kFull);
   };
+  // LDS byte offsets from two per-lane bases, as in the dK/dV kernel: row
+  // l32 + 32 tt, chunk 2 ks + g at (rbase ^ (ks << 5)) + tt rows; transposed
+  // K reads of block nt at (tbase ^ (nt << 6)) + kk rows (keys 4 g ..) and at
+  // that ^ 32 plus 8 rows (keys 8 + 4 g ..)
+  const int rbase = 2 * tile_off<D>(l32, 8 * g);
+  const int tbase = 2 * tile_off<D>(4 * g + ((lane & 15) >> 2), 16 * ((lane >> 4) & 1) + 4 * (lane & 3));
 
   f32x16 dq[D / 32];
 #pragma unroll
@@ -505,8 +512,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) 
       if (kb0 <= qw0 + 31 - a.window) need_mask = true;
     }
     if (skip) return;
-    const T* Kt = Ks[st];
-    const T* Vt = Vs[st];
+    const T* Kt = st ? K1 : K0;
+    const T* Vt = st ? V1 : V0;
+    int rb = rbase, tb = tbase;  // opaque per-step copies (addresses derived in the step)
+    asm volatile("" : "+v"(rb), "+v"(tb));
 
     // S^T and dP^T: block tt covers keys kb0 + 32 tt .. +31
     f32x16 s[BN / 32], dp[BN / 32];
@@ -516,9 +525,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) 
       dp[tt] = f32x16{};
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
-        const V8 kA = *reinterpret_cast<const V8*>(&Kt[tile_off<D>(32 * tt + l32, 16 * ks + 8 * g)]);
+        const int ro = (rb ^ (ks << 5)) + tt * 32 * D * 2;
+        const V8 kA = *reinterpret_cast<const V8*>(reinterpret_cast<const char*>(Kt) + ro);
         s[tt] = M::mma(kA, qreg[ks], s[tt]);
-        const V8 vA = *reinterpret_cast<const V8*>(&Vt[tile_off<D>(32 * tt + l32, 16 * ks + 8 * g)]);
+        const V8 vA = *reinterpret_cast<const V8*>(reinterpret_cast<const char*>(Vt) + ro);
         dp[tt] = M::mma(vA, dreg[ks], dp[tt]);
       }
     }
@@ -538,11 +548,18 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) 
     // dQ^T += K^T dS^T  (K^T read transposed from the row-major K tile)
 #pragma unroll
     for (int kk = 0; kk < BN / 16; ++kk) {
-      const int klo = 16 * kk + 4 * g, khi = 16 * kk + 8 + 4 * g;
 #pragma unroll
       for (int nt = 0; nt < D / 32; ++nt) {
-        const V8 kA = lds_tr_operand<T, D>(Kt, 32 * nt, klo, khi);
-        dq[nt] = M::mma(kA, sb[kk], dq[nt]);
+        typedef short s16x4 __attribute__((ext_vector_type(4)));
+        typedef short s16x8 __attribute__((ext_vector_type(8)));
+        typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+        const char* kb = reinterpret_cast<const char*>(Kt) + kk * 16 * D * 2;
+        const int off = tb ^ (nt << 6);
+        const s16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(kb + off));
+        const s16x4 x1 =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(kb + 8 * D * 2 + (off ^ 32)));
+        const s16x8 w = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        dq[nt] = M::mma(__builtin_bit_cast(V8, w), sb[kk], dq[nt]);
       }
     }
   };
