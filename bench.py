@@ -231,7 +231,7 @@ def measure_kernels(dev, spec, S):
         "attn_bwd": ("zk_attn_bwd (prep + attn_bwd_dkdv + attn_bwd_dq)", "mfma", 10),
         "rmsnorm_fwd": ("rmsnorm_fwd_vec<bf16,bf16,128,4>", "hbm", 32),
         "rmsnorm_bwd": ("rmsnorm_bwd_vec<bf16,bf16,256,2,2> + dw reduce", "hbm", 32),
-        "adamw": ("adamw_vec8<bf16,bf16,true>", "hbm", 10),
+        "adamw": ("adamw_elem<bf16,bf16,true>", "hbm", 10),
         "adamw_t": ("adamw_tile_t<bf16,bf16> (layer step with W^T copies)", "hbm", 10),
         "rope": ("rope_pos_kernel<bf16,128,half> (q and k of the q|k|v buffer)", "hbm", 20),
         "copy": ("device copy 1 GiB (HBM reference)", "hbm", 5),
@@ -286,7 +286,7 @@ TRAFFIC_CASES = {
     "rmsnorm_fwd": ("rmsnorm_fwd_vec<bf16,bf16,128,4>", ("rmsnorm_fwd_vec",)),
     "rmsnorm_bwd": ("rmsnorm_bwd_vec<bf16,bf16,256,2,2> + dw reduce",
                     ("rmsnorm_bwd_vec", "rmsnorm_dw_reduce")),
-    "adamw": ("adamw_vec8<bf16,bf16,true>", ("adamw_vec8",)),
+    "adamw": ("adamw_elem<bf16,bf16,true>", ("adamw_elem",)),
     "adamw_t": ("adamw_tile_t<bf16,bf16> (layer step with W^T copies)", ("adamw_tile_t",)),
 }
 

@@ -325,7 +325,7 @@ def test_bench_reads_recorded_traffic():
     import bench
     names = {
         "adamw_tile_t<bf16,bf16> (layer step with W^T copies)": 6_071_484_416,
-        "adamw_vec8<bf16,bf16,true>": 5_666_734_080,
+        "adamw_elem<bf16,bf16,true>": 5_666_734_080,
         "rmsnorm_bwd_vec<bf16,bf16,256,2,2> + dw reduce": 100_683_776,
         "zk_attn_bwd (prep + attn_bwd_dkdv + attn_bwd_dq)": None,
     }

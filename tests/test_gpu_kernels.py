@@ -351,6 +351,7 @@ def test_adamw_step_transposed_copy(dev, rows, cols, gdt, ldt):
         assert torch.equal(x[cov], y[cov]), what
         assert torch.equal(y[~cov], x0.to(dev)[~cov]), what + " outside the regions"
     assert torch.equal(low[cov], lowt[cov])
+    assert torch.equal(lowt[cov], pt[cov].to(ldt))   # the copy is the rounded master
     assert torch.equal(lowt[~cov], torch.zeros(64, dtype=ldt, device=dev))
     assert torch.equal(t1, lowt[:a].view(rows, cols).t())
     assert torch.equal(t2, lowt[a:2 * a].view(cols, rows).t())

@@ -2,10 +2,16 @@
 //
 // One pass over HBM: read p, g, m, v; write p, m, v (and the low-precision
 // compute copy of p when requested).  28 bytes per element with an fp32
-// grad, 26 with a bf16/fp16 grad, +2 for the low-precision copy.  Each thread
-// handles 8 consecutive elements per iteration (16-byte accesses on every
-// stream) in a grid-stride loop sized to keep every CU busy with several
-// workgroups; a scalar kernel finishes unaligned heads and ragged tails.
+// grad, 26 with a bf16/fp16 grad, +2 for the low-precision copy.
+//
+// The flat kernel accesses every stream one element per lane (4-byte, or
+// 2-byte for 16-bit types, accesses; 256 consecutive bytes of fp32 per wave
+// and instruction).  Measured on gfx950 over a 202M-element shard, one
+// element per thread ran at 78 % of the HBM peak, two at 72 % and four or
+// eight (16-byte accesses per lane) at 66-68 %.  The region kernel below
+// keeps 16-byte accesses: its one-element-per-lane form was slower alone
+// (63-64 %) and, run beside the attention backward as the stage runs it,
+// cost 2.3 ms per 8-layer step.
 #include <cmath>
 
 #include "zk_common.h"
@@ -81,9 +87,9 @@ __device__ __forceinline__ float adam_one(float& p, float g, float& m, float& v,
   return p;
 }
 
-// 8 elements per thread per iteration: p, m, v as two 16-byte accesses each,
-// the gradient and the low-precision copy as one 16-byte access for 2-byte
-// types (two for fp32).  L = float with kCopy = false means "no copy".
+// 8 elements per thread (the region kernel): p, m, v as two 16-byte accesses
+// each, the gradient and the low-precision copy as one 16-byte access for
+// 2-byte types.
 template <typename G>
 __device__ __forceinline__ void load_grad8(const G* g, int64_t i, float (&o)[8]) {
   float a[4], b[4];
@@ -128,52 +134,28 @@ __device__ __forceinline__ void store8<f16>(f16* dst, const float4& x, const flo
   *reinterpret_cast<f16x8*>(dst) = a;
 }
 
+// One element per thread, 256 consecutive elements per workgroup, no loop.
+// L = float with kCopy = false means "no copy".
 template <typename G, typename L, bool kCopy>
-__global__ __launch_bounds__(256) void adamw_vec8(
-    float* __restrict__ p, const G* __restrict__ g, float* __restrict__ m,
-    float* __restrict__ v, L* __restrict__ lowp, int64_t n8, AdamScalars s) {
-  // R groups of 8 elements per thread, R * 256 consecutive groups per
-  // workgroup; all R groups' loads are issued before any arithmetic.
-  constexpr int R = 2;
-  const int64_t q0 = static_cast<int64_t>(blockIdx.x) * (256 * R) + threadIdx.x;
-  float4 pa[R][2], ma[R][2], va[R][2];
-  float gv[R][8];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int64_t q = q0 + 256 * r;
-    if (q < n8) {
-      const int64_t i = q * 8;
-      pa[r][0] = *reinterpret_cast<const float4*>(p + i);
-      pa[r][1] = *reinterpret_cast<const float4*>(p + i + 4);
-      ma[r][0] = *reinterpret_cast<const float4*>(m + i);
-      ma[r][1] = *reinterpret_cast<const float4*>(m + i + 4);
-      va[r][0] = *reinterpret_cast<const float4*>(v + i);
-      va[r][1] = *reinterpret_cast<const float4*>(v + i + 4);
-      load_grad8<G>(g, i, gv[r]);
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int64_t q = q0 + 256 * r;
-    if (q >= n8) break;
-    const int64_t i = q * 8;
-    float4 &p0 = pa[r][0], &p1 = pa[r][1], &m0 = ma[r][0], &m1 = ma[r][1];
-    float4 &v0 = va[r][0], &v1 = va[r][1];
-    adam_one(p0.x, gv[r][0], m0.x, v0.x, s);
-    adam_one(p0.y, gv[r][1], m0.y, v0.y, s);
-    adam_one(p0.z, gv[r][2], m0.z, v0.z, s);
-    adam_one(p0.w, gv[r][3], m0.w, v0.w, s);
-    adam_one(p1.x, gv[r][4], m1.x, v1.x, s);
-    adam_one(p1.y, gv[r][5], m1.y, v1.y, s);
-    adam_one(p1.z, gv[r][6], m1.z, v1.z, s);
-    adam_one(p1.w, gv[r][7], m1.w, v1.w, s);
-    *reinterpret_cast<float4*>(p + i) = p0;
-    *reinterpret_cast<float4*>(p + i + 4) = p1;
-    *reinterpret_cast<float4*>(m + i) = m0;
-    *reinterpret_cast<float4*>(m + i + 4) = m1;
-    *reinterpret_cast<float4*>(v + i) = v0;
-    *reinterpret_cast<float4*>(v + i + 4) = v1;
-    if (kCopy) store8<L>(lowp + i, p0, p1);
+__global__ __launch_bounds__(256) void adamw_elem(float* __restrict__ p,
+                                                  const G* __restrict__ g,
+                                                  float* __restrict__ m,
+                                                  float* __restrict__ v,
+                                                  L* __restrict__ lowp, int64_t n,
+                                                  AdamScalars s) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  float pv = p[i], mv = m[i], vv = v[i];
+  adam_one(pv, static_cast<float>(g[i]), mv, vv, s);
+  p[i] = pv;
+  m[i] = mv;
+  v[i] = vv;
+  if (kCopy) {
+    // round the stored fp32 value: left fused, the last fma would feed
+    // v_fma_mix, which rounds the exact result to 16 bits in one step and
+    // in rare cases differs from rounding the fp32 master
+    asm volatile("" : "+v"(pv));
+    lowp[i] = static_cast<L>(pv);
   }
 }
 
@@ -285,43 +267,21 @@ __global__ __launch_bounds__(256) void adamw_tile_t(
   }
 }
 
-// groups of 8 elements one workgroup of adamw_vec8 covers
-static constexpr int64_t kAdamGroupsPerBlock = 512;
-
-// Any alignment / tail: one element per thread, dtypes by runtime code.
-__global__ __launch_bounds__(256) void adamw_scalar(
-    float* __restrict__ p, const void* __restrict__ g, int gdt,
-    float* __restrict__ m, float* __restrict__ v, void* __restrict__ lowp,
-    int ldt, int64_t begin, int64_t n, AdamScalars s) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t i = begin + static_cast<int64_t>(blockIdx.x) * blockDim.x +
-                   threadIdx.x;
-       i < n; i += stride) {
-    float pv = p[i], mv = m[i], vv = v[i];
-    adam_one(pv, load_dt(g, i, gdt), mv, vv, s);
-    p[i] = pv;
-    m[i] = mv;
-    v[i] = vv;
-    if (lowp != nullptr) store_dt(lowp, i, ldt, pv);
-  }
+template <typename G, typename L, bool kCopy>
+static void launch_elem(float* p, const void* g, float* m, float* v, void* lowp, int64_t n,
+                        const AdamScalars& s, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+  hipLaunchKernelGGL((adamw_elem<G, L, kCopy>), grid, dim3(256), 0, st, p,
+                     static_cast<const G*>(g), m, v, static_cast<L*>(lowp), n, s);
 }
 
 template <typename G>
-static void launch_vec(float* p, const void* g, float* m, float* v, void* lowp,
-                       int ldt, int64_t n8, const AdamScalars& s, int grid,
-                       hipStream_t st) {
-  if (lowp == nullptr)
-    hipLaunchKernelGGL((adamw_vec8<G, float, false>), dim3(grid), dim3(256), 0,
-                       st, p, (const G*)g, m, v, (float*)nullptr, n8, s);
-  else if (ldt == ZK_BF16)
-    hipLaunchKernelGGL((adamw_vec8<G, bf16, true>), dim3(grid), dim3(256), 0,
-                       st, p, (const G*)g, m, v, (bf16*)lowp, n8, s);
-  else if (ldt == ZK_F16)
-    hipLaunchKernelGGL((adamw_vec8<G, f16, true>), dim3(grid), dim3(256), 0,
-                       st, p, (const G*)g, m, v, (f16*)lowp, n8, s);
-  else
-    hipLaunchKernelGGL((adamw_vec8<G, float, true>), dim3(grid), dim3(256), 0,
-                       st, p, (const G*)g, m, v, (float*)lowp, n8, s);
+static void launch_flat(float* p, const void* g, float* m, float* v, void* lowp, int ldt,
+                        int64_t n, const AdamScalars& s, hipStream_t st) {
+  if (lowp == nullptr) launch_elem<G, float, false>(p, g, m, v, nullptr, n, s, st);
+  else if (ldt == ZK_BF16) launch_elem<G, bf16, true>(p, g, m, v, lowp, n, s, st);
+  else if (ldt == ZK_F16) launch_elem<G, f16, true>(p, g, m, v, lowp, n, s, st);
+  else launch_elem<G, float, true>(p, g, m, v, lowp, n, s, st);
 }
 
 static AdamScalars adam_scalars(double lr, double beta1, double beta2, double eps,
@@ -364,35 +324,19 @@ extern "C" int zk_adamw_step(float* param, const void* grad, int grad_dtype,
   if (n == 0) return ZK_OK;
   const AdamScalars s = adam_scalars(lr, beta1, beta2, eps, weight_decay, step);
 
+  ZK_REQUIRE(aligned(param, 4) && aligned(exp_avg, 4) && aligned(exp_avg_sq, 4) &&
+                 aligned(grad, dtype_bytes(grad_dtype)) &&
+                 (param_lowp == nullptr || aligned(param_lowp, dtype_bytes(lowp_dtype))),
+             ZK_EALIGN, "zk_adamw_step: operands must be aligned to their element size");
+  ZK_REQUIRE((n + 255) / 256 <= 0x7fffffffLL, ZK_EINVAL, "zk_adamw_step: shard too large (%lld)",
+             (long long)n);
   hipStream_t st = as_stream(stream);
-  const int gbytes = dtype_bytes(grad_dtype);
-  const bool vec = aligned(param, 16) && aligned(exp_avg, 16) &&
-                   aligned(exp_avg_sq, 16) && aligned(grad, 4 * gbytes) &&
-                   aligned(grad, 16) &&
-                   (param_lowp == nullptr || aligned(param_lowp, 16));
-  const int64_t n8 = vec ? n / 8 : 0;
-  const int max_grid = device_cus() * 16;
-  if (n8 > 0) {
-    // every group covered by exactly one thread (no grid-stride loop)
-    const int64_t want = (n8 + kAdamGroupsPerBlock - 1) / kAdamGroupsPerBlock;
-    ZK_REQUIRE(want < 0x7fffffff, ZK_EINVAL, "zk_adamw_step: shard too large (%lld)",
-               (long long)n);
-    const int grid = static_cast<int>(want);
-    if (grad_dtype == ZK_F32)
-      launch_vec<float>(param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_dtype, n8, s, grid, st);
-    else if (grad_dtype == ZK_BF16)
-      launch_vec<bf16>(param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_dtype, n8, s, grid, st);
-    else
-      launch_vec<f16>(param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_dtype, n8, s, grid, st);
-  }
-  const int64_t begin = n8 * 8;
-  if (begin < n) {
-    int64_t want = (n - begin + 255) / 256;
-    const int grid = static_cast<int>(want < max_grid ? want : max_grid);
-    hipLaunchKernelGGL(adamw_scalar, dim3(grid), dim3(256), 0, st, param, grad,
-                       grad_dtype, exp_avg, exp_avg_sq, param_lowp, lowp_dtype,
-                       begin, n, s);
-  }
+  if (grad_dtype == ZK_F32)
+    launch_flat<float>(param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_dtype, n, s, st);
+  else if (grad_dtype == ZK_BF16)
+    launch_flat<bf16>(param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_dtype, n, s, st);
+  else
+    launch_flat<f16>(param, grad, exp_avg, exp_avg_sq, param_lowp, lowp_dtype, n, s, st);
   return launch_status("zk_adamw_step");
 }
 
