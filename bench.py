@@ -159,7 +159,7 @@ class KernelCases:
                              weight_decay=0.1, step=step[0], lowp_out=lowp)
             return run, flops.adamw_bytes(n, 2, True)
         if name == "adamw_t":
-            # the step as the stage runs it: one launch over the layer's four
+            # zk_adamw_step_t's region kernel: one launch over the layer's four
             # projection matrices (each also written transposed) and the norms
             n, o, sp = spec.numel, spec.offsets(), spec
             p = torch.randn(n, device=dev)
@@ -464,8 +464,9 @@ def main():
     print("kernel timings done", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline(spec, S)
     # the dominant hand-written kernel of the step (by time): the AdamW pass as
-    # the stage runs it (one tiled launch per layer, writing W^T copies too)
-    a = kern["adamw_t"]
+    # the stage runs it (one flat launch per layer step over the layer's shard;
+    # the W^T copies are transposed out of its compute copy afterwards)
+    a = kern["adamw"]
     af, ab = kern["attn_fwd"], kern["attn_bwd"]
     line = {
         "metric": "decoder-layer fwd+bwd tokens/s at 1 GPU; attention TFLOP/s vs MFMA peak",
