@@ -218,7 +218,9 @@ int zk_adamw_step(float* param, const void* grad, int grad_dtype,
  * grad_output @ W of the nn.Linear projections, models/llama_simple.py:
  * 206-221, 293-295, 368 and the MLP at :418), kept current by the optimizer
  * step that already rewrites the compute copy.  Offsets, rows, cols, ld_t
- * multiples of 8; 16-byte aligned buffers. */
+ * multiples of 8; 16-byte aligned buffers; n = the shard's element count
+ * (param, grad, exp_avg, exp_avg_sq and param_lowp each hold n elements):
+ * a region that ends past n is rejected (ZK_EINVAL). */
 typedef struct zk_adamw_region {
   int64_t offset, rows, cols, ld_t;
   void* lowp_t;
@@ -226,7 +228,7 @@ typedef struct zk_adamw_region {
 int zk_adamw_step_t(float* param, const void* grad, int grad_dtype,
                     float* exp_avg, float* exp_avg_sq, void* param_lowp,
                     int lowp_dtype, const zk_adamw_region* regions, int n_regions,
-                    double lr, double beta1, double beta2, double eps,
+                    int64_t n, double lr, double beta1, double beta2, double eps,
                     double weight_decay, int64_t step, zk_stream_t stream);
 
 /* ------------------------------------------------- LM head cross-entropy --

@@ -101,16 +101,10 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     return w * h.to(x.dtype)
 
 
-def rmsnorm_v2(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
-    """torchtitan RMSNorm (models/llama_v2.py:41-47): same value with eps 1e-5
-    by default; _norm in fp32, type_as(x), then * w."""
-    acc = torch.float64 if x.dtype == torch.float64 else torch.float32
-    h = x.to(acc)
-    out = (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)).type_as(x)
-    return out * w
-
-
 def rmsnorm_rstd(x: torch.Tensor, eps: float) -> torch.Tensor:
+    """The per-row factor rsqrt(mean(x^2) + eps) of rmsnorm (HF LlamaRMSNorm's
+    ``torch.rsqrt(variance + eps)``), fp32 (fp64 for fp64 input): the value the
+    GPU forward saves for the backward."""
     acc = torch.float64 if x.dtype == torch.float64 else torch.float32
     return torch.rsqrt(x.to(acc).pow(2).mean(-1) + eps)
 
@@ -267,10 +261,91 @@ def attention_bwd(q, k, v, do, causal=True, window=0, scale=None):
     return dq.transpose(1, 2), dk, dv
 
 
+def flash_attention_lowp(q, k, v, causal=True, window=0, scale=None):
+    """Attention with the rounding points of the flash kernels the reference
+    runs for its bf16 / fp16 layers (HF LlamaFlashAttention2 -> flash-attn, or
+    LlamaSdpaAttention -> SDPA's flash backend, chosen at
+    models/llama_simple.py:396-416; FlashAttention-2, Dao 2023):
+      forward  S = scale Q K^T and the softmax in fp32; the unnormalised
+               probabilities exp(S - rowmax) rounded to the storage dtype for
+               the P V product (fp32 accumulation), divided by the fp32 row sum,
+               O rounded;
+      backward P = exp(S - lse) in fp32; dV = round(P)^T dO; dP = dO V^T;
+               dS = P (dP - rowsum(dO o O)) rounded to the storage dtype for
+               dQ = scale dS K and dK = scale dS^T Q (fp32 accumulation);
+               with GQA each query head's dK / dV is rounded and the group is
+               then summed (flash-attn's dk_expanded sum, or the autograd of
+               repeat_kv on the SDPA path).
+    Q/K/V in a 16-bit dtype (fp32 / fp64 inputs: no rounding at all, i.e.
+    ``attention``).  Differentiable; returns O only."""
+    return _FlashLowp.apply(q, k, v, bool(causal), int(window or 0), scale)
+
+
+def _round(t, dtype):
+    return t.to(dtype).to(t.dtype)
+
+
+class _FlashLowp(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, causal, window, scale):
+        dt = q.dtype
+        acc = torch.float64 if dt == torch.float64 else torch.float32
+        B, Sq, Hq, d = q.shape
+        Hkv = k.shape[2]
+        sc = 1.0 / math.sqrt(d) if scale is None else scale
+        kk = repeat_kv(k, Hq // Hkv).transpose(1, 2).to(acc)
+        vv = repeat_kv(v, Hq // Hkv).transpose(1, 2).to(acc)
+        qq = q.transpose(1, 2).to(acc)
+        s = torch.matmul(qq, kk.transpose(-1, -2).contiguous()) * sc
+        vis = attn_mask(Sq, k.shape[1], causal, window, q.device)
+        s = s.masked_fill(~vis, float("-inf"))
+        m = s.amax(-1, keepdim=True)
+        m = torch.where(torch.isfinite(m), m, torch.zeros_like(m))
+        p = torch.exp(s - m)
+        lsum = p.sum(-1, keepdim=True)
+        o = torch.matmul(_round(p, dt), vv) / torch.where(lsum > 0, lsum, torch.ones_like(lsum))
+        lse = (m + torch.log(lsum)).squeeze(-1)
+        out = o.transpose(1, 2).to(dt)
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.cfg = (causal, window, sc)
+        return out
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, out, lse = ctx.saved_tensors
+        causal, window, sc = ctx.cfg
+        dt = q.dtype
+        acc = torch.float64 if dt == torch.float64 else torch.float32
+        B, Sq, Hq, d = q.shape
+        Skv, Hkv = k.shape[1], k.shape[2]
+        n_rep = Hq // Hkv
+        kk = repeat_kv(k, n_rep).transpose(1, 2).to(acc)
+        vv = repeat_kv(v, n_rep).transpose(1, 2).to(acc)
+        qq = q.transpose(1, 2).to(acc)
+        dd = do.to(dt).transpose(1, 2).to(acc)
+        s = torch.matmul(qq, kk.transpose(-1, -2).contiguous()) * sc
+        vis = attn_mask(Sq, Skv, causal, window, q.device)
+        p = torch.exp(s - lse[..., None]).masked_fill(~vis, 0.0)
+        del s
+        dv = torch.matmul(_round(p, dt).transpose(-1, -2).contiguous(), dd)
+        dp = torch.matmul(dd, vv.transpose(-1, -2).contiguous())
+        delta = (dd * out.transpose(1, 2).to(acc)).sum(-1, keepdim=True)
+        ds = _round(p * (dp - delta), dt)
+        del p, dp
+        dq = (torch.matmul(ds, kk) * sc).transpose(1, 2).to(dt)
+        dk = torch.matmul(ds.transpose(-1, -2).contiguous(), qq) * sc
+        # per-query-head gradients in the storage dtype, then the group sum
+        dk = dk.to(dt).to(acc).view(B, Hkv, n_rep, Skv, d).sum(2).transpose(1, 2).to(dt)
+        dv = dv.to(dt).to(acc).view(B, Hkv, n_rep, Skv, d).sum(2).transpose(1, 2).to(dt)
+        return dq, dk, dv, None, None, None
+
+
 # -------------------------------------------------------------------- MLP --
 
 def silu(x: torch.Tensor) -> torch.Tensor:
-    return x * torch.sigmoid(x)
+    """ACT2FN["silu"] of HF LlamaMLP (nn.SiLU): x * sigmoid(x), one rounding
+    in a 16-bit dtype."""
+    return F.silu(x)
 
 
 def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
@@ -294,37 +369,54 @@ def mlp(x, wg, wu, wd):
 # ------------------------------------------------------------------ layer --
 
 def decoder_layer(x: torch.Tensor, p: dict[str, torch.Tensor], s: LayerShape,
-                  rope: str = "half", positions: torch.Tensor | None = None) -> torch.Tensor:
+                  rope: str = "half", positions: torch.Tensor | None = None,
+                  attn: str = "eager") -> torch.Tensor:
     """LlamaDecoderLayer.forward (models/llama_simple.py:456-479):
         h   = x + o_proj(Attn(RoPE(q_proj(n1)), RoPE(k_proj(n1)), v_proj(n1)))
         out = h + down(silu(gate(n2)) * up(n2)),   n1 = RMSNorm1(x), n2 = RMSNorm2(h)
     with the attention of a-7 (causal, optional sliding window, GQA).  The
     Mistral layer (HF MistralDecoderLayer via models/mistral_simple.py:13-41)
     is the same composition.  rope="interleaved" uses the llama_v2 pairing
-    (models/llama_v2.py:151-177, TransformerBlock :328-399)."""
+    (models/llama_v2.py:151-177, TransformerBlock :328-399).  attn="flash"
+    takes the attention through flash_attention_lowp (the flash kernels'
+    rounding points; the same value in fp32 / fp64).  ``positions``: int64
+    [S] token positions for RoPE (default 0 .. S-1)."""
     B, S, h = x.shape
-    n1 = rmsnorm(x, p["ln1"], s.eps)
+    T = B * S
+    n1 = rmsnorm(x, p["ln1"], s.eps).reshape(T, h)
     q = F.linear(n1, p["q"]).view(B, S, s.heads, s.head_dim)
     k = F.linear(n1, p["k"]).view(B, S, s.kv_heads, s.head_dim)
     v = F.linear(n1, p["v"]).view(B, S, s.kv_heads, s.head_dim)
     if rope == "half":
-        cos, sin = rope_cos_sin(S, s.head_dim, s.theta, x.dtype, positions)
+        cos, sin = rope_cos_sin(S, s.head_dim, s.theta, x.dtype,
+                                None if positions is None else positions.cpu())
         q, k = apply_rope_half(q, k, cos.to(x.device), sin.to(x.device))
     else:
         q, k = apply_rope_interleaved(q, k, rope_freqs_cis(s.head_dim, S, s.theta).to(x.device))
-    a, _ = attention(q, k, v, s.causal, s.window)
-    hdn = x + F.linear(a.reshape(B, S, s.heads * s.head_dim), p["o"])
-    n2 = rmsnorm(hdn, p["ln2"], s.eps)
-    return hdn + mlp(n2, p["gate"], p["up"], p["down"])
+    if attn == "flash":
+        a = flash_attention_lowp(q, k, v, s.causal, s.window)
+    else:
+        a, _ = attention(q, k, v, s.causal, s.window)
+    hdn = x + F.linear(a.reshape(T, s.heads * s.head_dim), p["o"]).view(B, S, h)
+    n2 = rmsnorm(hdn, p["ln2"], s.eps).reshape(T, h)
+    return hdn + mlp(n2, p["gate"], p["up"], p["down"]).view(B, S, h)
 
 
-def layer_fwd_bwd(x, p, s: LayerShape, dout, rope: str = "half"):
+def layer_fwd_bwd(x, p, s: LayerShape, dout, rope: str = "half", attn: str = "eager",
+                  positions: torch.Tensor | None = None):
     """Output, input gradient and parameter gradients of decoder_layer via
     autograd (the reference's backward is torch autograd over the same graph,
-    models/llama_simple.py:456-479).  Returns (out, dx, {name: grad})."""
+    models/llama_simple.py:456-479).  Returns (out, dx, {name: grad}).
+
+    With x, p and dout in bf16 / fp16 and attn="flash" this is the layer as
+    plain PyTorch computes it at that precision -- the reference's own bf16 /
+    fp16 layer up to GEMM summation order: every op rounds to the storage
+    dtype where the reference's does (RMSNorm's fp32 upcast, bf16 RoPE
+    tables, nn.SiLU, the residual adds) and attention has the flash kernels'
+    rounding points."""
     xr = x.detach().clone().requires_grad_(True)
     pr = {k: t.detach().clone().requires_grad_(True) for k, t in p.items()}
-    out = decoder_layer(xr, pr, s, rope)
+    out = decoder_layer(xr, pr, s, rope, positions=positions, attn=attn)
     out.backward(dout)
     return out.detach(), xr.grad, {k: t.grad for k, t in pr.items()}
 

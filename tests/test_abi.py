@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_error_text(lib):
-    assert lib.zk_abi_version() >= 1
+    assert lib.zk_abi_version() == 2
     rc = lib.zk_rmsnorm_fwd(None, None, None, None, None, None, 4, 8, 1e-6, 7, 0, None)
     assert rc == -2  # ZK_EDTYPE
     assert b"dtype" in lib.zk_last_error()
@@ -88,13 +88,18 @@ def test_validation_codes(lib):
     # adamw_step_t: overlapping regions, rows not a multiple of 8, too many regions
     R = _abi.AdamwRegion * 2
     regs = R(_abi.AdamwRegion(0, 8, 8, 0, None), _abi.AdamwRegion(32, 8, 8, 0, None))
-    assert lib.zk_adamw_step_t(p, p, 2, p, p, p, 2, ctypes.cast(regs, ctypes.c_void_p), 2, 1e-3,
-                               0.9, 0.999, 1e-8, 0.0, 1, None) == -1
+    assert lib.zk_adamw_step_t(p, p, 2, p, p, p, 2, ctypes.cast(regs, ctypes.c_void_p), 2, 1024,
+                               1e-3, 0.9, 0.999, 1e-8, 0.0, 1, None) == -1
     regs = R(_abi.AdamwRegion(0, 12, 8, 0, None), _abi.AdamwRegion(96, 8, 8, 0, None))
-    assert lib.zk_adamw_step_t(p, p, 2, p, p, p, 2, ctypes.cast(regs, ctypes.c_void_p), 2, 1e-3,
-                               0.9, 0.999, 1e-8, 0.0, 1, None) == -4
-    assert lib.zk_adamw_step_t(p, p, 2, p, p, p, 2, ctypes.cast(regs, ctypes.c_void_p), 9, 1e-3,
-                               0.9, 0.999, 1e-8, 0.0, 1, None) == -1
+    assert lib.zk_adamw_step_t(p, p, 2, p, p, p, 2, ctypes.cast(regs, ctypes.c_void_p), 2, 1024,
+                               1e-3, 0.9, 0.999, 1e-8, 0.0, 1, None) == -4
+    assert lib.zk_adamw_step_t(p, p, 2, p, p, p, 2, ctypes.cast(regs, ctypes.c_void_p), 9, 1024,
+                               1e-3, 0.9, 0.999, 1e-8, 0.0, 1, None) == -1
+    # a region past the shard's end (n elements) is rejected before any launch
+    regs = R(_abi.AdamwRegion(0, 8, 8, 0, None), _abi.AdamwRegion(64, 8, 16, 0, None))
+    assert lib.zk_adamw_step_t(p, p, 2, p, p, p, 2, ctypes.cast(regs, ctypes.c_void_p), 2, 128,
+                               1e-3, 0.9, 0.999, 1e-8, 0.0, 1, None) == -1
+    assert b"past the shard" in lib.zk_last_error()
     # gemm_swiglu: fp32, K not a multiple of 64, misaligned x, ld_x < K
     assert lib.zk_gemm_swiglu(p, 64, p, p, 64, p, p, 8, p, 8, None, 0, 8, 8, 64, 0, None) == -2
     assert lib.zk_gemm_swiglu(p, 64, p, p, 64, p, p, 8, p, 8, None, 0, 8, 8, 32, 2, None) == -4
@@ -335,3 +340,28 @@ def test_bench_reads_recorded_traffic():
         if algorithmic:
             assert 0.95 * algorithmic <= t <= 1.5 * algorithmic, (name, t)
     assert bench.recorded_traffic("no such kernel") is None
+
+
+def test_fused_adamw_step_param_steps_one_parameter(monkeypatch):
+    """FusedAdamW.step_param(p) (the stage runner's per-parameter hook) updates
+    p alone, however many parameters of the optimizer hold gradients; step()
+    updates each parameter with a gradient once.  The kernel call is replaced
+    by a recorder, so this runs on the CPU."""
+    from zorse_amd import optim
+    calls = []
+
+    def record(param, grad, m, v, **kw):
+        calls.append((param.data_ptr(), kw["step"]))
+    monkeypatch.setattr(optim.K, "adamw_step", record)
+    a, b, c = (torch.nn.Parameter(torch.zeros(8)) for _ in range(3))
+    opt = optim.FusedAdamW([a, b, c], lr=1e-3)
+    a.grad, b.grad = torch.ones(8), torch.ones(8)
+    opt.step_param(a)
+    assert calls == [(a.data_ptr(), 1)]
+    opt.step_param(c)                      # no gradient: nothing to do
+    assert len(calls) == 1
+    opt.step()
+    assert calls[1:] == [(a.data_ptr(), 2), (b.data_ptr(), 1)]
+    assert opt.state[a]["step"] == 2 and opt.state[b]["step"] == 1 and not opt.state[c]
+    with pytest.raises(ValueError):
+        opt.step_param(torch.nn.Parameter(torch.zeros(8)))

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from oracle import decoder as O
-from tests._tol import assert_close
+from tests._tol import assert_close, assert_loss, assert_matched
 
 pytestmark = pytest.mark.gpu
 
@@ -46,20 +46,36 @@ def _oracle_shape(layer):
                         window=s.window)
 
 
-def _check_layer(layer, x, dout, dtype, what):
+def _check_layer(layer, x, dout, dtype, what, rope="half"):
+    """Output, dx and all nine weight gradients against the fp64 oracle; for
+    16-bit layers also against the same layer computed by plain PyTorch in
+    that dtype (the precision-matched bar of tests/_tol.py) and the loss
+    <out, dout>."""
     xg = x.to(layer.flat_param.device).requires_grad_(True)
     out = layer(xg)[0]
     assert out.dtype == dtype and out.shape == x.shape
     out.backward(dout.to(xg.device))
     p = _oracle_params(layer, dtype)
-    rout, rdx, rgrads = O.layer_fwd_bwd(x.double(), p, _oracle_shape(layer), dout.double())
-    assert_close(out, rout, dtype, what + " out")
-    assert_close(xg.grad, rdx, dtype, what + " dx")
+    shape = _oracle_shape(layer)
+    rout, rdx, rgrads = O.layer_fwd_bwd(x.double(), p, shape, dout.double(), rope=rope)
     grad = layer.flat_param.grad
     offs = layer.spec.offsets()
-    for k in O.PARAM_ORDER:
-        a, b = offs[k]
-        assert_close(grad[a:b].view(rgrads[k].shape), rgrads[k], dtype, f"{what} d{k}")
+    got = {"out": out, "dx": xg.grad}
+    got.update({"d" + k: grad[offs[k][0]:offs[k][1]].view(rgrads[k].shape)
+                for k in O.PARAM_ORDER})
+    ref = {"out": rout, "dx": rdx}
+    ref.update({"d" + k: rgrads[k] for k in O.PARAM_ORDER})
+    if dtype == torch.float32:
+        for k in got:
+            assert_close(got[k], ref[k], dtype, f"{what} {k}")
+        return out, rout
+    lout, ldx, lgrads = O.layer_fwd_bwd(x, {k: v.to(dtype) for k, v in p.items()}, shape, dout,
+                                        rope=rope, attn="flash")
+    low = {"out": lout, "dx": ldx}
+    low.update({"d" + k: lgrads[k] for k in O.PARAM_ORDER})
+    for k in got:
+        assert_matched(got[k], ref[k], low[k], dtype, f"{what} {k}")
+    assert_loss(out, rout, lout, dout, f"{what} loss")
     return out, rout
 
 
@@ -97,9 +113,16 @@ def test_layer_bf16_matches_transformers_golden(dev):
     layer = L.LlamaDecoderLayer(cfg, 0, sliding_window=int(window), param_dtype=torch.bfloat16)
     layer = layer.to(dev)
     layer.load_named({k: torch.from_numpy(z["w_" + k]) for k in O.PARAM_ORDER})
-    x = torch.from_numpy(z["x"]).to(torch.bfloat16).to(dev)
-    out = layer(x)[0]
-    assert_close(out, torch.from_numpy(z["out"]), torch.bfloat16, "out")
+    x = torch.from_numpy(z["x"]).to(torch.bfloat16)
+    out = layer(x.to(dev))[0]
+    shape = O.LayerShape(hidden=int(hidden), heads=int(heads), kv_heads=int(kv), head_dim=int(hd),
+                         ffn=int(ffn), theta=theta, window=int(window))
+    wb = {k: torch.from_numpy(z["w_" + k]).to(torch.bfloat16) for k in O.PARAM_ORDER}
+    with torch.no_grad():
+        lout = O.decoder_layer(x, wb, shape, attn="flash")
+        rout = O.decoder_layer(x.double(), {k: v.double() for k, v in wb.items()}, shape)
+    assert_close(out, torch.from_numpy(z["out"]), torch.bfloat16, "out vs golden")
+    assert_matched(out, rout, lout, torch.bfloat16, "out")
 
 
 # ------------------------------------------------------------ scaled configs --
@@ -190,11 +213,13 @@ def test_block_and_profiler_protocol(dev):
     assert torch.allclose(blk.block.flat_param.grad, 2 * g1, rtol=1e-6, atol=1e-7)
     layer = blk.block
     p = _oracle_params(layer, torch.float16)
-    rout, _, rg = O.layer_fwd_bwd(x.detach().double().cpu(), p, _oracle_shape(layer),
-                                  gr.double().cpu())
-    assert_close(out, rout, torch.float16, "out")
+    xc, grc = x.detach().cpu(), gr.cpu()
+    rout, _, rg = O.layer_fwd_bwd(xc.double(), p, _oracle_shape(layer), grc.double())
+    lout, _, lg = O.layer_fwd_bwd(xc, {k: v.half() for k, v in p.items()}, _oracle_shape(layer),
+                                  grc, attn="flash")
+    assert_matched(out, rout, lout, torch.float16, "out")
     a, b = layer.spec.offsets()["q"]
-    assert_close(g1[a:b].view(rg["q"].shape), rg["q"], torch.float16, "dq_proj")
+    assert_matched(g1[a:b].view(rg["q"].shape), rg["q"], lg["q"], torch.float16, "dq_proj")
 
 
 def test_deepspeed_llama_model_forward(dev):
@@ -206,6 +231,82 @@ def test_deepspeed_llama_model_forward(dev):
     assert logits.shape == (1, 64, 512) and torch.isfinite(logits).all()
     logits.float().sum().backward()
     assert all(torch.isfinite(b.block.flat_param.grad).all() for b in model.layers)
+
+
+def test_layer_position_ids(dev):
+    """position_ids other than 0 .. S-1, given as a device tensor, rotate q / k
+    by those positions (forward and backward) -- against the oracle with the
+    same positions; the Block's cached arange and an explicit arange give the
+    plain result bit for bit; ids that differ between batch rows, negative
+    ids and a length mismatch are rejected."""
+    from zorse_amd import llama_simple as L
+    kw = dict(hidden_size=256, num_attention_heads=2, num_key_value_heads=1,
+              intermediate_size=512, rope_theta=1e4)
+    dtype = torch.bfloat16
+    layer = _layer(kw, dev, param_dtype=dtype, seed=31)
+    g = torch.Generator().manual_seed(32)
+    B, S = 2, 192
+    x = torch.randn(B, S, 256, generator=g).to(dtype)
+    dout = torch.randn(B, S, 256, generator=g).to(dtype)
+    pos = 3 * torch.arange(S) + 11          # gaps and an offset: tables past S
+    xg = x.to(dev).requires_grad_(True)
+    out = layer(xg, position_ids=pos[None].expand(B, S).to(dev))[0]
+    out.backward(dout.to(dev))
+    p = _oracle_params(layer, dtype)
+    shape = _oracle_shape(layer)
+    rout, rdx, rg = O.layer_fwd_bwd(x.double(), p, shape, dout.double(), positions=pos)
+    lout, ldx, lg = O.layer_fwd_bwd(x, {k: v.to(dtype) for k, v in p.items()}, shape, dout,
+                                    attn="flash", positions=pos)
+    assert_matched(out, rout, lout, dtype, "out")
+    assert_matched(xg.grad, rdx, ldx, dtype, "dx")
+    offs = layer.spec.offsets()
+    for k in ("q", "k", "o"):
+        a, b = offs[k]
+        assert_matched(layer.flat_param.grad[a:b].view(rg[k].shape), rg[k], lg[k], dtype, "d" + k)
+    # plain positions: three ways, one result
+    with torch.no_grad():
+        plain = layer(x.to(dev))[0]
+        explicit = layer(x.to(dev), position_ids=torch.arange(S, device=dev)[None])[0]
+        blk = L.Block(L.llama_config(**kw), 0, param_dtype=dtype).to(dev)
+        blk.block.flat_param.copy_(layer.flat_param)
+        viablock = blk(x.to(dev))
+        shifted = layer(x.to(dev), position_ids=pos[None].to(dev))[0]
+    assert torch.equal(plain, explicit) and torch.equal(plain, viablock)
+    assert not torch.equal(plain, shifted)
+    with pytest.raises(NotImplementedError):
+        layer(x.to(dev), position_ids=torch.stack([torch.arange(S), pos]).to(dev))
+    with pytest.raises(ValueError):
+        layer(x.to(dev), position_ids=(torch.arange(S) - 1)[None].to(dev))
+    with pytest.raises(ValueError):
+        layer(x.to(dev), position_ids=torch.arange(S - 1)[None].to(dev))
+
+
+def test_cross_entropy_ignore_index_and_label_range(dev):
+    """The chunked-vocabulary CE ignores exactly ignore_index (-100) like
+    F.cross_entropy -- loss and gradients against it in fp64 with a third of
+    the labels ignored -- and rejects labels outside [0, V) with ValueError
+    rather than computing a wrong loss."""
+    from zorse_amd.lm_head import lm_head_cross_entropy
+    g = torch.Generator().manual_seed(33)
+    T, h, V = 96, 64, 500
+    x = torch.randn(T, h, generator=g)
+    w = 0.1 * torch.randn(V, h, generator=g)
+    labels = torch.randint(0, V, (T,), generator=g)
+    labels[::3] = -100
+    xg, wg = x.to(dev).requires_grad_(True), w.to(dev).requires_grad_(True)
+    loss = lm_head_cross_entropy(xg, wg, labels.to(dev), chunk=128)
+    loss.backward()
+    xr, wr = x.double().requires_grad_(True), w.double().requires_grad_(True)
+    ref = torch.nn.functional.cross_entropy(xr @ wr.t(), labels)
+    ref.backward()
+    assert abs(loss.item() - ref.item()) <= 1e-4 * abs(ref.item())
+    assert_close(xg.grad, xr.grad, torch.float32, "dx")
+    assert_close(wg.grad, wr.grad, torch.float32, "dw")
+    for bad in (-1, V, V + 7):
+        lab = labels.clone()
+        lab[5] = bad
+        with pytest.raises(ValueError):
+            lm_head_cross_entropy(xg, wg, lab.to(dev), chunk=128)
 
 
 # ----------------------------------------------------------- stage + AdamW --
@@ -239,9 +340,15 @@ def test_stage_runner_optimizer_in_backwards(dev):
     prs = [{k: v.clone().requires_grad_(True) for k, v in p.items()} for p in before]
     y = O.decoder_layer(O.decoder_layer(xr, prs[0], shape), prs[1], shape)
     y.backward(dout.double())
+    # the same two-layer stack as plain PyTorch computes it in bf16
+    pls = [{k: v.to(dtype).requires_grad_(True) for k, v in p.items()} for p in before]
+    yl = O.decoder_layer(O.decoder_layer(x, pls[0], shape, attn="flash"), pls[1], shape,
+                         attn="flash")
+    yl.backward(dout)
     for i, (layer, pr, opt) in enumerate(zip(layers, prs, runner.optimizers)):
         gref = O.flatten({k: v.grad for k, v in pr.items()})
-        assert_close(captured[i], gref, dtype, f"layer {i} grad")
+        glow = O.flatten({k: v.grad for k, v in pls[i].items()})
+        assert_matched(captured[i], gref, glow, dtype, f"layer {i} grad")
         flat0 = O.flatten(before[i]).clone()
         m, v = torch.zeros_like(flat0), torch.zeros_like(flat0)
         O.adamw_step(flat0, captured[i].double().cpu(), m, v, 1, 1e-4, 0.9, 0.95, 1e-8, 0.1)
@@ -249,6 +356,48 @@ def test_stage_runner_optimizer_in_backwards(dev):
         assert_close(master, flat0, torch.float32, f"layer {i} master")
         assert torch.equal(layer.flat_param.detach().cpu(), master.cpu().to(dtype))
         assert layer.flat_param.grad is None
+
+
+def test_stage_steps_each_parameter_once(dev):
+    """A stage layer with several parameters (the last stage's output layer
+    is Sequential(norm, lm_head), models/llama_simple.py:559-561): each
+    parameter's post-accumulate hook steps that parameter alone, so every
+    parameter gets exactly one AdamW update per step in both overlap modes --
+    the same weights as torch.optim.AdamW applied once to the captured
+    gradients."""
+    from zorse_amd.stage import StageRunner
+    torch.manual_seed(34)
+    x = torch.randn(2, 16, 64, device=dev)
+    dout = torch.randn(2, 16, 64, device=dev)
+    init = torch.nn.Sequential(torch.nn.Linear(64, 64, bias=False),
+                               torch.nn.Linear(64, 64, bias=False)).to(dev)
+    results = {}
+    for mode in ("attention", "immediate"):
+        layer = torch.nn.Sequential(torch.nn.Linear(64, 64, bias=False),
+                                    torch.nn.Linear(64, 64, bias=False)).to(dev)
+        layer.load_state_dict(init.state_dict())
+        grads = {}
+        for name, p in layer.named_parameters():
+            p.register_post_accumulate_grad_hook(
+                lambda t, name=name: grads.__setitem__(name, t.grad.detach().clone()))
+        runner = StageRunner([layer], lr=1e-2, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1,
+                             optimizer_overlap=mode)
+        runner.step(x, dout)
+        runner.wait_optimizer()
+        torch.cuda.synchronize()
+        steps = {n: runner.optimizers[0].state[p]["step"] for n, p in layer.named_parameters()}
+        assert steps == {"0.weight": 1, "1.weight": 1}, (mode, steps)
+        ref = {n: p.detach().clone().requires_grad_(True) for n, p in init.named_parameters()}
+        opt = torch.optim.AdamW(list(ref.values()), lr=1e-2, betas=(0.9, 0.95), eps=1e-8,
+                                weight_decay=0.1, foreach=False)
+        for n, p in ref.items():
+            p.grad = grads[n]
+        opt.step()
+        for n, p in layer.named_parameters():
+            assert_close(p, ref[n], torch.float32, f"{mode} {n}")
+        results[mode] = [p.detach().clone() for p in layer.parameters()]
+    for a, b in zip(results["attention"], results["immediate"]):
+        assert torch.equal(a, b)
 
 
 def test_stage_transposed_weights(dev):
@@ -457,12 +606,20 @@ def test_llama_v2_block_vs_oracle(dev, dtype):
                          ffn=s.ffn, eps=s.eps, theta=s.rope_theta)
     p = _oracle_params(blk, dtype)
     rout, rdx, rg = O.layer_fwd_bwd(x.double(), p, shape, dout.double(), rope="interleaved")
-    assert_close(out, rout, dtype, "out")
-    assert_close(xg.grad, rdx, dtype, "dx")
     offs = s.offsets()
-    for k in O.PARAM_ORDER:
-        a, b = offs[k]
-        assert_close(blk.flat_param.grad[a:b].view(rg[k].shape), rg[k], dtype, "d" + k)
+    got = [("out", out, rout), ("dx", xg.grad, rdx)]
+    got += [("d" + k, blk.flat_param.grad[offs[k][0]:offs[k][1]].view(rg[k].shape), rg[k])
+            for k in O.PARAM_ORDER]
+    if dtype == torch.float32:
+        for name, a, r in got:
+            assert_close(a, r, dtype, name)
+        return
+    lout, ldx, lg = O.layer_fwd_bwd(x, {k: v.to(dtype) for k, v in p.items()}, shape, dout,
+                                    rope="interleaved", attn="flash")
+    low = {"out": lout, "dx": ldx, **{"d" + k: lg[k] for k in O.PARAM_ORDER}}
+    for name, a, r in got:
+        assert_matched(a, r, low[name], dtype, name)
+    assert_loss(out, rout, lout, dout)
 
 
 def test_profiler_protocol_small(dev):

@@ -94,6 +94,35 @@ def test_rmsnorm_bwd_closed_form_vs_autograd():
     assert torch.allclose(dx, x.grad) and torch.allclose(dw, w.grad)
 
 
+def test_rmsnorm_rstd_matches_hf_variance_and_closed_forms():
+    """rmsnorm_rstd is the factor HF LlamaRMSNorm multiplies by: with a unit
+    weight in fp64 the module's output divided by its input is rstd in every
+    element; a constant row c gives 1 / sqrt(c^2 + eps); a one-hot row gives
+    1 / sqrt(1 / h + eps); and mean((x rstd)^2) = m / (m + eps) with
+    m = mean(x^2).  A slip to sum, to sqrt, or a dropped eps fails."""
+    from transformers.models.llama.modeling_llama import LlamaRMSNorm
+    g = torch.Generator().manual_seed(21)
+    h, eps = 40, 1e-2
+    m = LlamaRMSNorm(h, eps=eps).double()
+    x = torch.randn(6, h, generator=g, dtype=torch.float64)
+    r = O.rmsnorm_rstd(x, eps)
+    assert r.shape == (6,) and r.dtype == torch.float64
+    # (HF upcasts to fp32 internally, hence fp32-level agreement)
+    assert torch.allclose(m(x) / x, r[:, None].expand(6, h), rtol=1e-6, atol=0)
+    c = torch.full((1, h), 0.3, dtype=torch.float64)
+    assert math.isclose(O.rmsnorm_rstd(c, eps).item(), 1 / math.sqrt(0.09 + eps), rel_tol=1e-14)
+    e = torch.zeros(1, h, dtype=torch.float64)
+    e[0, 7] = 1.0
+    assert math.isclose(O.rmsnorm_rstd(e, eps).item(), 1 / math.sqrt(1 / h + eps), rel_tol=1e-14)
+    ms = x.pow(2).mean(-1)
+    assert torch.allclose((x * r[:, None]).pow(2).mean(-1), ms / (ms + eps), rtol=1e-13)
+    # fp32 / bf16 input: fp32 result from the fp32-upcast variance (HF's order)
+    xb = x.to(torch.bfloat16)
+    rb = O.rmsnorm_rstd(xb, eps)
+    assert rb.dtype == torch.float32
+    assert torch.equal(rb, torch.rsqrt(xb.float().pow(2).mean(-1) + eps))
+
+
 # ------------------------------------------------------------------- RoPE --
 
 def test_rope_matches_hf():
@@ -249,6 +278,128 @@ def test_attention_rows_sum_to_one():
     ones = torch.ones(1, 10, 1, 4, dtype=torch.float64)
     out, _ = O.attention(q, k, ones, causal=True, window=3)
     assert torch.allclose(out, ones)
+
+
+def test_flash_attention_lowp_is_attention_without_rounding():
+    """In fp64 (no storage rounding) the flash-rounding attention is the eager
+    attention, forward and closed-form backward (GQA 4:1, causal, window):
+    this pins its indexing, scale, mask, LSE use and the GQA group sum."""
+    g = torch.Generator().manual_seed(22)
+    B, S, Hq, Hkv, d = 2, 23, 4, 1, 8
+    q = torch.randn(B, S, Hq, d, generator=g, dtype=torch.float64, requires_grad=True)
+    k = torch.randn(B, S, Hkv, d, generator=g, dtype=torch.float64, requires_grad=True)
+    v = torch.randn(B, S, Hkv, d, generator=g, dtype=torch.float64, requires_grad=True)
+    do = torch.randn(B, S, Hq, d, generator=g, dtype=torch.float64)
+    for W in (0, 5):
+        for t in (q, k, v):
+            t.grad = None
+        out = O.flash_attention_lowp(q, k, v, causal=True, window=W)
+        ref, _ = O.attention(q.detach(), k.detach(), v.detach(), causal=True, window=W)
+        assert torch.allclose(out, ref, atol=1e-13)
+        out.backward(do)
+        dq, dk, dv = O.attention_bwd(q.detach(), k.detach(), v.detach(), do, causal=True,
+                                     window=W)
+        assert torch.allclose(q.grad, dq, atol=1e-12)
+        assert torch.allclose(k.grad, dk, atol=1e-12)
+        assert torch.allclose(v.grad, dv, atol=1e-12)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_flash_attention_lowp_error_matches_sdpa(dtype):
+    """At 16-bit storage the flash-rounding attention is as accurate as torch's
+    own SDPA in that dtype (CPU flash kernel: fp32 softmax, 16-bit P): output
+    and gradient errors against fp64 within a factor 2 of SDPA's, and the
+    16-bit rounding is really applied (errors far above fp32's)."""
+    g = torch.Generator().manual_seed(23)
+    B, S, H, d = 1, 96, 2, 64
+    q64 = torch.randn(B, S, H, d, generator=g, dtype=torch.float64)
+    k64 = torch.randn(B, S, H, d, generator=g, dtype=torch.float64)
+    v64 = torch.randn(B, S, H, d, generator=g, dtype=torch.float64)
+    do64 = torch.randn(B, S, H, d, generator=g, dtype=torch.float64)
+    q, k, v, do = (t.to(dtype) for t in (q64, k64, v64, do64))
+    # the fp64 truth on the rounded inputs
+    refs = [t.double().requires_grad_(True) for t in (q, k, v)]
+    ro, _ = O.attention(*refs, causal=True)
+    ro.backward(do.double())
+    mine = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    mo = O.flash_attention_lowp(*mine, causal=True)
+    mo.backward(do)
+    lib = [t.clone().transpose(1, 2).requires_grad_(True) for t in (q, k, v)]
+    lo = F.scaled_dot_product_attention(*lib, is_causal=True)
+    lo.backward(do.transpose(1, 2))
+    lo = lo.transpose(1, 2)
+
+    def e(a, b):
+        return (a.double() - b.double()).abs().max().item()
+
+    pairs = [("o", mo, lo, ro)] + [(n, a.grad, b.grad.transpose(1, 2), c.grad)
+                                   for n, a, b, c in zip("qkv", mine, lib, refs)]
+    for name, got, sdpa, ref in pairs:
+        em, es = e(got, ref), e(sdpa, ref)
+        assert em <= 2.0 * es, (name, em, es)
+        assert em > 1e-5 * ref.abs().max().item(), (name, em)
+
+
+def test_layer_flash_path_is_the_eager_layer_in_fp64():
+    """layer_fwd_bwd(attn="flash") and the eager composition agree in fp64
+    (output, dx and all nine weight gradients), on the Mistral golden shape."""
+    shape, t = _load("mistral_swa_d64")
+    p = {k: t["w_" + k] for k in O.PARAM_ORDER}
+    a = O.layer_fwd_bwd(t["x"], p, shape, t["dout"])
+    b = O.layer_fwd_bwd(t["x"], p, shape, t["dout"], attn="flash")
+    assert torch.allclose(a[0], b[0], atol=1e-12) and torch.allclose(a[1], b[1], atol=1e-12)
+    for k in O.PARAM_ORDER:
+        assert torch.allclose(a[2][k], b[2][k], atol=1e-12), k
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_layer_lowp_is_transformers_layer_precision(dtype):
+    """The compute-precision layer (attn="flash" on 16-bit tensors) is as
+    accurate as transformers' own LlamaDecoderLayer run in that dtype with SDPA
+    attention (the reference's non-flash-attn path): every output / gradient
+    error against fp64 within a factor 2 (+1 ulp) of the transformers layer's."""
+    from transformers import LlamaConfig
+    from transformers.models.llama.modeling_llama import LlamaDecoderLayer, LlamaRotaryEmbedding
+    hidden, heads, kv, hd, ffn, S = 128, 4, 2, 32, 256, 80
+    cfg = LlamaConfig(hidden_size=hidden, num_attention_heads=heads, num_key_value_heads=kv,
+                      head_dim=hd, intermediate_size=ffn, rms_norm_eps=1e-6,
+                      max_position_embeddings=S, rope_theta=1e4, attention_dropout=0.0)
+    cfg._attn_implementation = "sdpa"
+    layer = LlamaDecoderLayer(cfg, 0)
+    g = torch.Generator().manual_seed(24)
+    names = {"q": layer.self_attn.q_proj.weight, "k": layer.self_attn.k_proj.weight,
+             "v": layer.self_attn.v_proj.weight, "o": layer.self_attn.o_proj.weight,
+             "gate": layer.mlp.gate_proj.weight, "up": layer.mlp.up_proj.weight,
+             "down": layer.mlp.down_proj.weight, "ln1": layer.input_layernorm.weight,
+             "ln2": layer.post_attention_layernorm.weight}
+    with torch.no_grad():
+        for k_, w in names.items():
+            w.copy_(1 + 0.1 * torch.randn(w.shape, generator=g) if k_.startswith("ln")
+                    else 0.05 * torch.randn(w.shape, generator=g))
+    layer = layer.to(dtype)
+    x = torch.randn(1, S, hidden, generator=g).to(dtype)
+    dout = torch.randn(1, S, hidden, generator=g).to(dtype)
+    rope = LlamaRotaryEmbedding(cfg)
+    pos = torch.arange(S)[None]
+    xr = x.clone().requires_grad_(True)
+    cos, sin = rope(xr, pos)
+    hf_out = layer(xr, attention_mask=None, position_ids=pos,
+                   position_embeddings=(cos.to(dtype), sin.to(dtype)))
+    hf_out = hf_out[0] if isinstance(hf_out, tuple) else hf_out
+    hf_out.backward(dout)
+    p = {k_: w.detach() for k_, w in names.items()}
+    shape = O.LayerShape(hidden=hidden, heads=heads, kv_heads=kv, head_dim=hd, ffn=ffn)
+    ref = O.layer_fwd_bwd(x.double(), {k_: w.double() for k_, w in p.items()}, shape,
+                          dout.double())
+    low = O.layer_fwd_bwd(x, p, shape, dout, attn="flash")
+    ulp = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10}[dtype]
+    cases = [("out", low[0], hf_out, ref[0]), ("dx", low[1], xr.grad, ref[1])]
+    cases += [("d" + k_, low[2][k_], names[k_].grad, ref[2][k_]) for k_ in O.PARAM_ORDER]
+    for name, mine, hf, r in cases:
+        em = (mine.double() - r).abs().max().item()
+        eh = (hf.double() - r).abs().max().item()
+        floor = ulp * 2.0 ** math.floor(math.log2(r.abs().max().item()))
+        assert em <= 2.0 * eh + floor, (name, em, eh)
 
 
 # -------------------------------------------------------------------- MLP --

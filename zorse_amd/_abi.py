@@ -95,7 +95,7 @@ SIGNATURES = {
                            _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr]),
     "zk_adamw_step": (_int, [_ptr, _ptr, _int, _ptr, _ptr, _ptr, _int, _i64,
                              _f64, _f64, _f64, _f64, _f64, _i64, _ptr]),
-    "zk_adamw_step_t": (_int, [_ptr, _ptr, _int, _ptr, _ptr, _ptr, _int, _ptr, _int,
+    "zk_adamw_step_t": (_int, [_ptr, _ptr, _int, _ptr, _ptr, _ptr, _int, _ptr, _int, _i64,
                                 _f64, _f64, _f64, _f64, _f64, _i64, _ptr]),
     "zk_cast": (_int, [_ptr, _int, _ptr, _int, _i64, _int, _ptr]),
     "zk_ce_fwd_chunk": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr, _int,

@@ -342,9 +342,9 @@ extern "C" int zk_adamw_step(float* param, const void* grad, int grad_dtype,
 
 extern "C" int zk_adamw_step_t(float* param, const void* grad, int grad_dtype, float* exp_avg,
                                float* exp_avg_sq, void* param_lowp, int lowp_dtype,
-                               const zk_adamw_region* regions, int n_regions, double lr,
-                               double beta1, double beta2, double eps, double weight_decay,
-                               int64_t step, zk_stream_t stream) {
+                               const zk_adamw_region* regions, int n_regions, int64_t n,
+                               double lr, double beta1, double beta2, double eps,
+                               double weight_decay, int64_t step, zk_stream_t stream) {
   ZK_REQUIRE(valid_dtype(grad_dtype), ZK_EDTYPE, "zk_adamw_step_t: bad grad dtype %d",
              grad_dtype);
   ZK_REQUIRE(lowp_dtype == ZK_BF16 || lowp_dtype == ZK_F16, ZK_EDTYPE,
@@ -379,6 +379,9 @@ extern "C" int zk_adamw_step_t(float* param, const void* grad, int grad_dtype, f
     reg.first_tile[i] = tiles;
     tiles += tx * ty;
     prev_end = r.offset + r.rows * r.cols;
+    ZK_REQUIRE(prev_end <= n, ZK_EINVAL,
+               "zk_adamw_step_t: region %d ends at %lld, past the shard's %lld elements", i,
+               (long long)prev_end, (long long)n);
   }
   reg.first_tile[n_regions] = tiles;
   reg.n = n_regions;

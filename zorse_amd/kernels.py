@@ -59,6 +59,7 @@ def rmsnorm_fwd(x: torch.Tensor, weight: torch.Tensor, eps: float,
     rows = x.numel() // hidden if hidden else 0
     if out is not None:
         y, rstd = out[0], out[1]
+        _require_gpu(x, y, rstd)
         if y.shape != x.shape or y.dtype != x.dtype or not y.is_contiguous():
             raise ValueError("out y must match x")
         if rstd.numel() != rows or rstd.dtype != torch.float32 or not rstd.is_contiguous():
@@ -71,7 +72,14 @@ def rmsnorm_fwd(x: torch.Tensor, weight: torch.Tensor, eps: float,
         if residual.shape != x.shape or residual.dtype != x.dtype:
             raise ValueError("residual must match x in shape and dtype")
         _require_contig("residual", residual)
-        h = out[2] if out is not None and len(out) > 2 else torch.empty_like(x)
+        if out is not None and len(out) > 2:
+            h = out[2]
+            _require_gpu(h)
+            if h.shape != x.shape or h.dtype != x.dtype or not h.is_contiguous() \
+                    or h.device != dev:
+                raise ValueError("out h must match x (shape, dtype, device, contiguous)")
+        else:
+            h = torch.empty_like(x)
     check(lib().zk_rmsnorm_fwd(ptr(x), ptr(residual), ptr(h) if residual is not None else None,
                                ptr(weight), ptr(y), ptr(rstd), rows, hidden, float(eps),
                                dtype_code(x.dtype), dtype_code(weight.dtype),
@@ -90,8 +98,9 @@ def rmsnorm_bwd(dy: torch.Tensor, h: torch.Tensor, weight: torch.Tensor,
                 dw_dtype: torch.dtype | None = None, out: torch.Tensor | None = None,
                 workspace: torch.Tensor | None = None):
     """Returns (dx, dw).  dx includes dres when given; dw is written (or
-    accumulated into) ``dw`` if supplied, else a new tensor of ``dw_dtype``
-    (default: weight dtype).  ``out`` / ``workspace`` may be preallocated."""
+    accumulated into) ``dw`` if supplied, else a new tensor -- in the weight's
+    dtype either way (``dw_dtype``, if given, must be that dtype).  ``out`` /
+    ``workspace`` may be preallocated."""
     dev = _require_gpu(dy, h, weight, rstd, dres, dw)
     hidden = h.shape[-1]
     for name, t in (("dy", dy), ("h", h), ("rstd", rstd), ("weight", weight)):
@@ -105,12 +114,17 @@ def rmsnorm_bwd(dy: torch.Tensor, h: torch.Tensor, weight: torch.Tensor,
         if dres.shape != h.shape or dres.dtype != h.dtype:
             raise ValueError("dres must match h")
         _require_contig("dres", dres)
+    if dw_dtype is not None and dw_dtype != weight.dtype:
+        raise ValueError(f"dw is written in the weight's dtype {weight.dtype} (got dw_dtype "
+                         f"{dw_dtype})")
     if dw is None:
-        dw = torch.empty(hidden, device=dev, dtype=dw_dtype or weight.dtype)
+        dw = torch.empty(hidden, device=dev, dtype=weight.dtype)
         accumulate = False
-    elif dw.shape != (hidden,) or not dw.is_contiguous():
-        raise ValueError("dw must be a contiguous [hidden] tensor")
+    elif dw.shape != (hidden,) or not dw.is_contiguous() or dw.dtype != weight.dtype:
+        raise ValueError(f"dw must be a contiguous [hidden] tensor of the weight's dtype "
+                         f"{weight.dtype}")
     if out is not None:
+        _require_gpu(h, out)
         if out.shape != h.shape or out.dtype != h.dtype or not out.is_contiguous():
             raise ValueError("out must match h")
         dx = out
@@ -118,6 +132,7 @@ def rmsnorm_bwd(dy: torch.Tensor, h: torch.Tensor, weight: torch.Tensor,
         dx = torch.empty_like(h)
     ws_elems = rmsnorm_bwd_workspace_elems(rows, hidden)
     if workspace is not None:
+        _require_gpu(h, workspace)
         if workspace.dtype != torch.float32 or workspace.numel() < ws_elems or \
                 not workspace.is_contiguous():
             raise ValueError(f"workspace must be contiguous fp32 with >= {ws_elems} elements")
@@ -150,6 +165,8 @@ def swiglu_fwd(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = 
     rows, cols = gate.shape
     if out is None:
         out = torch.empty(rows, cols, device=dev, dtype=gate.dtype)
+    elif out.shape != (rows, cols) or out.dtype != gate.dtype or out.device != dev:
+        raise ValueError("out must be [rows, cols] of gate's dtype on gate's device")
     ldz = _row_view_check("out", out)
     check(lib().zk_swiglu_fwd(ptr(gate), ptr(up), ld, ptr(out), ldz, rows, cols,
                               dtype_code(gate.dtype), stream_handle(dev)), "zk_swiglu_fwd")
@@ -428,7 +445,7 @@ def adamw_step_t(param: torch.Tensor, grad: torch.Tensor, exp_avg: torch.Tensor,
                              ptr(lt) if lt is not None else None)
     check(lib().zk_adamw_step_t(ptr(param), ptr(grad), dtype_code(grad.dtype), ptr(exp_avg),
                                 ptr(exp_avg_sq), ptr(lowp_out), dtype_code(lowp_out.dtype),
-                                ctypes.cast(arr, ctypes.c_void_p), len(regions), float(lr),
+                                ctypes.cast(arr, ctypes.c_void_p), len(regions), n, float(lr),
                                 float(beta1), float(beta2), float(eps), float(weight_decay),
                                 int(step), stream_handle(dev)), "zk_adamw_step_t")
 
@@ -446,7 +463,7 @@ def cast_(src: torch.Tensor, dst: torch.Tensor, accumulate: bool = False) -> tor
 def transpose(src: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """out = src^T for a 2-D tensor with unit column stride; ``out`` (rows
     with unit stride, shape (cols, rows)) may be supplied."""
-    dev = _require_gpu(src)
+    dev = _require_gpu(src, out)
     if src.dim() != 2 or src.stride(1) != 1:
         raise ValueError("transpose needs a 2-D tensor with unit column stride")
     rows, cols = src.shape

@@ -148,13 +148,26 @@ def _dgrad(dy, wmat, transpose_weight, wt=None):
     return torch.mm(dy, wmat)
 
 
-def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=None):
+def _rope_for(S, spec, dtype, device, positions):
+    """RoPE tables covering positions 0 .. S-1, or 0 .. max(positions) when
+    explicit positions are given (int64 [S] on the device)."""
+    n_pos = S
+    if positions is not None:
+        n_pos = max(S, int(positions.max().item()) + 1)
+    return rope_tables(n_pos, spec.head_dim, spec.rope_theta, dtype, device,
+                       spec.interleaved_rope)
+
+
+def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=None,
+                  positions: torch.Tensor | None = None):
     """Forward on compute-dtype tensors; returns (out, saved tuple).
 
     ``attn_cache`` (optional) is an AttentionCache: a hit supplies the
     attention output and LSE of an earlier forward of the same input and
     weights, so the attention forward is skipped (the recompute of the
-    reference's pipeline backward); a miss computes them and records them."""
+    reference's pipeline backward); a miss computes them and records them.
+    ``positions`` (optional): int64 [S] token positions for RoPE, shared by
+    the batch (default 0 .. S-1)."""
     B, S, h = x.shape
     T = B * S
     d, Hq, Hkv = spec.head_dim, spec.heads, spec.kv_heads
@@ -164,8 +177,8 @@ def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=Non
     q = qkv[:, :spec.q_dim].view(B, S, Hq, d)
     k = qkv[:, spec.q_dim:spec.q_dim + spec.kv_dim].view(B, S, Hkv, d)
     v = qkv[:, spec.q_dim + spec.kv_dim:].view(B, S, Hkv, d)
-    cos, sin = rope_tables(S, d, spec.rope_theta, x.dtype, x.device, spec.interleaved_rope)
-    K.rope_(q, k, cos, sin, interleaved=spec.interleaved_rope)
+    cos, sin = _rope_for(S, spec, x.dtype, x.device, positions)
+    K.rope_(q, k, cos, sin, positions=positions, interleaved=spec.interleaved_rope)
     hit = attn_cache.take() if attn_cache is not None else None
     if hit is not None:
         o, lse = hit
@@ -188,7 +201,7 @@ def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=Non
         z = zs = K.swiglu_fwd(gu[:, :F], gu[:, F:])
     out = torch.addmm(hdn, z, w.down.t())            # residual + down(z)
     del z
-    saved = (x2, n1, rstd1, qkv, o2, lse, hdn, n2, rstd2, gu, zs)
+    saved = (x2, n1, rstd1, qkv, o2, lse, hdn, n2, rstd2, gu, zs, positions)
     return out.view(B, S, h), saved
 
 
@@ -205,7 +218,7 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
     (compute dtype, flat layout) and returns dx.  ``wt`` (optional): W^T of
     the qkv, o, gu and down weights, current with ``w``."""
     wt = wt or {}
-    x2, n1, rstd1, qkv, o2, lse, hdn, n2, rstd2, gu, zs = saved
+    x2, n1, rstd1, qkv, o2, lse, hdn, n2, rstd2, gu, zs, positions = saved
     T, h = x2.shape
     B = dout.shape[0]
     S = T // B
@@ -249,8 +262,9 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
     K.attn_bwd(q, k, v, o2.view(B, S, Hq, d), do2.view(B, S, Hq, d), lse,
                causal=spec.causal, window=spec.window, dq=dq, dk=dk, dv=dv)
     del do2
-    cos, sin = rope_tables(S, d, spec.rope_theta, dout.dtype, dout.device, spec.interleaved_rope)
-    K.rope_(dq, dk, cos, sin, interleaved=spec.interleaved_rope, inverse=True)
+    cos, sin = _rope_for(S, spec, dout.dtype, dout.device, positions)
+    K.rope_(dq, dk, cos, sin, positions=positions, interleaved=spec.interleaved_rope,
+            inverse=True)
     dn1 = _dgrad(dqkv, w.qkv, False, wt.get("qkv"))  # [T, h]
     _wgrad(dqkv, n1, g.qkv)
     del dqkv
@@ -317,22 +331,25 @@ class DecoderLayerFunction(torch.autograd.Function):
     """autograd node of one decoder layer: inputs (x, flat_param)."""
 
     @staticmethod
-    def forward(ctx, x, flat_param, spec, weights_lowp, attn_cache=None, wt=None):
+    def forward(ctx, x, flat_param, spec, weights_lowp, attn_cache=None, wt=None,
+                positions=None):
         w_flat = weights_lowp if weights_lowp is not None else flat_param
         w = FlatViews(spec, w_flat)
         if attn_cache is not None:
             attn_cache.bind(x, flat_param, w_flat)
         with torch.autocast("cuda", enabled=False):
-            out, saved = layer_forward(x.contiguous(), w, spec, attn_cache)
+            out, saved = layer_forward(x.contiguous(), w, spec, attn_cache, positions)
         ctx.spec = spec
         ctx.wt = wt
         ctx.param_dtype = flat_param.dtype
-        ctx.save_for_backward(w_flat, *saved)
+        ctx.positions = saved[-1]
+        ctx.save_for_backward(w_flat, *saved[:-1])
         return out
 
     @staticmethod
     def backward(ctx, dout):
         w_flat, *saved = ctx.saved_tensors
+        saved = (*saved, ctx.positions)
         spec = ctx.spec
         w = FlatViews(spec, w_flat)
         dout = dout.to(w_flat.dtype).contiguous()
@@ -341,4 +358,4 @@ class DecoderLayerFunction(torch.autograd.Function):
             dx = layer_backward(dout, saved, w, spec, grad_flat, ctx.wt)
         if ctx.param_dtype != grad_flat.dtype:
             grad_flat = grad_flat.to(ctx.param_dtype)
-        return dx, grad_flat, None, None, None, None
+        return dx, grad_flat, None, None, None, None, None

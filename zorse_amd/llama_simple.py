@@ -245,16 +245,42 @@ class FlatDecoderLayer(nn.Module):
         self._lowp_cache = (key, w)
         return w
 
-    def _run(self, x: torch.Tensor) -> torch.Tensor:
+    def _run(self, x: torch.Tensor, positions: torch.Tensor | None = None) -> torch.Tensor:
         """The fused layer on x [B, S, h]; under autocast an fp32 input runs in
-        the autocast dtype (the profiler protocol)."""
+        the autocast dtype (the profiler protocol).  ``positions``: int64 [S]
+        RoPE positions on x's device, or None for 0 .. S-1."""
         cdt = x.dtype
         if cdt == torch.float32 and torch.is_autocast_enabled("cuda"):
             cdt = torch.get_autocast_dtype("cuda")
             x = x.to(cdt)
         wt = self._transposed_weights() if cdt == self.flat_param.dtype else None
         return DecoderLayerFunction.apply(x, self.flat_param, self.spec,
-                                          self._compute_weights(cdt), self.attn_cache, wt)
+                                          self._compute_weights(cdt), self.attn_cache, wt,
+                                          positions)
+
+    # position_ids tensors known to hold arange(S) (the Block's cached ids):
+    # recognised by identity, so the common call costs no check
+    _arange_ids = None
+
+    def _positions(self, position_ids, S, device):
+        """None when position_ids is None or 0 .. S-1, else the int64 [S]
+        positions on ``device`` (every batch row must hold the same ids)."""
+        if position_ids is None or position_ids is self._arange_ids:
+            return None
+        ids = position_ids.reshape(-1, position_ids.shape[-1])
+        if ids.shape[-1] != S:
+            raise ValueError(f"position_ids has {ids.shape[-1]} positions for {S} tokens")
+        if ids.dtype not in (torch.int32, torch.int64):
+            raise ValueError("position_ids must be an integer tensor")
+        if ids.shape[0] > 1 and not bool((ids == ids[:1]).all()):
+            raise NotImplementedError("position_ids that differ between batch rows are not "
+                                      "supported")
+        pos = ids[0].to(device=device, dtype=torch.int64).contiguous()
+        if bool((pos < 0).any()):
+            raise ValueError("position_ids must be non-negative")
+        if bool(torch.equal(pos, torch.arange(S, device=device))):
+            return None
+        return pos
 
 
 class LlamaDecoderLayer(FlatDecoderLayer):
@@ -293,13 +319,8 @@ class LlamaDecoderLayer(FlatDecoderLayer):
                                       "layer applies the causal / sliding-window mask itself")
         if past_key_value is not None or use_cache or output_attentions:
             raise NotImplementedError("KV caches and attention weights are not produced")
-        if position_ids is not None:
-            S = hidden_states.shape[1]
-            pos = position_ids.reshape(-1, position_ids.shape[-1])[0]
-            if pos.numel() != S or (pos.device.type == "cpu" and not torch.equal(
-                    pos, torch.arange(S, dtype=pos.dtype))):
-                raise NotImplementedError("only position_ids = arange(S) are supported")
-        return (self._run(hidden_states),)
+        pos = self._positions(position_ids, hidden_states.shape[1], hidden_states.device)
+        return (self._run(hidden_states, pos),)
 
 
 class Block(nn.Module):
@@ -316,6 +337,8 @@ class Block(nn.Module):
         if self.cached_position_ids is None or self.cached_position_ids.size(1) != seq_length:
             self.cached_position_ids = torch.arange(0, seq_length, device=x.device,
                                                     dtype=torch.long).unsqueeze(0)
+            # the layer takes these ids as 0 .. S-1 without checking them
+            self.block._arange_ids = self.cached_position_ids
         return self.block(x, attention_mask=None, position_ids=self.cached_position_ids)[0]
 
 

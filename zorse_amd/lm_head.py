@@ -38,10 +38,13 @@ def _bwd_chunk(logits, labels, col0, lse, scale):
 
 
 class LMHeadCrossEntropyFunction(torch.autograd.Function):
-    """loss = mean_t CE(x_t W^T, label_t) over tokens whose label >= 0."""
+    """loss = mean_t CE(x_t W^T, label_t) over tokens whose label is not
+    ``ignore_index`` -- F.cross_entropy's semantics: every other label must
+    lie in [0, V) (checked on the host; an out-of-range label raises
+    ValueError as F.cross_entropy raises on it)."""
 
     @staticmethod
-    def forward(ctx, x, weight, labels, chunk):
+    def forward(ctx, x, weight, labels, chunk, ignore_index=-100):
         K._require_gpu(x, weight, labels)
         if x.dim() != 2 or weight.dim() != 2 or x.shape[1] != weight.shape[1]:
             raise ValueError("x must be [T, h] and weight [V, h]")
@@ -49,8 +52,13 @@ class LMHeadCrossEntropyFunction(torch.autograd.Function):
             raise ValueError("labels must be int64 [T]")
         x = x.contiguous()
         w = weight if weight.dtype == x.dtype else weight.to(x.dtype)
-        labels = labels.contiguous()
         T, V = x.shape[0], w.shape[0]
+        ignored = labels == ignore_index
+        if bool((~ignored & ((labels < 0) | (labels >= V))).any()):
+            raise ValueError(f"labels must lie in [0, {V}) or equal ignore_index "
+                             f"({ignore_index})")
+        # the kernels skip rows whose label is negative
+        labels = torch.where(ignored, torch.full_like(labels, -1), labels).contiguous()
         run_max = torch.full((T,), float("-inf"), device=x.device, dtype=torch.float32)
         run_sum = torch.zeros(T, device=x.device, dtype=torch.float32)
         target = torch.zeros(T, device=x.device, dtype=torch.float32)
@@ -82,15 +90,16 @@ class LMHeadCrossEntropyFunction(torch.autograd.Function):
             torch.mm(dlog.t(), x, out=dw[c0:c0 + chunk])
         if dw.dtype != ctx.weight_dtype:
             dw = dw.to(ctx.weight_dtype)
-        return dx.to(x.dtype), dw, None, None
+        return dx.to(x.dtype), dw, None, None, None
 
 
-def lm_head_cross_entropy(x, weight, labels, chunk: int = 8192):
-    """Mean cross-entropy of logits x W^T against labels (negative = ignored);
-    x [..., h] is flattened over its leading dims."""
+def lm_head_cross_entropy(x, weight, labels, chunk: int = 8192, ignore_index: int = -100):
+    """Mean cross-entropy of logits x W^T against labels, skipping tokens whose
+    label is ``ignore_index`` (F.cross_entropy's default -100); x [..., h] is
+    flattened over its leading dims."""
     h = x.shape[-1]
     return LMHeadCrossEntropyFunction.apply(x.reshape(-1, h), weight, labels.reshape(-1),
-                                            int(chunk))
+                                            int(chunk), int(ignore_index))
 
 
 class OutputLayerLoss(torch.nn.Module):

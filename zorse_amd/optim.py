@@ -70,37 +70,53 @@ class FusedAdamW(torch.optim.Optimizer):
             with torch.enable_grad():
                 loss = closure()
         for group in self.param_groups:
-            b1, b2 = group["betas"]
             for p in group["params"]:
-                if p.grad is None:
-                    continue
-                if p.grad.is_sparse:
-                    raise RuntimeError("FusedAdamW does not support sparse gradients")
-                if not p.is_contiguous() or not p.grad.is_contiguous():
-                    raise ValueError("FusedAdamW needs contiguous parameters and gradients")
-                st = self._init_state(p)
-                if st["exp_avg"].device != p.device:
-                    for k in ("exp_avg", "exp_avg_sq", "master"):
-                        if k in st:
-                            st[k] = st[k].to(p.device)
-                st["step"] += 1
-                master = st.get("master")
-                hyper = dict(lr=group["lr"], beta1=b1, beta2=b2, eps=group["eps"],
-                             weight_decay=group["weight_decay"], step=st["step"])
-                regions = self._tcopies.get(p) if master is not None else None
-                if not regions:
-                    K.adamw_step(master if master is not None else p.view(-1),
-                                 p.grad.view(-1), st["exp_avg"], st["exp_avg_sq"],
-                                 lowp_out=p.view(-1) if master is not None else None, **hyper)
-                else:
-                    self._step_regions(p, st, master, regions, hyper)
-                # the kernel wrote p through a raw pointer: advance its version
-                # counter as an in-place torch op would, so caches keyed on it
-                # (compute-dtype weight copies, attention caches) see the update
-                torch.autograd.graph.increment_version(p)
-                for fn in self._step_hooks.get(p, ()):
-                    fn(p)
+                if p.grad is not None:
+                    self._step_one(group, p)
         return loss
+
+    @torch.no_grad()
+    def step_param(self, p: torch.Tensor) -> None:
+        """Step ``p`` alone (the other parameters of this optimizer are left
+        as they are, whatever their gradients): the per-parameter step of an
+        optimizer-in-backward hook, which fires once per parameter as its
+        gradient completes.  No-op when ``p.grad`` is None."""
+        for group in self.param_groups:
+            for q in group["params"]:
+                if q is p:
+                    if p.grad is not None:
+                        self._step_one(group, p)
+                    return
+        raise ValueError("step_param: the tensor is not a parameter of this optimizer")
+
+    def _step_one(self, group: dict, p: torch.Tensor) -> None:
+        b1, b2 = group["betas"]
+        if p.grad.is_sparse:
+            raise RuntimeError("FusedAdamW does not support sparse gradients")
+        if not p.is_contiguous() or not p.grad.is_contiguous():
+            raise ValueError("FusedAdamW needs contiguous parameters and gradients")
+        st = self._init_state(p)
+        if st["exp_avg"].device != p.device:
+            for k in ("exp_avg", "exp_avg_sq", "master"):
+                if k in st:
+                    st[k] = st[k].to(p.device)
+        st["step"] += 1
+        master = st.get("master")
+        hyper = dict(lr=group["lr"], beta1=b1, beta2=b2, eps=group["eps"],
+                     weight_decay=group["weight_decay"], step=st["step"])
+        regions = self._tcopies.get(p) if master is not None else None
+        if not regions:
+            K.adamw_step(master if master is not None else p.view(-1),
+                         p.grad.view(-1), st["exp_avg"], st["exp_avg_sq"],
+                         lowp_out=p.view(-1) if master is not None else None, **hyper)
+        else:
+            self._step_regions(p, st, master, regions, hyper)
+        # the kernel wrote p through a raw pointer: advance its version
+        # counter as an in-place torch op would, so caches keyed on it
+        # (compute-dtype weight copies, attention caches) see the update
+        torch.autograd.graph.increment_version(p)
+        for fn in self._step_hooks.get(p, ()):
+            fn(p)
 
     @staticmethod
     def _step_regions(p, st, master, regions, hyper):

@@ -126,7 +126,9 @@ class StageRunner:
         side.wait_stream(cur)
         with torch.cuda.stream(side):
             grad = p.grad
-            opt.step()
+            # this parameter only: a layer with several parameters gets one
+            # hook call per parameter, and each must be stepped exactly once
+            opt.step_param(p)
             grad.record_stream(side)
             p.grad = None
 
