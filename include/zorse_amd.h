@@ -82,6 +82,26 @@ int zk_rmsnorm_bwd(const void* dy, const void* h, const void* w,
                    int64_t rows, int64_t hidden, int act_dtype, int w_dtype,
                    zk_stream_t stream);
 
+/* zk_rmsnorm_bwd without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  No counterpart in the reference.  The
+ * dw partial rows go to a static device array of
+ * ZK_RMSNORM_BWD_SCRATCH_FLOATS floats (16 MiB) that each GPU the library
+ * runs on holds until the process ends; its address is looked up on the
+ * first call on a device, which must be the current device (the stream must
+ * belong to it).  The entry point allocates nothing.  (rows, hidden) whose
+ * zk_rmsnorm_bwd_workspace() exceeds the array are rejected with
+ * ZK_EWORKSPACE (any rows at hidden <= 8192: at most 512 partial rows).
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (different streams, or concurrent host threads) race and must be
+ * serialised by the caller.  Results are identical to zk_rmsnorm_bwd's. */
+#define ZK_RMSNORM_BWD_SCRATCH_FLOATS ((int64_t)4 << 20)
+int zk_rmsnorm_bwd_noalloc(const void* dy, const void* h, const void* w,
+                           const float* rstd, const void* dres, void* dx,
+                           void* dw, int accumulate, int64_t rows,
+                           int64_t hidden, int act_dtype, int w_dtype,
+                           zk_stream_t stream);
+
 /* ----------------------------------------------------------------- SwiGLU --
  * Replaces the activation of HF LlamaMLP.forward, act_fn(gate(x)) * up(x)
  * (imported at models/llama_simple.py:10, built at :418; torchtitan

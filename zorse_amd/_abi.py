@@ -76,6 +76,8 @@ SIGNATURES = {
     "zk_rmsnorm_bwd_workspace": (_i64, [_i64, _i64]),
     "zk_rmsnorm_bwd": (_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _int,
                               _ptr, _i64, _i64, _i64, _int, _int, _ptr]),
+    "zk_rmsnorm_bwd_noalloc": (_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _int,
+                                      _i64, _i64, _int, _int, _ptr]),
     "zk_swiglu_fwd": (_int, [_ptr, _ptr, _i64, _ptr, _i64, _i64, _i64, _int, _ptr]),
     "zk_swiglu_bwd": (_int, [_ptr, _i64, _ptr, _ptr, _i64, _ptr, _ptr, _i64,
                              _i64, _i64, _int, _ptr]),

@@ -13,6 +13,8 @@
 // reduces deterministically (no atomics).  Rows whose width is not a
 // multiple of 8, wider than 8192, or misaligned buffers take the scalar
 // kernels, which read the row twice.
+#include <mutex>
+
 #include "vec.h"
 
 namespace zk {
@@ -466,24 +468,21 @@ extern "C" int64_t zk_rmsnorm_bwd_workspace(int64_t rows, int64_t hidden) {
   return parts * hidden;
 }
 
-extern "C" int zk_rmsnorm_bwd(const void* dy, const void* h, const void* w,
-                              const float* rstd, const void* dres, void* dx,
-                              void* dw, int accumulate, float* workspace,
-                              int64_t workspace_elems, int64_t rows,
-                              int64_t hidden, int act_dtype, int w_dtype,
-                              zk_stream_t stream) {
-  ZK_REQUIRE(valid_dtype(act_dtype) && valid_dtype(w_dtype), ZK_EDTYPE,
-             "zk_rmsnorm_bwd: bad dtype code (%d, %d)", act_dtype, w_dtype);
-  ZK_REQUIRE(rows >= 0 && hidden > 0, ZK_EINVAL,
-             "zk_rmsnorm_bwd: bad shape rows=%lld hidden=%lld",
-             (long long)rows, (long long)hidden);
-  ZK_REQUIRE(dy && h && w && rstd && dx && dw, ZK_EINVAL,
-             "zk_rmsnorm_bwd: null pointer");
+namespace zk {
+
+// The backward of both entry points, with the dw partial rows in `workspace`
+// (workspace_elems floats, at least zk_rmsnorm_bwd_workspace(rows, hidden)).
+// Every launched workgroup writes its whole partial row before the reduction
+// reads it, so the workspace needs no clearing.
+static int rmsnorm_bwd_impl(const char* who, const void* dy, const void* h, const void* w,
+                            const float* rstd, const void* dres, void* dx, void* dw,
+                            int accumulate, float* workspace, int64_t workspace_elems,
+                            int64_t rows, int64_t hidden, int act_dtype, int w_dtype,
+                            hipStream_t s) {
   const int64_t need = zk_rmsnorm_bwd_workspace(rows, hidden);
   ZK_REQUIRE(workspace_elems >= need && (need == 0 || workspace != nullptr),
-             ZK_EWORKSPACE, "zk_rmsnorm_bwd: workspace %lld < %lld floats",
+             ZK_EWORKSPACE, "%s: workspace %lld < %lld floats", who,
              (long long)workspace_elems, (long long)need);
-  hipStream_t s = as_stream(stream);
   const int64_t parts = rows == 0 ? 0 : need / hidden;
   if (rows == 0) {
     // nothing to differentiate; the reduce below writes dw = 0 (or keeps it)
@@ -498,5 +497,89 @@ extern "C" int zk_rmsnorm_bwd(const void* dy, const void* h, const void* w,
   }
   hipLaunchKernelGGL(rmsnorm_dw_reduce, dim3((hidden + 63) / 64), dim3(1024),
                      0, s, workspace, parts, hidden, dw, w_dtype, accumulate);
-  return launch_status("zk_rmsnorm_bwd");
+  return launch_status(who);
+}
+
+static int check_bwd_args(const char* who, const void* dy, const void* h, const void* w,
+                          const float* rstd, const void* dx, const void* dw, int64_t rows,
+                          int64_t hidden, int act_dtype, int w_dtype) {
+  ZK_REQUIRE(valid_dtype(act_dtype) && valid_dtype(w_dtype), ZK_EDTYPE,
+             "%s: bad dtype code (%d, %d)", who, act_dtype, w_dtype);
+  ZK_REQUIRE(rows >= 0 && hidden > 0, ZK_EINVAL, "%s: bad shape rows=%lld hidden=%lld", who,
+             (long long)rows, (long long)hidden);
+  ZK_REQUIRE(dy && h && w && rstd && dx && dw, ZK_EINVAL, "%s: null pointer", who);
+  return ZK_OK;
+}
+
+// ---- the allocation-free variant's scratch ---------------------------------
+// The dw partial rows of zk_rmsnorm_bwd_noalloc live in this file-scope device
+// array: every GPU the library runs on holds its own copy (16 MiB) until the
+// process ends.  Host code never passes the array's name to a kernel (on the
+// host it is a stand-in, not a device address): the device address comes
+// from hipGetSymbolAddress, looked up once per device with that device
+// current, and that pointer is what the kernels receive.
+static __device__ __align__(256) float scratch[ZK_RMSNORM_BWD_SCRATCH_FLOATS];
+
+static constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static float* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of the current device's scratch array.
+static int scratch_for_current_device(const char* who, float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  ZK_REQUIRE(e == hipSuccess, static_cast<int>(e), "%s: hipGetDevice failed: %s", who,
+             hipGetErrorString(e));
+  ZK_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, ZK_EUNSUPPORTED,
+             "%s: device %d beyond the %d the scratch table holds", who, dev,
+             kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    ZK_REQUIRE(e == hipSuccess && p != nullptr, e == hipSuccess ? ZK_EINVAL : static_cast<int>(e),
+               "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", who, dev,
+               hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return ZK_OK;
+}
+
+}  // namespace zk
+
+extern "C" int zk_rmsnorm_bwd(const void* dy, const void* h, const void* w,
+                              const float* rstd, const void* dres, void* dx,
+                              void* dw, int accumulate, float* workspace,
+                              int64_t workspace_elems, int64_t rows,
+                              int64_t hidden, int act_dtype, int w_dtype,
+                              zk_stream_t stream) {
+  const int rc = check_bwd_args("zk_rmsnorm_bwd", dy, h, w, rstd, dx, dw, rows, hidden,
+                                act_dtype, w_dtype);
+  if (rc != ZK_OK) return rc;
+  return rmsnorm_bwd_impl("zk_rmsnorm_bwd", dy, h, w, rstd, dres, dx, dw, accumulate,
+                          workspace, workspace_elems, rows, hidden, act_dtype, w_dtype,
+                          as_stream(stream));
+}
+
+extern "C" int zk_rmsnorm_bwd_noalloc(const void* dy, const void* h, const void* w,
+                                      const float* rstd, const void* dres, void* dx,
+                                      void* dw, int accumulate, int64_t rows,
+                                      int64_t hidden, int act_dtype, int w_dtype,
+                                      zk_stream_t stream) {
+  const char* who = "zk_rmsnorm_bwd_noalloc";
+  int rc = check_bwd_args(who, dy, h, w, rstd, dx, dw, rows, hidden, act_dtype, w_dtype);
+  if (rc != ZK_OK) return rc;
+  const int64_t need = zk_rmsnorm_bwd_workspace(rows, hidden);
+  ZK_REQUIRE(need <= ZK_RMSNORM_BWD_SCRATCH_FLOATS, ZK_EWORKSPACE,
+             "%s: rows=%lld hidden=%lld need %lld floats of scratch, more than the static "
+             "%lld (ZK_RMSNORM_BWD_SCRATCH_FLOATS); use zk_rmsnorm_bwd with a workspace",
+             who, (long long)rows, (long long)hidden, (long long)need,
+             (long long)ZK_RMSNORM_BWD_SCRATCH_FLOATS);
+  float* ws = nullptr;
+  rc = scratch_for_current_device(who, &ws);
+  if (rc != ZK_OK) return rc;
+  return rmsnorm_bwd_impl(who, dy, h, w, rstd, dres, dx, dw, accumulate, ws,
+                          ZK_RMSNORM_BWD_SCRATCH_FLOATS, rows, hidden, act_dtype, w_dtype,
+                          as_stream(stream));
 }
