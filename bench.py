@@ -253,29 +253,137 @@ def measure_kernels(dev, spec, S):
     return rows
 
 
+def host_cpu() -> dict:
+    """The host CPU as lscpu names it: model, sockets x cores x threads per
+    core, and the CPUs this process may run on."""
+    info = {}
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], stdout=subprocess.PIPE, stderr=subprocess.DEVNULL,
+                             text=True, timeout=20).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            info[key.strip()] = val.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return {"model": info.get("Model name"), "sockets": info.get("Socket(s)"),
+            "cores_per_socket": info.get("Core(s) per socket"),
+            "threads_per_core": info.get("Thread(s) per core"), "cpus": info.get("CPU(s)"),
+            "usable_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity")
+            else os.cpu_count()}
+
+
+def cpu_threads() -> int:
+    """Threads for the CPU baseline: the host's CPU count, capped by the CPU
+    share the GPU box gives one GPU's job (OMP_NUM_THREADS, set to that share
+    on the box; a larger count would oversubscribe the cores other jobs on
+    the host hold)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    share = os.environ.get("OMP_NUM_THREADS")
+    if share and share.isdigit() and int(share) > 0:
+        n = min(n, int(share))
+    return max(1, n or 1)
+
+
 def cpu_baseline(spec, S, seed=3):
     """The CPU oracle (plain PyTorch, fp32) timed on one layer's fwd+bwd at the
-    stage's shape -- a bounded sample (1 of the 8 layers, 1 iteration after a
-    short warm-up) of the same workload, on the host's cores."""
+    stage's shape -- a bounded sample (1 of the 8 layers) of the same
+    workload, on the host's cores: one untimed iteration at the full shape
+    (warm-up), then one timed iteration."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import decoder as O
-    threads = min(os.cpu_count() or 1, 16)
+    threads = cpu_threads()
     torch.set_num_threads(threads)
     shape = O.LayerShape(hidden=spec.hidden, heads=spec.heads, kv_heads=spec.kv_heads,
                          head_dim=spec.head_dim, ffn=spec.ffn, theta=spec.rope_theta)
     g = torch.Generator().manual_seed(seed)
     p = O.init_params(shape, g)
-    warm_x = torch.randn(1, 128, spec.hidden, generator=g)
-    O.layer_fwd_bwd(warm_x, p, shape, torch.randn_like(warm_x))
     x = torch.randn(1, S, spec.hidden, generator=g)
     dout = torch.randn(1, S, spec.hidden, generator=g)
     t0 = time.perf_counter()
+    O.layer_fwd_bwd(x, p, shape, dout)       # warm-up at the full shape
+    warm = time.perf_counter() - t0
+    t0 = time.perf_counter()
     O.layer_fwd_bwd(x, p, shape, dout)
     dt = time.perf_counter() - t0
-    return {"value": round(S / dt, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"oracle (plain PyTorch fp32) fwd+bwd of 1 of the 8 layers at seq {S}, "
-                      f"1 timed iteration ({dt:.2f} s) on {threads} host threads",
+    cpu = host_cpu()
+    return {"value": round(S / dt, 1), "unit": "tokens/s", "cores": threads, "threads": threads,
+            "kind": "port", "host_cpu": cpu,
+            "sample": f"oracle (plain PyTorch fp32) fwd+bwd of 1 of the 8 layers at seq {S}: "
+                      f"1 warm-up iteration at the full shape ({warm:.2f} s), then 1 timed "
+                      f"iteration ({dt:.2f} s), torch.set_num_threads({threads}) on "
+                      f"{cpu.get('model')} ({cpu.get('usable_cpus')} usable CPUs; threads "
+                      f"capped at the job's CPU share)",
             "seconds": round(dt, 2)}
+
+
+def summarize_stage(root: str, layers: int, steps: int, warmup: int) -> str:
+    """Markdown summary of a rocprofv3 kernel trace of ``bench.py --steps
+    <steps> --warmup <warmup> --layers <layers>`` (``root/bench_kernel_trace.csv``
+    and ``root/bench_kernel_stats.csv``): kernel time per timed stage step by
+    group over the window from the end of the warm-up's last ``adamw_elem``
+    launch to the end of the last timed step's, the GPU's busy time in that
+    window (overlapping kernels counted once), and the whole run's kernel
+    table."""
+    import collections
+    import csv
+    trace = sorted(csv.DictReader(open(os.path.join(root, "bench_kernel_trace.csv"))),
+                   key=lambda r: int(r["Start_Timestamp"]))
+    adam = [r for r in trace if "adamw_elem" in r["Kernel_Name"]]
+    first, last = warmup * layers - 1, (warmup + steps) * layers - 1
+    if warmup < 1 or len(adam) <= last:
+        raise SystemExit(f"need >= 1 warm-up step and {last + 1} adamw_elem launches in the "
+                         f"trace ({len(adam)} found)")
+    t0, t1 = int(adam[first]["End_Timestamp"]), int(adam[last]["End_Timestamp"])
+    win = [r for r in trace
+           if int(r["Start_Timestamp"]) >= t0 and int(r["End_Timestamp"]) <= t1]
+    groups = [("hipBLASLt GEMMs", ("Cijk",)),
+              ("attention bwd: prep, dkdv, dq", ("attn_bwd",)),
+              ("AdamW (optimizer stream, overlapped)", ("adamw",)),
+              ("attention fwd", ("attn_fwd",)),
+              ("SwiGLU (with transposed outputs)", ("swiglu",)),
+              ("transposes (backward operands, optimizer W^T copies)", ("transpose",)),
+              ("RMSNorm fwd / bwd", ("rmsnorm",)), ("RoPE fwd / bwd", ("rope",)),
+              ("device copies", ("copyBuffer",))]
+    tot, other = collections.defaultdict(float), 0.0
+    for r in win:
+        d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6
+        for name, pats in groups:
+            if any(p in r["Kernel_Name"] for p in pats):
+                tot[name] += d
+                break
+        else:
+            other += d
+    allk = sum(tot.values()) + other
+    lines = ["| kernel group | ms per timed step | share of kernel time |", "|---|---|---|"]
+    for name, _ in groups:
+        lines.append(f"| {name} | {tot[name] / steps:.2f} | {100 * tot[name] / allk:.1f} % |")
+    if other > 0:
+        lines.append(f"| other | {other / steps:.2f} | {100 * other / allk:.1f} % |")
+    iv = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in win)
+    busy, (cs, ce) = 0, iv[0]
+    for a, b in iv[1:]:
+        if a > ce:
+            busy += ce - cs
+            cs, ce = a, b
+        else:
+            ce = max(ce, b)
+    busy += ce - cs
+    lines += ["", f"GPU busy over the {steps} timed steps: {busy / steps / 1e6:.2f} ms per step "
+                  f"(window {(t1 - t0) / steps / 1e6:.2f} ms per step)."]
+    rest = adam[last + 1:]
+    if rest:
+        avg = sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rest) / len(rest)
+        lines.append(f"bench.py's `adamw` case after the stage: {len(rest)} launches of "
+                     f"`adamw_elem`, {avg / 1e6:.3f} ms on average.")
+    lines += ["", "All kernels of the run (rocprofv3 `bench_kernel_stats.csv`, top 30):", "",
+              "| kernel | calls | total ms | avg us | % |", "|---|---|---|---|---|"]
+    stats = list(csv.DictReader(open(os.path.join(root, "bench_kernel_stats.csv"))))
+    for r in stats[:30]:
+        lines.append(f"| `{r['Name'][:110]}` | {r['Calls']} | "
+                     f"{float(r['TotalDurationNs']) / 1e6:.2f} | "
+                     f"{float(r['AverageNs']) / 1e3:.1f} | {float(r['Percentage']):.2f} |")
+    return "\n".join(lines) + "\n"
 
 
 # kernel-case labels (as in the JSON line) and the rocprofv3 kernel names they cover
@@ -405,7 +513,15 @@ def main():
     ap.add_argument("--summarize-traffic", metavar="DIR",
                     help="print the HBM-traffic table from rocprofv3 --pmc runs of the kernel "
                          "cases under DIR and exit (no GPU needed)")
+    ap.add_argument("--summarize-stage", metavar="DIR",
+                    help="print the per-group kernel time of a rocprofv3 --kernel-trace --stats "
+                         "run of this bench (DIR holds bench_kernel_trace.csv / "
+                         "bench_kernel_stats.csv; pass that run's --steps / --warmup / "
+                         "--layers) and exit (no GPU needed)")
     args = ap.parse_args()
+    if args.summarize_stage:
+        print(summarize_stage(args.summarize_stage, args.layers, args.steps, args.warmup), end="")
+        return
     if args.summarize_mfma:
         print(summarize_mfma(args.summarize_mfma), end="")
         return
