@@ -199,7 +199,8 @@ typedef struct zk_attn_desc {
 int zk_attn_fwd(const zk_attn_desc* desc, const void* q, const void* k,
                 const void* v, void* o, float* lse, zk_stream_t stream);
 
-/* Bytes of workspace zk_attn_bwd needs (fp32 dQ accumulator + row deltas). */
+/* Bytes of workspace zk_attn_bwd needs: the fp32 row deltas rowsum(dO o O)
+ * and the log2-domain LSE, [B, Hq, Sq] each. */
 int64_t zk_attn_bwd_workspace(const zk_attn_desc* desc);
 
 /* Backward (FlashAttention-2 recomputation from lse): writes dq, dk, dv
@@ -209,6 +210,21 @@ int zk_attn_bwd(const zk_attn_desc* desc, const void* q, const void* k,
                 const void* v, const void* o, const void* dout,
                 const float* lse, void* dq, void* dk, void* dv,
                 void* workspace, int64_t workspace_bytes, zk_stream_t stream);
+
+/* zk_attn_bwd for Q / K that the forward rotated with RoPE: dq and dk are
+ * stored already taken back through the rotation (its transpose), i.e. they
+ * are the gradients with respect to the un-rotated q and k -- the backward of
+ * apply_rotary_pos_emb (models/llama_simple.py:34-58, half-split pairing) or
+ * apply_rotary_emb (models/llama_v2.py:151-177, interleaved pairing) fused
+ * into the attention backward.  cos / sin, n_pos, positions and pairing as
+ * for zk_rope (the tables the forward rotation used; positions NULL means
+ * 0 .. S-1, which needs n_pos >= Sq).  Needs Sq == Skv. */
+int zk_attn_bwd_rope(const zk_attn_desc* desc, const void* q, const void* k,
+                     const void* v, const void* o, const void* dout,
+                     const float* lse, void* dq, void* dk, void* dv,
+                     void* workspace, int64_t workspace_bytes,
+                     const float* cos, const float* sin, int64_t n_pos,
+                     const int64_t* positions, int pairing, zk_stream_t stream);
 
 /* ------------------------------------------------------------------ AdamW --
  * Replaces torch.optim.Adam(fused=True).step() on the layer's flat fp32

@@ -292,6 +292,62 @@ def test_flash_attention_autograd_with_rope(dev, dtype):
     assert_close(vd.grad, va.grad, dtype, "dv")
 
 
+ROPE_BWD_CASES = [
+    # B, S, Hq, Hkv, d, window, interleaved, explicit positions, dtype
+    (1, 256, 4, 1, 128, 0, False, False, torch.bfloat16),
+    (2, 160, 4, 2, 64, 48, False, True, torch.float16),
+    (1, 200, 2, 2, 128, 0, True, False, torch.bfloat16),
+    (1, 96, 4, 2, 64, 0, True, True, torch.float32),
+]
+
+
+@pytest.mark.parametrize("case", ROPE_BWD_CASES, ids=lambda c: "-".join(str(v) for v in c))
+def test_attention_bwd_fused_inverse_rope(dev, case):
+    """zk_attn_bwd_rope: the attention backward that also takes dq / dk back
+    through RoPE's rotation, against the fp64 oracle's autograd through the
+    rotation and the attention (so the rotation's transpose, the pairing and
+    the positions are all checked), and against the unfused path (attention
+    backward, then the inverse zk_rope pass) within the dtype's bar."""
+    from zorse_amd import kernels as K
+    from zorse_amd.functional import rope_tables
+    B, S, Hq, Hkv, d, window, inter, explicit, dtype = case
+    print(f"attention bwd + inverse rope {case}", flush=True)
+    theta = 1e4
+    g = torch.Generator().manual_seed(S + d)
+    pos = (torch.randperm(S, generator=g) + 5) if explicit else None
+    n_pos = int(pos.max()) + 1 if explicit else S
+    cos, sin = rope_tables(n_pos, d, theta, dtype, dev, inter)
+    q0 = _rand((B, S, Hq, d), dtype, 60)
+    k0 = _rand((B, S, Hkv, d), dtype, 61)
+    v = _rand((B, S, Hkv, d), dtype, 62)
+    do = _rand((B, S, Hq, d), dtype, 63)
+    q, k = q0.to(dev), k0.to(dev)
+    pdev = pos.to(dev) if explicit else None
+    K.rope_(q, k, cos, sin, positions=pdev, interleaved=inter)
+    o, lse = K.attn_fwd(q, k, v.to(dev), causal=True, window=window)
+    dq, dk, dv = K.attn_bwd(q, k, v.to(dev), o, do.to(dev), lse, causal=True, window=window,
+                            rope=(cos, sin, pdev, inter))
+    # unfused: attention backward, then the inverse rotation pass
+    uq, uk, uv = K.attn_bwd(q, k, v.to(dev), o, do.to(dev), lse, causal=True, window=window)
+    K.rope_(uq, uk, cos, sin, positions=pdev, interleaved=inter, inverse=True)
+    # fp64 oracle: autograd through the same rotation (the reference's tables)
+    qa, ka, va = (t.double().requires_grad_(True) for t in (q0, k0, v))
+    if inter:
+        fc = O.rope_freqs_cis(d, n_pos, theta)
+        fc = fc[pos] if explicit else fc[:S]
+        rq, rk = O.apply_rope_interleaved(qa, ka, fc)
+    else:
+        c, s_ = O.rope_cos_sin(S, d, theta, dtype, positions=pos)
+        rq, rk = O.apply_rope_half(qa, ka, c.double(), s_.double())
+    ro, _ = O.attention(rq, rk, va, True, window)
+    ro.backward(do.double())
+    for name, got, ref, unf in (("dq", dq, qa.grad, uq), ("dk", dk, ka.grad, uk),
+                                ("dv", dv, va.grad, uv)):
+        assert_close(got, ref, dtype, name)
+        assert_close(got, unf.double(), dtype, name + " vs unfused")
+    assert torch.equal(dv, uv)
+
+
 # ------------------------------------------------------------------ AdamW --
 
 @pytest.mark.parametrize("gdt", ALL)

@@ -95,6 +95,9 @@ SIGNATURES = {
     "zk_attn_bwd_workspace": (_i64, [ctypes.POINTER(AttnDesc)]),
     "zk_attn_bwd": (_int, [ctypes.POINTER(AttnDesc), _ptr, _ptr, _ptr, _ptr,
                            _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr]),
+    "zk_attn_bwd_rope": (_int, [ctypes.POINTER(AttnDesc), _ptr, _ptr, _ptr, _ptr,
+                                _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _ptr, _i64,
+                                _ptr, _int, _ptr]),
     "zk_adamw_step": (_int, [_ptr, _ptr, _int, _ptr, _ptr, _ptr, _int, _i64,
                              _f64, _f64, _f64, _f64, _f64, _i64, _ptr]),
     "zk_adamw_step_t": (_int, [_ptr, _ptr, _int, _ptr, _ptr, _ptr, _int, _ptr, _int, _i64,

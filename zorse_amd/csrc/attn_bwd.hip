@@ -382,6 +382,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv(AttnArgs a) {
   // dK = scale (Q^T dS)^T, dV = (dO^T P)^T: lane holds key my_key and
   // d rows 32 nt + 8 a4 + 4 g + 0..3 (4 consecutive elements).
   if (my_key < a.Skv) {
+    if (a.rope_cos != nullptr) rope_inverse_regs<D>(dk, a, my_key, g);
     typedef T T4 __attribute__((ext_vector_type(4)));
     T* dkp = static_cast<T*>(a.dk) + b * a.dk_sb + hk * a.dk_sh + my_key * a.dk_ss;
     T* dvp = static_cast<T*>(a.dv) + b * a.dv_sb + hk * a.dv_sh + my_key * a.dv_ss;
@@ -571,6 +572,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) 
   }
 
   if (my_q < a.Sq) {
+    if (a.rope_cos != nullptr) rope_inverse_regs<D>(dq, a, my_q, g);
     typedef T T4 __attribute__((ext_vector_type(4)));
     T* dqp = static_cast<T*>(a.dq) + b * a.dq_sb + hq * a.dq_sh + my_q * a.dq_ss;
 #pragma unroll
@@ -588,6 +590,24 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) 
 
 // ------------------------------------------------------------- fp32 path ---
 // Simple per-row kernels for fp32 layers (small shapes, no MFMA).
+
+// The inverse RoPE rotation of one row x[0 .. d) at sequence position `row`
+// (the same pairings and formula as rope_inverse_regs).
+__device__ __forceinline__ void rope_inverse_row(float* x, const AttnArgs& a, int64_t row) {
+  int64_t pos = a.rope_pos != nullptr ? a.rope_pos[row] : row;
+  if (pos < 0) pos = 0;
+  if (pos > a.rope_npos - 1) pos = a.rope_npos - 1;
+  const int64_t half = a.d / 2;
+  const float* ct = a.rope_cos + pos * half;
+  const float* st = a.rope_sin + pos * half;
+  for (int64_t i = 0; i < half; ++i) {
+    const int64_t ia = a.rope_interleaved ? 2 * i : i;
+    const int64_t ib = a.rope_interleaved ? 2 * i + 1 : i + half;
+    const float u = x[ia], w = x[ib];
+    x[ia] = fmaf(u, ct[i], w * st[i]);
+    x[ib] = fmaf(w, ct[i], -u * st[i]);
+  }
+}
 template <int D>
 __global__ __launch_bounds__(64) void attn_bwd_dq_f32(AttnArgs a) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
@@ -615,6 +635,7 @@ __global__ __launch_bounds__(64) void attn_bwd_dq_f32(AttnArgs a) {
     const float ds = p * (dp - del) * a.scale;
     for (int e = 0; e < a.d; ++e) acc[e] = fmaf(ds, kr[e], acc[e]);
   }
+  if (a.rope_cos != nullptr) rope_inverse_row(acc, a, qi);
   float* dq = static_cast<float*>(a.dq) + b * a.dq_sb + hq * a.dq_sh + qi * a.dq_ss;
   for (int e = 0; e < a.d; ++e) dq[e] = acc[e];
 }
@@ -653,6 +674,7 @@ __global__ __launch_bounds__(64) void attn_bwd_dkv_f32(AttnArgs a) {
       }
     }
   }
+  if (a.rope_cos != nullptr) rope_inverse_row(dk, a, kj);
   float* dkp = static_cast<float*>(a.dk) + b * a.dk_sb + hk * a.dk_sh + kj * a.dk_ss;
   float* dvp = static_cast<float*>(a.dv) + b * a.dv_sb + hk * a.dv_sh + kj * a.dv_ss;
   for (int e = 0; e < a.d; ++e) { dkp[e] = dk[e]; dvp[e] = dv[e]; }
@@ -668,22 +690,77 @@ extern "C" int64_t zk_attn_bwd_workspace(const zk_attn_desc* desc) {
   return 2 * rows * 4 + 512;
 }
 
+namespace zk {
+struct RopeInv {
+  const float* cos;
+  const float* sin;
+  int64_t n_pos;
+  const int64_t* positions;
+  int pairing;
+};
+
+static int attn_bwd_impl(const char* who, const zk_attn_desc* desc, const void* q,
+                         const void* k, const void* v, const void* o, const void* dout,
+                         const float* lse, void* dq, void* dk, void* dv, void* workspace,
+                         int64_t workspace_bytes, const RopeInv* rope, zk_stream_t stream);
+}  // namespace zk
+
 extern "C" int zk_attn_bwd(const zk_attn_desc* desc, const void* q,
                            const void* k, const void* v, const void* o,
                            const void* dout, const float* lse, void* dq,
                            void* dk, void* dv, void* workspace,
                            int64_t workspace_bytes, zk_stream_t stream) {
-  int rc = check_attn_desc(desc, "zk_attn_bwd", true);
+  return attn_bwd_impl("zk_attn_bwd", desc, q, k, v, o, dout, lse, dq, dk, dv, workspace,
+                       workspace_bytes, nullptr, stream);
+}
+
+extern "C" int zk_attn_bwd_rope(const zk_attn_desc* desc, const void* q, const void* k,
+                                const void* v, const void* o, const void* dout,
+                                const float* lse, void* dq, void* dk, void* dv,
+                                void* workspace, int64_t workspace_bytes, const float* cos,
+                                const float* sin, int64_t n_pos, const int64_t* positions,
+                                int pairing, zk_stream_t stream) {
+  const char* who = "zk_attn_bwd_rope";
+  ZK_REQUIRE(cos != nullptr && sin != nullptr, ZK_EINVAL, "%s: null RoPE table", who);
+  ZK_REQUIRE(pairing == ZK_ROPE_HALF || pairing == ZK_ROPE_INTERLEAVED, ZK_EINVAL,
+             "%s: bad pairing %d", who, pairing);
+  ZK_REQUIRE(n_pos > 0, ZK_EINVAL, "%s: empty RoPE table", who);
+  ZK_REQUIRE(desc == nullptr || positions != nullptr || n_pos >= desc->Sq, ZK_EINVAL,
+             "%s: table holds %lld positions < S=%lld", who, (long long)n_pos,
+             (long long)(desc ? desc->Sq : 0));
+  ZK_REQUIRE(desc == nullptr || desc->d % 2 == 0, ZK_EINVAL, "%s: odd head_dim", who);
+  ZK_REQUIRE(aligned(cos, 16) && aligned(sin, 16), ZK_EALIGN,
+             "%s: RoPE tables must be 16-byte aligned", who);
+  const RopeInv r = {cos, sin, n_pos, positions, pairing};
+  return attn_bwd_impl(who, desc, q, k, v, o, dout, lse, dq, dk, dv, workspace,
+                       workspace_bytes, &r, stream);
+}
+
+namespace zk {
+static int attn_bwd_impl(const char* who, const zk_attn_desc* desc, const void* q,
+                         const void* k, const void* v, const void* o, const void* dout,
+                         const float* lse, void* dq, void* dk, void* dv, void* workspace,
+                         int64_t workspace_bytes, const RopeInv* rope, zk_stream_t stream) {
+  int rc = check_attn_desc(desc, who, true);
   if (rc != ZK_OK) return rc;
+  ZK_REQUIRE(rope == nullptr || desc->Sq == desc->Skv, ZK_EUNSUPPORTED,
+             "%s: fused RoPE needs Sq == Skv", who);
   const int64_t need = zk_attn_bwd_workspace(desc);
   ZK_REQUIRE(workspace != nullptr && workspace_bytes >= need, ZK_EWORKSPACE,
-             "zk_attn_bwd: workspace %lld < %lld bytes",
+             "%s: workspace %lld < %lld bytes", who,
              (long long)workspace_bytes, (long long)need);
   if (desc->B == 0 || (desc->Sq == 0 && desc->Skv == 0)) return ZK_OK;
   ZK_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv, ZK_EINVAL,
-             "zk_attn_bwd: null pointer");
+             "%s: null pointer", who);
   AttnArgs a = {};
   fill_args(a, desc);
+  if (rope != nullptr) {
+    a.rope_cos = rope->cos;
+    a.rope_sin = rope->sin;
+    a.rope_npos = rope->n_pos;
+    a.rope_pos = rope->positions;
+    a.rope_interleaved = rope->pairing == ZK_ROPE_INTERLEAVED;
+  }
   a.q = q; a.k = k; a.v = v; a.o = o; a.dout = dout; a.lse = lse;
   a.dq = dq; a.dk = dk; a.dv = dv;
   const uintptr_t base = (reinterpret_cast<uintptr_t>(workspace) + 255) & ~uintptr_t(255);
@@ -704,11 +781,11 @@ extern "C" int zk_attn_bwd(const zk_attn_desc* desc, const void* q,
       if (qrows > 0) hipLaunchKernelGGL(attn_bwd_dq_f32<128>, dim3((qrows + 63) / 64), dim3(64), 0, s, a);
       if (krows > 0) hipLaunchKernelGGL(attn_bwd_dkv_f32<128>, dim3((krows + 63) / 64), dim3(64), 0, s, a);
     }
-    return launch_status("zk_attn_bwd");
+    return launch_status(who);
   }
   ZK_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(o, 16) &&
                  aligned(dout, 16) && aligned(dq, 8) && aligned(dk, 8) && aligned(dv, 8),
-             ZK_EALIGN, "zk_attn_bwd: tensors must be 16-byte aligned");
+             ZK_EALIGN, "%s: tensors must be 16-byte aligned", who);
   const int64_t n_kt = (desc->Skv + DkdvCfg<128>::BK - 1) / DkdvCfg<128>::BK;
   const int64_t n_qt = (desc->Sq + DqCfg<128>::BM - 1) / DqCfg<128>::BM;
   const dim3 kgrid(static_cast<unsigned>(n_kt * desc->B * desc->Hkv));
@@ -747,5 +824,6 @@ extern "C" int zk_attn_bwd(const zk_attn_desc* desc, const void* q,
     if (desc->d == 128) ZK_BWD(f16, 128); else ZK_BWD(f16, 64);
   }
 #undef ZK_BWD
-  return launch_status("zk_attn_bwd");
+  return launch_status(who);
 }
+}  // namespace zk

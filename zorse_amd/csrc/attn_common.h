@@ -19,7 +19,6 @@ struct AttnArgs {
   void* dq;
   void* dk;
   void* dv;
-  float* dq_acc;  // backward workspace: fp32 [B, Sq, Hq, d]
   float* delta;   // backward workspace: fp32 [B, Hq, Sq]
   float* lse2;    // backward workspace: lse * log2(e), fp32 [B, Hq, Sq]
   int64_t B, Sq, Skv, Hq, Hkv, d;
@@ -34,6 +33,15 @@ struct AttnArgs {
   float scale_log2;  // scale * log2(e)
   int causal;
   int64_t window;
+  // backward only, optional: the transpose of the RoPE rotation the forward
+  // applied to Q and K, applied to dQ and dK before they are stored.  fp32
+  // tables [rope_npos, d/2] (cos, sin), positions int64 [S] or null for
+  // 0 .. S-1; rope_cos == null: no rotation.
+  const float* rope_cos;
+  const float* rope_sin;
+  const int64_t* rope_pos;
+  int64_t rope_npos;
+  int rope_interleaved;
 };
 
 // MFMA selection by storage type: 32x32x16 with fp32 accumulation.
@@ -55,6 +63,59 @@ struct Mfma<f16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
 };
+
+// Transpose of the RoPE rotation, in registers.  x[nt][j] holds element
+// d = 32 nt + 8 (j / 4) + 4 g + j % 4 of one row at sequence position `row`
+// (the MFMA accumulator layout of a lane whose half is g), already in fp32.
+// Half-split pairing (models/llama_simple.py:27-58): pairs (i, i + D / 2),
+// i.e. nt and nt + D / 64 with the same j; interleaved pairing
+// (models/llama_v2.py:151-177): pairs (2i, 2i + 1), i.e. j and j + 1 for
+// even j.  With c, s the table values of pair i at the row's position, the
+// forward rotated (a, b) -> (a c - b s, a s + b c); this applies
+// (a, b) -> (a c + b s, b c - a s).
+template <int D>
+__device__ __forceinline__ void rope_inverse_regs(f32x16 (&x)[D / 32], const AttnArgs& a,
+                                                  int64_t row, int g) {
+  int64_t pos = a.rope_pos != nullptr ? a.rope_pos[row] : row;
+  if (pos < 0) pos = 0;
+  if (pos > a.rope_npos - 1) pos = a.rope_npos - 1;
+  const float* ct = a.rope_cos + pos * (D / 2);
+  const float* st = a.rope_sin + pos * (D / 2);
+  if (a.rope_interleaved) {
+#pragma unroll
+    for (int nt = 0; nt < D / 32; ++nt)
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        const int d0 = 32 * nt + 8 * a4 + 4 * g;  // even: pairs (d0, d0+1), (d0+2, d0+3)
+        const float2 c2 = *reinterpret_cast<const float2*>(ct + d0 / 2);
+        const float2 s2 = *reinterpret_cast<const float2*>(st + d0 / 2);
+        const float cs[2] = {c2.x, c2.y}, sn[2] = {s2.x, s2.y};
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const float u = x[nt][4 * a4 + 2 * p], w = x[nt][4 * a4 + 2 * p + 1];
+          x[nt][4 * a4 + 2 * p] = fmaf(u, cs[p], w * sn[p]);
+          x[nt][4 * a4 + 2 * p + 1] = fmaf(w, cs[p], -u * sn[p]);
+        }
+      }
+  } else {
+    constexpr int HALF_NT = D / 64;
+#pragma unroll
+    for (int nt = 0; nt < HALF_NT; ++nt)
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        const int i0 = 32 * nt + 8 * a4 + 4 * g;  // 4 consecutive pair indices
+        const float4 c4 = *reinterpret_cast<const float4*>(ct + i0);
+        const float4 s4 = *reinterpret_cast<const float4*>(st + i0);
+        const float cs[4] = {c4.x, c4.y, c4.z, c4.w}, sn[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float u = x[nt][4 * a4 + e], w = x[nt + HALF_NT][4 * a4 + e];
+          x[nt][4 * a4 + e] = fmaf(u, cs[e], w * sn[e]);
+          x[nt + HALF_NT][4 * a4 + e] = fmaf(w, cs[e], -u * sn[e]);
+        }
+      }
+  }
+}
 
 // True when key `kj` is visible from query `qi`.
 __device__ __forceinline__ bool attn_visible(int64_t qi, int64_t kj,

@@ -128,12 +128,14 @@ class FlashAttentionFunction(torch.autograd.Function):
         do = do.contiguous()
         if do.stride() != o.stride():
             do = do.view(o.shape)
-        dq, dk, dv = K.attn_bwd(q, k, v, o, do, lse, causal=causal, window=window,
-                                scale=scale)
+        rope = None
         if rope_theta is not None:
             B, S, Hq, d = q.shape
             cos, sin = rope_tables(S, d, rope_theta, q.dtype, q.device, interleaved)
-            K.rope_(dq, dk, cos, sin, interleaved=interleaved, inverse=True)
+            rope = (cos, sin, None, interleaved)
+        # with RoPE the kernels also apply the rotation's transpose to dq / dk
+        dq, dk, dv = K.attn_bwd(q, k, v, o, do, lse, causal=causal, window=window,
+                                scale=scale, rope=rope)
         return dq, dk, dv, None, None, None, None, None
 
 

@@ -364,10 +364,16 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool 
 
 
 def attn_bwd(q, k, v, o, do, lse, *, causal: bool = True, window: int = 0,
-             scale: float | None = None, dq=None, dk=None, dv=None):
+             scale: float | None = None, dq=None, dk=None, dv=None, rope=None):
     """Flash attention backward.  Returns (dq, dk, dv); outputs may be given
-    as (strided) views, e.g. slices of one fused [T, (Hq+2Hkv) d] buffer."""
-    dev = _require_gpu(q, k, v, o, do, lse, dq, dk, dv)
+    as (strided) views, e.g. slices of one fused [T, (Hq+2Hkv) d] buffer.
+
+    ``rope`` = (cos, sin, positions, interleaved): q and k were rotated by
+    RoPE with these tables (as ``rope_``); dq and dk are then returned
+    through the transpose rotation, i.e. with respect to the un-rotated
+    q / k -- the inverse rope_ pass fused into the kernels."""
+    dev = _require_gpu(q, k, v, o, do, lse, dq, dk, dv,
+                       *(rope[:3] if rope is not None else ()))
     d = q.shape[3]
     if scale is None:
         scale = 1.0 / math.sqrt(d)
@@ -384,9 +390,30 @@ def attn_bwd(q, k, v, o, do, lse, *, causal: bool = True, window: int = 0,
     desc = _attn_desc(q, k, v, o, scale, causal, window, dq, dk, dv)
     nbytes = lib().zk_attn_bwd_workspace(desc)
     ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
-    check(lib().zk_attn_bwd(desc, ptr(q), ptr(k), ptr(v), ptr(o), ptr(do), ptr(lse),
-                            ptr(dq), ptr(dk), ptr(dv), ptr(ws), nbytes,
-                            stream_handle(dev)), "zk_attn_bwd")
+    if rope is None:
+        check(lib().zk_attn_bwd(desc, ptr(q), ptr(k), ptr(v), ptr(o), ptr(do), ptr(lse),
+                                ptr(dq), ptr(dk), ptr(dv), ptr(ws), nbytes,
+                                stream_handle(dev)), "zk_attn_bwd")
+        return dq, dk, dv
+    cos, sin, positions, interleaved = rope
+    d, S = q.shape[3], q.shape[1]
+    for name, t in (("cos", cos), ("sin", sin)):
+        if t.dtype != torch.float32 or t.dim() != 2 or t.shape[1] != d // 2 or \
+                not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous fp32 [n_pos, {d // 2}] table")
+    if cos.shape != sin.shape:
+        raise ValueError("cos and sin tables differ in shape")
+    if positions is not None:
+        if positions.dtype != torch.int64 or positions.numel() != S or \
+                not positions.is_contiguous():
+            raise ValueError("positions must be a contiguous int64 [S] tensor")
+    elif cos.shape[0] < S:
+        raise ValueError(f"table holds {cos.shape[0]} positions < S={S}")
+    check(lib().zk_attn_bwd_rope(desc, ptr(q), ptr(k), ptr(v), ptr(o), ptr(do), ptr(lse),
+                                 ptr(dq), ptr(dk), ptr(dv), ptr(ws), nbytes, ptr(cos), ptr(sin),
+                                 cos.shape[0], ptr(positions),
+                                 _abi.ZK_ROPE_INTERLEAVED if interleaved else _abi.ZK_ROPE_HALF,
+                                 stream_handle(dev)), "zk_attn_bwd_rope")
     return dq, dk, dv
 
 

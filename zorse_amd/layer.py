@@ -259,12 +259,12 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
     dv = dqkv[:, spec.q_dim + spec.kv_dim:].view(B, S, Hkv, d)
     for fn in list(BEFORE_ATTENTION_BACKWARD):
         fn()
-    K.attn_bwd(q, k, v, o2.view(B, S, Hq, d), do2.view(B, S, Hq, d), lse,
-               causal=spec.causal, window=spec.window, dq=dq, dk=dk, dv=dv)
-    del do2
+    # the attention backward also takes dq / dk back through RoPE's rotation
     cos, sin = _rope_for(S, spec, dout.dtype, dout.device, positions)
-    K.rope_(dq, dk, cos, sin, positions=positions, interleaved=spec.interleaved_rope,
-            inverse=True)
+    K.attn_bwd(q, k, v, o2.view(B, S, Hq, d), do2.view(B, S, Hq, d), lse,
+               causal=spec.causal, window=spec.window, dq=dq, dk=dk, dv=dv,
+               rope=(cos, sin, positions, spec.interleaved_rope))
+    del do2
     dn1 = _dgrad(dqkv, w.qkv, False, wt.get("qkv"))  # [T, h]
     _wgrad(dqkv, n1, g.qkv)
     del dqkv
