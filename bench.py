@@ -228,7 +228,7 @@ def measure_kernels(dev, spec, S):
     rows = {}
     spec_of = {
         "attn_fwd": ("attn_fwd_kernel<bf16,128,full>", "mfma", 20),
-        "attn_bwd": ("zk_attn_bwd (prep + attn_bwd_dkdv + attn_bwd_dq)", "mfma", 10),
+        "attn_bwd": ("zk_attn_bwd (attn_bwd_dq + attn_bwd_dkdv)", "mfma", 10),
         "rmsnorm_fwd": ("rmsnorm_fwd_vec<bf16,bf16,128,4>", "hbm", 32),
         "rmsnorm_bwd": ("rmsnorm_bwd_vec<bf16,bf16,256,2,2> + dw reduce", "hbm", 32),
         "adamw": ("adamw_elem<bf16,bf16,true>", "hbm", 10),
@@ -338,7 +338,7 @@ def summarize_stage(root: str, layers: int, steps: int, warmup: int) -> str:
     win = [r for r in trace
            if int(r["Start_Timestamp"]) >= t0 and int(r["End_Timestamp"]) <= t1]
     groups = [("hipBLASLt GEMMs", ("Cijk",)),
-              ("attention bwd: prep, dkdv, dq", ("attn_bwd",)),
+              ("attention bwd: dq, dkdv", ("attn_bwd",)),
               ("AdamW (optimizer stream, overlapped)", ("adamw",)),
               ("attention fwd", ("attn_fwd",)),
               ("SwiGLU (with transposed outputs)", ("swiglu",)),
@@ -389,8 +389,8 @@ def summarize_stage(root: str, layers: int, steps: int, warmup: int) -> str:
 # kernel-case labels (as in the JSON line) and the rocprofv3 kernel names they cover
 TRAFFIC_CASES = {
     "attn_fwd": ("attn_fwd_kernel<bf16,128,full>", ("attn_fwd_kernel",)),
-    "attn_bwd": ("zk_attn_bwd (prep + attn_bwd_dkdv + attn_bwd_dq)",
-                 ("attn_bwd_prep", "attn_bwd_dkdv", "attn_bwd_dq")),
+    "attn_bwd": ("zk_attn_bwd (attn_bwd_dq + attn_bwd_dkdv)",
+                 ("attn_bwd_dkdv", "attn_bwd_dq")),
     "rmsnorm_fwd": ("rmsnorm_fwd_vec<bf16,bf16,128,4>", ("rmsnorm_fwd_vec",)),
     "rmsnorm_bwd": ("rmsnorm_bwd_vec<bf16,bf16,256,2,2> + dw reduce",
                     ("rmsnorm_bwd_vec", "rmsnorm_dw_reduce")),

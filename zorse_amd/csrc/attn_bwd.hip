@@ -1,7 +1,14 @@
 // Flash-attention backward for gfx950 (bf16 / fp16 storage), atomic-free.
 //
-// Three kernels, all on the caller's stream:
-//  1. attn_bwd_prep: delta[b,h,i] = sum_d dO[i,d] * O[i,d] (fp32).
+// Two kernels, both on the caller's stream, in this order:
+//  1. attn_bwd_dq: Q-stationary (the forward's structure).  A workgroup owns
+//     128 queries of one (batch, q-head), 32 per wave with Q and dO rows in
+//     registers, and streams 64-key tiles of K and V through LDS:
+//       S^T = K Q^T,  dP^T = V dO^T,  dS^T = P^T (dP^T - delta),
+//       dQ^T += K^T dS^T              (K^T read transposed from LDS)
+//     Each lane owns one query, so lse and delta are per-lane scalars; the
+//     kernel first forms delta = rowsum(dO o O) from the dO row it holds and
+//     one read of O, and stores it with the log2-domain LSE for kernel 2.
 //  2. attn_bwd_dkdv: KV-stationary.  A workgroup owns 128 keys of one
 //     (batch, kv-head) -- 32 keys per wave, that wave's K rows held in
 //     registers and its V rows in LDS as MFMA B operands -- and loops over
@@ -14,16 +21,12 @@
 //     with dO^T / Q^T read transposed straight from the row-major LDS tiles
 //     (ds_read_tr16_b64) and P / dS fed from the score accumulators as the B
 //     operand (a fixed query permutation, matched by the transposed reads).
-//  3. attn_bwd_dq: Q-stationary (the forward's structure).  A workgroup owns
-//     128 queries of one (batch, q-head), 32 per wave with Q and dO rows in
-//     registers, and streams 64-key tiles of K and V through LDS:
-//       S^T = K Q^T,  dP^T = V dO^T,  dS^T = P^T (dP^T - delta),
-//       dQ^T += K^T dS^T              (K^T read transposed from LDS)
-//     Each lane owns one query, so lse and delta are per-lane scalars.
 // dQ is produced by its own pass instead of fp32 atomics into a shared
 // accumulator: S and dP are recomputed there (4 of the 14 d-length products
-// per pair), which costs less than device-scope atomic traffic and keeps the
-// result deterministic.
+// per pair), which costs less than device-scope atomic traffic (measured:
+// fp32 atomic adds into an L2-sized accumulator run at ~0.3 TB/s here) and
+// keeps the result deterministic.  With RoPE (zk_attn_bwd_rope) both
+// epilogues apply the rotation's transpose before storing dQ / dK.
 #include <type_traits>
 
 #include "attn_common.h"
@@ -35,9 +38,10 @@ int check_attn_desc(const zk_attn_desc* d, const char* who, bool bwd);
 void fill_args(AttnArgs& a, const zk_attn_desc* d);
 
 // ----------------------------------------------------------------- prep ----
-// 8 lanes per (b, q, h) row; each lane covers d/8 elements.  Writes
-// delta = rowsum(dO o O) and lse2 = lse * log2(e) (+inf for an empty row, so
-// that exp2(s - lse2) = 0), both fp32 [B, Hq, Sq].
+// fp32 path: 8 lanes per (b, q, h) row; each lane covers d/8 elements.
+// Writes delta = rowsum(dO o O) and lse2 = lse * log2(e) (+inf for an empty
+// row, so that exp2(s - lse2) = 0), both fp32 [B, Hq, Sq].  (The MFMA path
+// forms both inside attn_bwd_dq.)
 template <typename T>
 __global__ __launch_bounds__(256) void attn_bwd_prep(AttnArgs a) {
   const int64_t rows = a.B * a.Sq * a.Hq;
@@ -63,66 +67,6 @@ __global__ __launch_bounds__(256) void attn_bwd_prep(AttnArgs a) {
     a.delta[i] = acc;
     const float l = a.lse[i];
     a.lse2[i] = l == -INFINITY ? INFINITY : l * kLog2e;
-  }
-}
-
-// Vector variant for 2-byte storage and d = 64 / 128: D / 8 lanes per row,
-// 16-byte loads, grid (query blocks, B * Hq) so that the delta / lse2 writes
-// of a workgroup are consecutive queries of one head.
-template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_bwd_prep_vec(AttnArgs a) {
-  constexpr int LPR = D / 8;        // lanes per row
-  constexpr int RPB = 256 / LPR;    // rows per workgroup
-  const int64_t q = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
-  const int64_t bh = blockIdx.y;
-  const int64_t b = bh / a.Hq, h = bh % a.Hq;
-  const int sub = threadIdx.x % LPR;
-  float acc = 0.f;
-  if (q < a.Sq) {
-    const T* Or = static_cast<const T*>(a.o) + b * a.o_sb + q * a.o_ss + h * a.o_sh + 8 * sub;
-    const T* Dr = static_cast<const T*>(a.dout) + b * a.o_sb + q * a.o_ss + h * a.o_sh + 8 * sub;
-    float ov[8], dv[8];
-    Vec8<T>::load(Or, ov);
-    Vec8<T>::load(Dr, dv);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc = fmaf(ov[e], dv[e], acc);
-  }
-#pragma unroll
-  for (int off = 1; off < LPR; off <<= 1) acc += __shfl_xor(acc, off, 64);
-  if (q < a.Sq && sub == 0) {
-    const int64_t i = bh * a.Sq + q;
-    a.delta[i] = acc;
-    const float l = a.lse[i];
-    a.lse2[i] = l == -INFINITY ? INFINITY : l * kLog2e;
-  }
-}
-
-// Position-major variant for many heads: a workgroup takes every q-head row
-// of one (batch, query) -- with heads contiguous, one run of Hq d elements of
-// O and of dO -- D / 8 lanes per row, 256 / (D / 8) rows per pass.
-template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_bwd_prep_pos(AttnArgs a) {
-  constexpr int LPR = D / 8;
-  constexpr int RPP = 256 / LPR;  // head rows per pass
-  const int64_t q = blockIdx.x, b = blockIdx.y;
-  const int sub = threadIdx.x % LPR;
-  const T* Ob = static_cast<const T*>(a.o) + b * a.o_sb + q * a.o_ss + 8 * sub;
-  const T* Db = static_cast<const T*>(a.dout) + b * a.o_sb + q * a.o_ss + 8 * sub;
-  for (int64_t h = threadIdx.x / LPR; h < a.Hq; h += RPP) {
-    float ov[8], dv[8];
-    Vec8<T>::load(Ob + h * a.o_sh, ov);
-    Vec8<T>::load(Db + h * a.o_sh, dv);
-    float acc = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc = fmaf(ov[e], dv[e], acc);
-#pragma unroll
-    for (int off = 1; off < LPR; off <<= 1) acc += __shfl_xor(acc, off, 64);
-    if (sub == 0) {
-      const int64_t i = (b * a.Hq + h) * a.Sq + q;
-      a.delta[i] = acc;
-      const float l = a.lse[i];
-      a.lse2[i] = l == -INFINITY ? INFINITY : l * kLog2e;
-    }
   }
 }
 
@@ -465,10 +409,31 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) 
       dreg[ks] = V8{};
     }
   }
+  // delta = rowsum(dO o O) and the log2-domain LSE of this lane's query,
+  // computed here (each lane holds half of the row: d = 16 ks + 8 g + 0..7)
+  // and stored for the dK / dV kernel, which runs after this one
   float lse2 = INFINITY, del = 0.f;
-  if (my_q < a.Sq) {
-    lse2 = a.lse2[(b * a.Hq + hq) * a.Sq + my_q];
-    del = a.delta[(b * a.Hq + hq) * a.Sq + my_q];
+  {
+    const T* Op = static_cast<const T*>(a.o) + b * a.o_sb + hq * a.o_sh;
+    float part = 0.f;
+    if (my_q < a.Sq) {
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks) {
+        const V8 ov = *reinterpret_cast<const V8*>(Op + my_q * a.o_ss + 16 * ks + 8 * g);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) part = fmaf(to_f32(ov[e]), to_f32(dreg[ks][e]), part);
+      }
+    }
+    del = part + other_half(part);
+    if (my_q < a.Sq) {
+      const int64_t i = (b * a.Hq + hq) * a.Sq + my_q;
+      const float l = a.lse[i];
+      lse2 = l == -INFINITY ? INFINITY : l * kLog2e;
+      if (g == 0) {
+        a.delta[i] = del;
+        a.lse2[i] = lse2;
+      }
+    }
   }
 
   int64_t kv_lo = 0, kv_hi = a.Skv;
@@ -794,28 +759,17 @@ static int attn_bwd_impl(const char* who, const zk_attn_desc* desc, const void* 
   const bool k_full = desc->Skv % DqCfg<128>::BN == 0;
 #define ZK_BWD(T, D)                                                                        \
   do {                                                                                      \
-    if (rows > 0 && desc->Hq * (D / 8) >= 128 && desc->B <= 65535 &&                    \
-        desc->Sq < 0x7fffffff) {                                                            \
-      const dim3 pos_grid(static_cast<unsigned>(desc->Sq), static_cast<unsigned>(desc->B)); \
-      hipLaunchKernelGGL((attn_bwd_prep_pos<T, D>), pos_grid, dim3(256), 0, s, a);         \
-    } else if (rows > 0 && desc->B * desc->Hq <= 65535) {                                   \
-      const dim3 vgrid(static_cast<unsigned>((desc->Sq + 256 / (D / 8) - 1) / (256 / (D / 8))), \
-                       static_cast<unsigned>(desc->B * desc->Hq));                          \
-      hipLaunchKernelGGL((attn_bwd_prep_vec<T, D>), vgrid, dim3(256), 0, s, a);            \
-    } else if (rows > 0) {                                                                  \
-      hipLaunchKernelGGL(attn_bwd_prep<T>, pgrid, dim3(256), 0, s, a);                      \
+    if (n_qt > 0) {                                                                         \
+      if (k_full)                                                                           \
+        hipLaunchKernelGGL((attn_bwd_dq<T, D, true>), qgrid, dim3(256), 0, s, a, n_qt);     \
+      else                                                                                  \
+        hipLaunchKernelGGL((attn_bwd_dq<T, D, false>), qgrid, dim3(256), 0, s, a, n_qt);    \
     }                                                                                       \
     if (n_kt > 0) {                                                                         \
       if (q_full)                                                                           \
         hipLaunchKernelGGL((attn_bwd_dkdv<T, D, true>), kgrid, dim3(256), 0, s, a);         \
       else                                                                                  \
         hipLaunchKernelGGL((attn_bwd_dkdv<T, D, false>), kgrid, dim3(256), 0, s, a);        \
-    }                                                                                       \
-    if (n_qt > 0) {                                                                         \
-      if (k_full)                                                                           \
-        hipLaunchKernelGGL((attn_bwd_dq<T, D, true>), qgrid, dim3(256), 0, s, a, n_qt);     \
-      else                                                                                  \
-        hipLaunchKernelGGL((attn_bwd_dq<T, D, false>), qgrid, dim3(256), 0, s, a, n_qt);    \
     }                                                                                       \
   } while (0)
   if (desc->dtype == ZK_BF16) {
