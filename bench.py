@@ -579,9 +579,12 @@ def main():
     kern = measure_kernels(dev, spec, S)
     print("kernel timings done", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline(spec, S)
-    # the dominant hand-written kernel of the step (by time): the AdamW pass as
-    # the stage runs it (one flat launch per layer step over the layer's shard;
-    # the W^T copies are transposed out of its compute copy afterwards)
+    # the dominant hand-written kernel of the step (by time): the flat AdamW
+    # kernel alone, one launch over a layer's shard as the stage makes it.  The
+    # stage's optimizer step then also transposes the four projection matrices
+    # out of the kernel's compute copy (zk_transpose, ~0.8 GB more per layer
+    # step), which this figure leaves out (bench.py's adamw_t case measures
+    # the one-launch form that includes those copies).
     a = kern["adamw"]
     af, ab = kern["attn_fwd"], kern["attn_bwd"]
     line = {
@@ -613,7 +616,9 @@ def main():
                      "unit": a["unit"], "frac": a["frac"],
                      "traffic": a["traffic"],
                      "kernel": a["kernel"], "avg_ms": a["avg_ms"],
-                     "algorithmic_bytes": a["work_per_launch"]},
+                     "algorithmic_bytes": a["work_per_launch"],
+                     "scope": "the AdamW kernel alone; the stage's four W^T transposes per "
+                              "layer step are not included"},
         "attention_roofline": {
             "fwd": {"kernel": af["kernel"], "achieved": af["achieved"], "peak": af["peak"],
                     "unit": "TFLOP/s", "frac": af["frac"], "avg_ms": af["avg_ms"],
