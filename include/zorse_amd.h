@@ -226,6 +226,22 @@ int zk_attn_bwd_rope(const zk_attn_desc* desc, const void* q, const void* k,
                      const float* cos, const float* sin, int64_t n_pos,
                      const int64_t* positions, int pairing, zk_stream_t stream);
 
+/* zk_attn_bwd_rope (or, with cos == sin == NULL, zk_attn_bwd) that also
+ * stores dq, dk, dv transposed: dq_t [Hq d, B Sq], dk_t / dv_t [Hkv d, B Skv]
+ * (row = head * d + i, column = batch * S + position, rows ld_t elements
+ * apart) -- the dY^T operand of the q / k / v projections' weight gradients
+ * (the backward of the nn.Linear q_proj / k_proj / v_proj,
+ * models/llama_simple.py:206-221), written from the attention kernels'
+ * epilogues instead of by a separate transpose of their output.  bf16 / fp16
+ * only; Sq, Skv and ld_t multiples of 8, ld_t >= B * S, 16-byte aligned. */
+int zk_attn_bwd_rope_t(const zk_attn_desc* desc, const void* q, const void* k,
+                       const void* v, const void* o, const void* dout,
+                       const float* lse, void* dq, void* dk, void* dv,
+                       void* workspace, int64_t workspace_bytes,
+                       const float* cos, const float* sin, int64_t n_pos,
+                       const int64_t* positions, int pairing, void* dq_t, void* dk_t,
+                       void* dv_t, int64_t ld_t, zk_stream_t stream);
+
 /* ------------------------------------------------------------------ AdamW --
  * Replaces torch.optim.Adam(fused=True).step() on the layer's flat fp32
  * parameter shard as run in the reduce-grad callback

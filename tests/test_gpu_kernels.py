@@ -292,6 +292,46 @@ def test_flash_attention_autograd_with_rope(dev, dtype):
     assert_close(vd.grad, va.grad, dtype, "dv")
 
 
+TRANSPOSED_CASES = [
+    # B, S, Hq, Hkv, d, window, rope (None / "half" / "interleaved"), dtype
+    (1, 256, 4, 2, 128, 0, "half", torch.bfloat16),
+    (2, 200, 4, 1, 64, 0, "interleaved", torch.float16),
+    (1, 328, 2, 2, 128, 96, None, torch.bfloat16),
+    (2, 64, 8, 2, 64, 0, None, torch.float16),
+]
+
+
+@pytest.mark.parametrize("case", TRANSPOSED_CASES, ids=lambda c: "-".join(str(v) for v in c))
+def test_attention_bwd_transposed_outputs(dev, case):
+    """zk_attn_bwd_rope_t: the dq / dk / dv^T written from the kernels'
+    epilogues (into row slices of one [(Hq + 2 Hkv) d, B S] buffer, as the
+    layer passes them) are exactly the transposes of the row-major outputs,
+    which in turn equal those of the call without transposed outputs."""
+    from zorse_amd import kernels as K
+    from zorse_amd.functional import rope_tables
+    B, S, Hq, Hkv, d, window, rope, dtype = case
+    print(f"attention bwd transposed outputs {case}", flush=True)
+    q = _rand((B, S, Hq, d), dtype, 70).to(dev)
+    k = _rand((B, S, Hkv, d), dtype, 71).to(dev)
+    v = _rand((B, S, Hkv, d), dtype, 72).to(dev)
+    do = _rand((B, S, Hq, d), dtype, 73).to(dev)
+    r = None
+    if rope is not None:
+        cos, sin = rope_tables(S, d, 1e4, dtype, dev, rope == "interleaved")
+        r = (cos, sin, None, rope == "interleaved")
+        K.rope_(q, k, cos, sin, interleaved=rope == "interleaved")
+    o, lse = K.attn_fwd(q, k, v, causal=True, window=window)
+    T, qd, kd = B * S, Hq * d, Hkv * d
+    t = torch.full((qd + 2 * kd, T), float("nan"), device=dev, dtype=dtype)
+    dq, dk, dv = K.attn_bwd(q, k, v, o, do, lse, causal=True, window=window, rope=r,
+                            transposed=(t[:qd], t[qd:qd + kd], t[qd + kd:]))
+    assert torch.equal(t[:qd], dq.reshape(T, qd).t())
+    assert torch.equal(t[qd:qd + kd], dk.reshape(T, kd).t())
+    assert torch.equal(t[qd + kd:], dv.reshape(T, kd).t())
+    pq, pk, pv = K.attn_bwd(q, k, v, o, do, lse, causal=True, window=window, rope=r)
+    assert torch.equal(dq, pq) and torch.equal(dk, pk) and torch.equal(dv, pv)
+
+
 ROPE_BWD_CASES = [
     # B, S, Hq, Hkv, d, window, interleaved, explicit positions, dtype
     (1, 256, 4, 1, 128, 0, False, False, torch.bfloat16),

@@ -98,6 +98,9 @@ SIGNATURES = {
     "zk_attn_bwd_rope": (_int, [ctypes.POINTER(AttnDesc), _ptr, _ptr, _ptr, _ptr,
                                 _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _ptr, _i64,
                                 _ptr, _int, _ptr]),
+    "zk_attn_bwd_rope_t": (_int, [ctypes.POINTER(AttnDesc), _ptr, _ptr, _ptr, _ptr,
+                                  _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _ptr, _i64,
+                                  _ptr, _int, _ptr, _ptr, _ptr, _i64, _ptr]),
     "zk_adamw_step": (_int, [_ptr, _ptr, _int, _ptr, _ptr, _ptr, _int, _i64,
                              _f64, _f64, _f64, _f64, _f64, _i64, _ptr]),
     "zk_adamw_step_t": (_int, [_ptr, _ptr, _int, _ptr, _ptr, _ptr, _int, _ptr, _int, _i64,

@@ -345,6 +345,18 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv(AttnArgs a) {
         *reinterpret_cast<T4*>(dvp + d0) = wv;
       }
   }
+  if (a.dk_t != nullptr) {
+    // dK^T / dV^T rows hk D .. +D-1, token columns b Skv + k0 ..; the V rows'
+    // LDS (128 x D elements) holds the tile once every wave is past its last step
+    __syncthreads();
+    const int64_t left = a.Skv - k0;
+    const int nc = static_cast<int>(left < BK ? left : BK);
+    const int64_t off = hk * D * a.t_ld + b * a.Skv + k0;
+    T* tile = &Vw[0][0];  // all D rows in one array (the second pointer is unused)
+    store_rows_transposed<T, D, D>(dk, a.scale, tile, tile, static_cast<T*>(a.dk_t) + off, a.t_ld,
+                                   nc);
+    store_rows_transposed<T, D, D>(dv, 1.f, tile, tile, static_cast<T*>(a.dv_t) + off, a.t_ld, nc);
+  }
 }
 
 // ------------------------------------------------------------------ dQ -----
@@ -551,6 +563,15 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) 
         *reinterpret_cast<T4*>(dqp + d0) = w;
       }
   }
+  if (a.dq_t != nullptr) {
+    // dQ^T rows hq D .. +D-1, token columns b Sq + q0 ..; the K / V stages
+    // hold the tile once every wave is past its last step
+    __syncthreads();
+    const int64_t left = a.Sq - q0;
+    store_rows_transposed<T, D, BN * D / 128>(
+        dq, a.scale, K0, K1, static_cast<T*>(a.dq_t) + hq * D * a.t_ld + b * a.Sq + q0, a.t_ld,
+        static_cast<int>(left < BM ? left : BM));
+  }
 }
 
 // ------------------------------------------------------------- fp32 path ---
@@ -664,10 +685,18 @@ struct RopeInv {
   int pairing;
 };
 
+struct TransposedOut {
+  void* dq_t;
+  void* dk_t;
+  void* dv_t;
+  int64_t ld;
+};
+
 static int attn_bwd_impl(const char* who, const zk_attn_desc* desc, const void* q,
                          const void* k, const void* v, const void* o, const void* dout,
                          const float* lse, void* dq, void* dk, void* dv, void* workspace,
-                         int64_t workspace_bytes, const RopeInv* rope, zk_stream_t stream);
+                         int64_t workspace_bytes, const RopeInv* rope,
+                         const TransposedOut* tout, zk_stream_t stream);
 }  // namespace zk
 
 extern "C" int zk_attn_bwd(const zk_attn_desc* desc, const void* q,
@@ -676,16 +705,12 @@ extern "C" int zk_attn_bwd(const zk_attn_desc* desc, const void* q,
                            void* dk, void* dv, void* workspace,
                            int64_t workspace_bytes, zk_stream_t stream) {
   return attn_bwd_impl("zk_attn_bwd", desc, q, k, v, o, dout, lse, dq, dk, dv, workspace,
-                       workspace_bytes, nullptr, stream);
+                       workspace_bytes, nullptr, nullptr, stream);
 }
 
-extern "C" int zk_attn_bwd_rope(const zk_attn_desc* desc, const void* q, const void* k,
-                                const void* v, const void* o, const void* dout,
-                                const float* lse, void* dq, void* dk, void* dv,
-                                void* workspace, int64_t workspace_bytes, const float* cos,
-                                const float* sin, int64_t n_pos, const int64_t* positions,
-                                int pairing, zk_stream_t stream) {
-  const char* who = "zk_attn_bwd_rope";
+namespace zk {
+static int check_rope(const char* who, const zk_attn_desc* desc, const float* cos,
+                      const float* sin, int64_t n_pos, const int64_t* positions, int pairing) {
   ZK_REQUIRE(cos != nullptr && sin != nullptr, ZK_EINVAL, "%s: null RoPE table", who);
   ZK_REQUIRE(pairing == ZK_ROPE_HALF || pairing == ZK_ROPE_INTERLEAVED, ZK_EINVAL,
              "%s: bad pairing %d", who, pairing);
@@ -696,18 +721,62 @@ extern "C" int zk_attn_bwd_rope(const zk_attn_desc* desc, const void* q, const v
   ZK_REQUIRE(desc == nullptr || desc->d % 2 == 0, ZK_EINVAL, "%s: odd head_dim", who);
   ZK_REQUIRE(aligned(cos, 16) && aligned(sin, 16), ZK_EALIGN,
              "%s: RoPE tables must be 16-byte aligned", who);
+  return ZK_OK;
+}
+}  // namespace zk
+
+extern "C" int zk_attn_bwd_rope_t(const zk_attn_desc* desc, const void* q, const void* k,
+                                  const void* v, const void* o, const void* dout,
+                                  const float* lse, void* dq, void* dk, void* dv,
+                                  void* workspace, int64_t workspace_bytes, const float* cos,
+                                  const float* sin, int64_t n_pos, const int64_t* positions,
+                                  int pairing, void* dq_t, void* dk_t, void* dv_t, int64_t ld_t,
+                                  zk_stream_t stream) {
+  const char* who = "zk_attn_bwd_rope_t";
+  const RopeInv r = {cos, sin, n_pos, positions, pairing};
+  if (cos != nullptr || sin != nullptr) {
+    const int rc = check_rope(who, desc, cos, sin, n_pos, positions, pairing);
+    if (rc != ZK_OK) return rc;
+  }
+  const TransposedOut t = {dq_t, dk_t, dv_t, ld_t};
+  return attn_bwd_impl(who, desc, q, k, v, o, dout, lse, dq, dk, dv, workspace,
+                       workspace_bytes, cos != nullptr ? &r : nullptr, &t, stream);
+}
+
+extern "C" int zk_attn_bwd_rope(const zk_attn_desc* desc, const void* q, const void* k,
+                                const void* v, const void* o, const void* dout,
+                                const float* lse, void* dq, void* dk, void* dv,
+                                void* workspace, int64_t workspace_bytes, const float* cos,
+                                const float* sin, int64_t n_pos, const int64_t* positions,
+                                int pairing, zk_stream_t stream) {
+  const char* who = "zk_attn_bwd_rope";
+  const int rc = check_rope(who, desc, cos, sin, n_pos, positions, pairing);
+  if (rc != ZK_OK) return rc;
   const RopeInv r = {cos, sin, n_pos, positions, pairing};
   return attn_bwd_impl(who, desc, q, k, v, o, dout, lse, dq, dk, dv, workspace,
-                       workspace_bytes, &r, stream);
+                       workspace_bytes, &r, nullptr, stream);
 }
 
 namespace zk {
 static int attn_bwd_impl(const char* who, const zk_attn_desc* desc, const void* q,
                          const void* k, const void* v, const void* o, const void* dout,
                          const float* lse, void* dq, void* dk, void* dv, void* workspace,
-                         int64_t workspace_bytes, const RopeInv* rope, zk_stream_t stream) {
+                         int64_t workspace_bytes, const RopeInv* rope,
+                         const TransposedOut* tout, zk_stream_t stream) {
   int rc = check_attn_desc(desc, who, true);
   if (rc != ZK_OK) return rc;
+  if (tout != nullptr) {
+    ZK_REQUIRE(tout->dq_t && tout->dk_t && tout->dv_t, ZK_EINVAL,
+               "%s: null transposed output", who);
+    ZK_REQUIRE(desc->dtype != ZK_F32, ZK_EUNSUPPORTED,
+               "%s: transposed outputs need a 2-byte dtype", who);
+    ZK_REQUIRE(desc->Sq % 8 == 0 && desc->Skv % 8 == 0 && tout->ld % 8 == 0 &&
+                   tout->ld >= desc->B * desc->Sq && tout->ld >= desc->B * desc->Skv,
+               ZK_EINVAL, "%s: transposed outputs need Sq, Skv, ld multiples of 8 and "
+               "ld >= B S (ld %lld)", who, (long long)tout->ld);
+    ZK_REQUIRE(aligned(tout->dq_t, 16) && aligned(tout->dk_t, 16) && aligned(tout->dv_t, 16),
+               ZK_EALIGN, "%s: transposed outputs must be 16-byte aligned", who);
+  }
   ZK_REQUIRE(rope == nullptr || desc->Sq == desc->Skv, ZK_EUNSUPPORTED,
              "%s: fused RoPE needs Sq == Skv", who);
   const int64_t need = zk_attn_bwd_workspace(desc);
@@ -728,6 +797,12 @@ static int attn_bwd_impl(const char* who, const zk_attn_desc* desc, const void* 
   }
   a.q = q; a.k = k; a.v = v; a.o = o; a.dout = dout; a.lse = lse;
   a.dq = dq; a.dk = dk; a.dv = dv;
+  if (tout != nullptr) {
+    a.dq_t = tout->dq_t;
+    a.dk_t = tout->dk_t;
+    a.dv_t = tout->dv_t;
+    a.t_ld = tout->ld;
+  }
   const uintptr_t base = (reinterpret_cast<uintptr_t>(workspace) + 255) & ~uintptr_t(255);
   a.delta = reinterpret_cast<float*>(base);
   a.lse2 = a.delta + ((desc->B * desc->Hq * desc->Sq + 63) & ~int64_t(63));

@@ -42,7 +42,50 @@ struct AttnArgs {
   const int64_t* rope_pos;
   int64_t rope_npos;
   int rope_interleaved;
+  // backward only, optional: dQ / dK / dV also stored transposed, [H d, B S]
+  // (feature rows of t_ld elements, token b S + s along a row), the layout
+  // the projections' weight gradients read; null: not stored
+  void* dq_t;
+  void* dk_t;
+  void* dv_t;
+  int64_t t_ld;
 };
+
+// Transposed store of a workgroup's 128 rows of gradient: lane l of wave w
+// holds x[nt][j] = element 32 nt + 8 (j / 4) + 4 g + j % 4 (g = l / 32) of
+// row 32 w + l % 32, the MFMA accumulator layout; rows go out as the columns
+// 0 .. ncols - 1 (ncols a multiple of 8) of the D feature rows at dst (row
+// stride ld elements), scaled by `scale`.  The values pass through an LDS tile
+// [D][128] whose first RP feature rows are at `lo`, the rest at `hi` (two
+// arrays the caller no longer needs; every wave must be done with them on
+// entry).  16-byte stores, 16 lanes per 256-byte feature row.  Ends with a
+// barrier, so the tile may be reused at once.
+template <typename T, int D, int RP>
+__device__ __forceinline__ void store_rows_transposed(const f32x16 (&x)[D / 32], float scale,
+                                                      T* lo, T* hi, T* dst, int64_t ld,
+                                                      int ncols) {
+  const int tid = threadIdx.x, l32 = tid & 31, g = (tid >> 5) & 1, wave = tid >> 6;
+  const int c = 32 * wave + l32;
+#pragma unroll
+  for (int nt = 0; nt < D / 32; ++nt)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int r = 32 * nt + 8 * (j >> 2) + 4 * g + (j & 3);
+      T* t = 32 * nt < RP ? lo + r * 128 : hi + (r - RP) * 128;
+      t[c] = static_cast<T>(x[nt][j] * scale);
+    }
+  __syncthreads();
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int i = 0; i < D * 16 / 256; ++i) {
+    const int id = 256 * i + tid;
+    const int r = id >> 4, col = 8 * (id & 15);
+    const T* t = r < RP ? lo + r * 128 : hi + (r - RP) * 128;
+    if (col < ncols)
+      *reinterpret_cast<u32x4*>(dst + r * ld + col) = *reinterpret_cast<const u32x4*>(t + col);
+  }
+  __syncthreads();
+}
 
 // MFMA selection by storage type: 32x32x16 with fp32 accumulation.
 template <typename T>

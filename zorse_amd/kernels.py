@@ -364,16 +364,24 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool 
 
 
 def attn_bwd(q, k, v, o, do, lse, *, causal: bool = True, window: int = 0,
-             scale: float | None = None, dq=None, dk=None, dv=None, rope=None):
+             scale: float | None = None, dq=None, dk=None, dv=None, rope=None,
+             transposed=None):
     """Flash attention backward.  Returns (dq, dk, dv); outputs may be given
     as (strided) views, e.g. slices of one fused [T, (Hq+2Hkv) d] buffer.
 
     ``rope`` = (cos, sin, positions, interleaved): q and k were rotated by
     RoPE with these tables (as ``rope_``); dq and dk are then returned
     through the transpose rotation, i.e. with respect to the un-rotated
-    q / k -- the inverse rope_ pass fused into the kernels."""
+    q / k -- the inverse rope_ pass fused into the kernels.
+
+    ``transposed`` = (dq_t, dk_t, dv_t): 2-D [H d, B S] buffers (rows
+    contiguous, one common row stride, a multiple of 8; 2-byte dtypes, S a
+    multiple of 8) that also receive dq / dk / dv transposed -- the operand
+    layout of the projections' weight-gradient GEMMs -- from the kernels'
+    epilogues."""
     dev = _require_gpu(q, k, v, o, do, lse, dq, dk, dv,
-                       *(rope[:3] if rope is not None else ()))
+                       *(rope[:3] if rope is not None else ()),
+                       *(transposed if transposed is not None else ()))
     d = q.shape[3]
     if scale is None:
         scale = 1.0 / math.sqrt(d)
@@ -390,7 +398,17 @@ def attn_bwd(q, k, v, o, do, lse, *, causal: bool = True, window: int = 0,
     desc = _attn_desc(q, k, v, o, scale, causal, window, dq, dk, dv)
     nbytes = lib().zk_attn_bwd_workspace(desc)
     ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
+    if transposed is not None:
+        ld_t = _check_transposed(transposed, q, k)
     if rope is None:
+        if transposed is not None:
+            dq_t, dk_t, dv_t = transposed
+            check(lib().zk_attn_bwd_rope_t(desc, ptr(q), ptr(k), ptr(v), ptr(o), ptr(do),
+                                           ptr(lse), ptr(dq), ptr(dk), ptr(dv), ptr(ws), nbytes,
+                                           None, None, 0, None, 0, ptr(dq_t), ptr(dk_t),
+                                           ptr(dv_t), ld_t, stream_handle(dev)),
+                  "zk_attn_bwd_rope_t")
+            return dq, dk, dv
         check(lib().zk_attn_bwd(desc, ptr(q), ptr(k), ptr(v), ptr(o), ptr(do), ptr(lse),
                                 ptr(dq), ptr(dk), ptr(dv), ptr(ws), nbytes,
                                 stream_handle(dev)), "zk_attn_bwd")
@@ -409,12 +427,41 @@ def attn_bwd(q, k, v, o, do, lse, *, causal: bool = True, window: int = 0,
             raise ValueError("positions must be a contiguous int64 [S] tensor")
     elif cos.shape[0] < S:
         raise ValueError(f"table holds {cos.shape[0]} positions < S={S}")
+    pairing = _abi.ZK_ROPE_INTERLEAVED if interleaved else _abi.ZK_ROPE_HALF
+    if transposed is not None:
+        dq_t, dk_t, dv_t = transposed
+        check(lib().zk_attn_bwd_rope_t(desc, ptr(q), ptr(k), ptr(v), ptr(o), ptr(do), ptr(lse),
+                                       ptr(dq), ptr(dk), ptr(dv), ptr(ws), nbytes, ptr(cos),
+                                       ptr(sin), cos.shape[0], ptr(positions), pairing,
+                                       ptr(dq_t), ptr(dk_t), ptr(dv_t), ld_t,
+                                       stream_handle(dev)), "zk_attn_bwd_rope_t")
+        return dq, dk, dv
     check(lib().zk_attn_bwd_rope(desc, ptr(q), ptr(k), ptr(v), ptr(o), ptr(do), ptr(lse),
                                  ptr(dq), ptr(dk), ptr(dv), ptr(ws), nbytes, ptr(cos), ptr(sin),
-                                 cos.shape[0], ptr(positions),
-                                 _abi.ZK_ROPE_INTERLEAVED if interleaved else _abi.ZK_ROPE_HALF,
+                                 cos.shape[0], ptr(positions), pairing,
                                  stream_handle(dev)), "zk_attn_bwd_rope")
     return dq, dk, dv
+
+
+def _check_transposed(transposed, q, k):
+    """Validates attn_bwd's transposed outputs; returns their row stride."""
+    if len(transposed) != 3:
+        raise ValueError("transposed must be (dq_t, dk_t, dv_t)")
+    B, Sq, Hq, d = q.shape
+    Skv, Hkv = k.shape[1], k.shape[2]
+    want = ((Hq * d, B * Sq), (Hkv * d, B * Skv), (Hkv * d, B * Skv))
+    ld = transposed[0].stride(0) if transposed[0].dim() == 2 else -1
+    for name, t, shape in zip(("dq_t", "dk_t", "dv_t"), transposed, want):
+        if t.dim() != 2 or tuple(t.shape) != shape:
+            raise ValueError(f"{name} must be [{shape[0]}, {shape[1]}]")
+        if t.dtype != q.dtype or q.dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError(f"{name} must be bf16 / fp16 like q")
+        if t.stride(1) != 1 or t.stride(0) != ld or ld % 8 != 0 or t.data_ptr() % 16 != 0:
+            raise ValueError("transposed outputs need unit column stride, one common row "
+                             "stride that is a multiple of 8, and 16-byte alignment")
+    if Sq % 8 != 0 or Skv % 8 != 0:
+        raise ValueError("transposed outputs need sequence lengths that are multiples of 8")
+    return ld
 
 
 # ------------------------------------------------------------------ AdamW --

@@ -105,6 +105,11 @@ def _mm(a, b, out=None):
 _TRANSPOSE_MIN_TOKENS = 1024
 
 
+# The attention backward writes dqkv^T (the q|k|v weight gradient's operand)
+# from its epilogues instead of a separate transpose of dqkv.
+_ATTN_WRITES_DQKV_T = True
+
+
 def _transposing(t):
     return t.dtype in (torch.bfloat16, torch.float16) and t.shape[0] >= _TRANSPOSE_MIN_TOKENS
 
@@ -257,17 +262,24 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
     dq = dqkv[:, :spec.q_dim].view(B, S, Hq, d)
     dk = dqkv[:, spec.q_dim:spec.q_dim + spec.kv_dim].view(B, S, Hkv, d)
     dv = dqkv[:, spec.q_dim + spec.kv_dim:].view(B, S, Hkv, d)
+    # dqkv^T (the weight gradient's operand) comes from the attention
+    # kernels' epilogues when the GEMM takes the transposed form
+    dqkvt = None
+    if _ATTN_WRITES_DQKV_T and _transposing(qkv) and S % 8 == 0:
+        dqkvt = torch.empty(qkv.shape[1], T, device=qkv.device, dtype=qkv.dtype)
     for fn in list(BEFORE_ATTENTION_BACKWARD):
         fn()
     # the attention backward also takes dq / dk back through RoPE's rotation
     cos, sin = _rope_for(S, spec, dout.dtype, dout.device, positions)
+    kv0, kv1 = spec.q_dim, spec.q_dim + spec.kv_dim
     K.attn_bwd(q, k, v, o2.view(B, S, Hq, d), do2.view(B, S, Hq, d), lse,
                causal=spec.causal, window=spec.window, dq=dq, dk=dk, dv=dv,
-               rope=(cos, sin, positions, spec.interleaved_rope))
+               rope=(cos, sin, positions, spec.interleaved_rope),
+               transposed=None if dqkvt is None else (dqkvt[:kv0], dqkvt[kv0:kv1], dqkvt[kv1:]))
     del do2
     dn1 = _dgrad(dqkv, w.qkv, False, wt.get("qkv"))  # [T, h]
-    _wgrad(dqkv, n1, g.qkv)
-    del dqkv
+    _wgrad(dqkv, n1, g.qkv, dyt=dqkvt)
+    del dqkv, dqkvt
     dx, _ = K.rmsnorm_bwd(dn1, x2, w.ln1, rstd1, dres=dh, dw=g.ln1)
     return dx.view(B, S, h)
 
