@@ -1,10 +1,12 @@
 // Flash-attention forward for gfx950 (bf16 / fp16 storage, fp32 softmax).
 //
-// Workgroup = 4 waves = 128 queries of one (batch, q-head); each wave owns 32
-// queries whose Q rows stay in registers for the whole kernel.  The kernel
-// streams 64-key tiles of K and V through LDS (row-major, XOR-swizzled
-// 16-byte chunks, see tile_off) with the next tile's global loads in flight
-// during the current tile's math.
+// Workgroup = 8 waves = 256 queries of one (batch, q-head) for d = 128, one
+// workgroup per CU (two waves per SIMD; 4 waves / 128 queries for d = 64);
+// each wave owns 32 queries whose Q rows stay in registers for the whole
+// kernel.  The kernel streams 64-key tiles of K and V
+// through LDS (row-major, XOR-swizzled 16-byte chunks, see tile_off) with the
+// next tile's global loads in flight during the current tile's math; each
+// tile feeds all eight waves.
 //
 // Orientation: the score tile is computed transposed, S^T = K Q^T, with
 // v_mfma_f32_32x32x16 (A = K rows from LDS, B = Q from registers).  In the
@@ -32,12 +34,16 @@
 
 namespace zk {
 
+static constexpr int kFwdThreads = 512;            // the most threads per workgroup
+
 template <typename T, int D>
 struct FwdCfg {
-  static constexpr int BM = 128;                   // queries per workgroup
+  // d = 128: 8 waves (one workgroup per CU at ~220 registers); d = 64: 4
+  // waves, so that three workgroups of ~145 registers still share a CU
+  static constexpr int NW = D == 128 ? 8 : 4;      // waves per workgroup
+  static constexpr int NT = 64 * NW;
+  static constexpr int BM = 32 * NW;               // queries per workgroup
   static constexpr int BN = 64;                    // keys per tile
-  static constexpr int CPT = BN * D / 8 / 256;     // 16-byte chunks / thread / tile
-  static_assert(CPT >= 1, "tile too small for 256 threads");
 };
 
 __device__ __forceinline__ float fast_exp2(float x) {
@@ -49,12 +55,12 @@ static constexpr float kRescaleThreshold = 8.0f;
 
 // kFull: Skv is a multiple of the key tile, so no tile runs past the end.
 template <typename T, int D, bool kFull>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(kFwdThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
   typedef FwdCfg<T, D> C;
   typedef Mfma<T> M;
   typedef typename M::vec8 V8;
-  constexpr int BM = C::BM, BN = C::BN;
+  constexpr int BM = C::BM, BN = C::BN, NT = C::NT;
   // each stage its own array: the compiler then sees that the next tile's
   // asynchronous loads do not alias this tile's reads (and adds no wait)
   __shared__ __attribute__((aligned(16))) T K0[BN * D], K1[BN * D], V0[BN * D], V1[BN * D];
@@ -92,7 +98,7 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
   const int64_t t_hi = kv_hi > kv_lo ? (kv_hi + BN - 1) / BN : t_lo;
 
   // K / V tiles double-buffered in LDS, loaded asynchronously one tile ahead
-  TileLoader<T, D, BN> kload, vload;
+  TileLoader<T, D, BN, NT> kload, vload;
   kload.init(a.k_ss);
   vload.init(a.v_ss);
   auto issue = [&](int64_t k0, int st) {
@@ -394,14 +400,15 @@ extern "C" int zk_attn_fwd(const zk_attn_desc* desc, const void* q,
   }
   ZK_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(o, 16),
              ZK_EALIGN, "zk_attn_fwd: q/k/v/o must be 16-byte aligned");
-  const int64_t n_qt = (desc->Sq + 127) / 128;
-  const dim3 grid(static_cast<unsigned>(n_qt * desc->B * desc->Hq));
 #define ZK_FWD(T, D)                                                                    \
   do {                                                                                  \
+    constexpr int BM = FwdCfg<T, D>::BM, NT = FwdCfg<T, D>::NT;                         \
+    const int64_t n_qt = (desc->Sq + BM - 1) / BM;                                      \
+    const dim3 grid(static_cast<unsigned>(n_qt * desc->B * desc->Hq));                  \
     if (desc->Skv % FwdCfg<T, D>::BN == 0)                                              \
-      hipLaunchKernelGGL((attn_fwd_kernel<T, D, true>), grid, dim3(256), 0, s, a, n_qt);  \
+      hipLaunchKernelGGL((attn_fwd_kernel<T, D, true>), grid, dim3(NT), 0, s, a, n_qt);    \
     else                                                                                \
-      hipLaunchKernelGGL((attn_fwd_kernel<T, D, false>), grid, dim3(256), 0, s, a, n_qt); \
+      hipLaunchKernelGGL((attn_fwd_kernel<T, D, false>), grid, dim3(NT), 0, s, a, n_qt);  \
   } while (0)
   if (desc->dtype == ZK_BF16) {
     if (desc->d == 128) ZK_FWD(bf16, 128); else ZK_FWD(bf16, 64);
