@@ -73,6 +73,8 @@ __global__ __launch_bounds__(256) void attn_bwd_prep(AttnArgs a) {
 // ------------------------------------------------------------- dK / dV -----
 template <int D>
 struct DkdvCfg {
+  // 4 waves, two workgroups per CU (8 waves and 256 keys per workgroup, one
+  // workgroup per CU, measured 2-5 % slower)
   static constexpr int BK = 128;              // keys per workgroup (32 per wave)
   static constexpr int MQ = 32;               // queries per block
   static constexpr int MB = MQ / 32;          // 32-row MFMA blocks per query block
@@ -352,17 +354,22 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv(AttnArgs a) {
     const int64_t left = a.Skv - k0;
     const int nc = static_cast<int>(left < BK ? left : BK);
     const int64_t off = hk * D * a.t_ld + b * a.Skv + k0;
-    T* tile = &Vw[0][0];  // all D rows in one array (the second pointer is unused)
-    store_rows_transposed<T, D, D>(dk, a.scale, tile, tile, static_cast<T*>(a.dk_t) + off, a.t_ld,
-                                   nc);
-    store_rows_transposed<T, D, D>(dv, 1.f, tile, tile, static_cast<T*>(a.dv_t) + off, a.t_ld, nc);
+    T* tile = &Vw[0][0];  // all D rows in one array (the other pointers are unused)
+    store_rows_transposed<T, D, BK, D>(dk, a.scale, tile, tile, tile, tile,
+                                       static_cast<T*>(a.dk_t) + off, a.t_ld, nc);
+    store_rows_transposed<T, D, BK, D>(dv, 1.f, tile, tile, tile, tile,
+                                       static_cast<T*>(a.dv_t) + off, a.t_ld, nc);
   }
 }
 
 // ------------------------------------------------------------------ dQ -----
 template <int D>
 struct DqCfg {
-  static constexpr int BM = 128;              // queries per workgroup (32 per wave)
+  // 4 waves, two workgroups per CU (8 waves sharing each K / V tile, as the
+  // forward does, measured equal here: this kernel is not bound by its tile loads)
+  static constexpr int NW = 4;
+  static constexpr int NT = 64 * NW;
+  static constexpr int BM = 32 * NW;          // queries per workgroup (32 per wave)
   static constexpr int BN = 64;               // keys per tile
 };
 
@@ -372,7 +379,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) 
   typedef DqCfg<D> C;
   typedef Mfma<T> M;
   typedef typename M::vec8 V8;
-  constexpr int BM = C::BM, BN = C::BN;
+  constexpr int BM = C::BM, BN = C::BN, NT = C::NT;
   // swizzled rows; each stage its own array, so the compiler sees that the
   // next tile's asynchronous loads do not alias this tile's reads
   __shared__ __attribute__((aligned(16))) T K0[BN * D], K1[BN * D], V0[BN * D], V1[BN * D];
@@ -454,7 +461,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) 
   const int64_t t_lo = kv_lo / BN;
   const int64_t t_hi = kv_hi > kv_lo ? (kv_hi + BN - 1) / BN : t_lo;
 
-  TileLoader<T, D, BN> kload, vload;
+  TileLoader<T, D, BN, NT> kload, vload;
   kload.init(a.k_ss);
   vload.init(a.v_ss);
   auto issue = [&](int64_t kb0, int st) {
@@ -568,9 +575,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) 
     // hold the tile once every wave is past its last step
     __syncthreads();
     const int64_t left = a.Sq - q0;
-    store_rows_transposed<T, D, BN * D / 128>(
-        dq, a.scale, K0, K1, static_cast<T*>(a.dq_t) + hq * D * a.t_ld + b * a.Sq + q0, a.t_ld,
-        static_cast<int>(left < BM ? left : BM));
+    store_rows_transposed<T, D, BM, BN * D / BM>(
+        dq, a.scale, K0, K1, V0, V1, static_cast<T*>(a.dq_t) + hq * D * a.t_ld + b * a.Sq + q0,
+        a.t_ld, static_cast<int>(left < BM ? left : BM));
   }
 }
 
@@ -827,18 +834,19 @@ static int attn_bwd_impl(const char* who, const zk_attn_desc* desc, const void* 
                  aligned(dout, 16) && aligned(dq, 8) && aligned(dk, 8) && aligned(dv, 8),
              ZK_EALIGN, "%s: tensors must be 16-byte aligned", who);
   const int64_t n_kt = (desc->Skv + DkdvCfg<128>::BK - 1) / DkdvCfg<128>::BK;
-  const int64_t n_qt = (desc->Sq + DqCfg<128>::BM - 1) / DqCfg<128>::BM;
   const dim3 kgrid(static_cast<unsigned>(n_kt * desc->B * desc->Hkv));
-  const dim3 qgrid(static_cast<unsigned>(n_qt * desc->B * desc->Hq));
   const bool q_full = desc->Sq % DkdvCfg<128>::MQ == 0;
   const bool k_full = desc->Skv % DqCfg<128>::BN == 0;
 #define ZK_BWD(T, D)                                                                        \
   do {                                                                                      \
+    constexpr int BMq = DqCfg<D>::BM, NTq = DqCfg<D>::NT;                                   \
+    const int64_t n_qt = (desc->Sq + BMq - 1) / BMq;                                        \
+    const dim3 qgrid(static_cast<unsigned>(n_qt * desc->B * desc->Hq));                     \
     if (n_qt > 0) {                                                                         \
       if (k_full)                                                                           \
-        hipLaunchKernelGGL((attn_bwd_dq<T, D, true>), qgrid, dim3(256), 0, s, a, n_qt);     \
+        hipLaunchKernelGGL((attn_bwd_dq<T, D, true>), qgrid, dim3(NTq), 0, s, a, n_qt);     \
       else                                                                                  \
-        hipLaunchKernelGGL((attn_bwd_dq<T, D, false>), qgrid, dim3(256), 0, s, a, n_qt);    \
+        hipLaunchKernelGGL((attn_bwd_dq<T, D, false>), qgrid, dim3(NTq), 0, s, a, n_qt);    \
     }                                                                                       \
     if (n_kt > 0) {                                                                         \
       if (q_full)                                                                           \

@@ -51,38 +51,43 @@ struct AttnArgs {
   int64_t t_ld;
 };
 
-// Transposed store of a workgroup's 128 rows of gradient: lane l of wave w
-// holds x[nt][j] = element 32 nt + 8 (j / 4) + 4 g + j % 4 (g = l / 32) of
-// row 32 w + l % 32, the MFMA accumulator layout; rows go out as the columns
-// 0 .. ncols - 1 (ncols a multiple of 8) of the D feature rows at dst (row
-// stride ld elements), scaled by `scale`.  The values pass through an LDS tile
-// [D][128] whose first RP feature rows are at `lo`, the rest at `hi` (two
-// arrays the caller no longer needs; every wave must be done with them on
-// entry).  16-byte stores, 16 lanes per 256-byte feature row.  Ends with a
-// barrier, so the tile may be reused at once.
-template <typename T, int D, int RP>
+// Transposed store of a workgroup's rows of gradient: lane l of wave w holds
+// x[nt][j] = element 32 nt + 8 (j / 4) + 4 g + j % 4 (g = l / 32) of row
+// 32 w + l % 32 (the MFMA accumulator layout), NCOL = 32 x (waves) rows in
+// all; they go out as the columns 0 .. ncols - 1 (ncols a multiple of 8) of
+// the D feature rows at dst (row stride ld elements), scaled by `scale`.  The
+// values pass through an LDS tile [D][NCOL] held by up to four arrays the
+// caller no longer needs, RP feature rows each (p0 first); every wave must be
+// done with them on entry.  16-byte stores, NCOL / 8 lanes per feature row.
+// Ends with a barrier, so the arrays may be reused at once.
+template <typename T, int D, int NCOL, int RP>
 __device__ __forceinline__ void store_rows_transposed(const f32x16 (&x)[D / 32], float scale,
-                                                      T* lo, T* hi, T* dst, int64_t ld,
-                                                      int ncols) {
+                                                      T* p0, T* p1, T* p2, T* p3, T* dst,
+                                                      int64_t ld, int ncols) {
+  static_assert(RP % 32 == 0 && D <= 4 * RP, "feature rows per array");
+  constexpr int NT = 2 * NCOL;  // threads: 64 per 32 columns
   const int tid = threadIdx.x, l32 = tid & 31, g = (tid >> 5) & 1, wave = tid >> 6;
   const int c = 32 * wave + l32;
+  auto row_ptr = [&](int r) __attribute__((always_inline)) {
+    T* p = r < RP ? p0 : r < 2 * RP ? p1 : r < 3 * RP ? p2 : p3;
+    return p + (r % RP) * NCOL;
+  };
 #pragma unroll
   for (int nt = 0; nt < D / 32; ++nt)
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int r = 32 * nt + 8 * (j >> 2) + 4 * g + (j & 3);
-      T* t = 32 * nt < RP ? lo + r * 128 : hi + (r - RP) * 128;
-      t[c] = static_cast<T>(x[nt][j] * scale);
+      row_ptr(r)[c] = static_cast<T>(x[nt][j] * scale);
     }
   __syncthreads();
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  constexpr int CPR = NCOL / 8;  // 16-byte chunks per feature row
 #pragma unroll
-  for (int i = 0; i < D * 16 / 256; ++i) {
-    const int id = 256 * i + tid;
-    const int r = id >> 4, col = 8 * (id & 15);
-    const T* t = r < RP ? lo + r * 128 : hi + (r - RP) * 128;
+  for (int i = 0; i < D * CPR / NT; ++i) {
+    const int id = NT * i + tid;
+    const int r = id / CPR, col = 8 * (id % CPR);
     if (col < ncols)
-      *reinterpret_cast<u32x4*>(dst + r * ld + col) = *reinterpret_cast<const u32x4*>(t + col);
+      *reinterpret_cast<u32x4*>(dst + r * ld + col) = *reinterpret_cast<const u32x4*>(row_ptr(r) + col);
   }
   __syncthreads();
 }
