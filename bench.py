@@ -360,6 +360,33 @@ def summarize_stage(root: str, layers: int, steps: int, warmup: int) -> str:
         lines.append(f"| {name} | {tot[name] / steps:.2f} | {100 * tot[name] / allk:.1f} % |")
     if other > 0:
         lines.append(f"| other | {other / steps:.2f} | {100 * other / allk:.1f} % |")
+    # timeline shares: each instant of the window split evenly among the groups
+    # running then, and the time each group runs with nothing beside it
+    ev = []
+    for r in win:
+        g = next((name for name, pats in groups if any(p in r["Kernel_Name"] for p in pats)),
+                 "other")
+        ev += [(int(r["Start_Timestamp"]), 1, g), (int(r["End_Timestamp"]), -1, g)]
+    ev.sort()
+    active, share, alone, last = collections.Counter(), collections.Counter(), \
+        collections.Counter(), t0
+    for t, d, g in ev:
+        running = [k for k, c in active.items() if c]
+        n = sum(active.values())
+        for k in running:
+            share[k] += (t - last) * active[k] / n
+        if n == 1:
+            alone[running[0]] += t - last
+        active[g] += d
+        last = t
+    lines += ["", "The same window as a timeline: each instant split evenly among the kernel groups "
+                  "running then (the shares sum to the GPU's busy time), and the time each group "
+                  "runs with nothing beside it:", "",
+              "| kernel group | timeline share (ms per step) | running alone (ms per step) |",
+              "|---|---|---|"]
+    for name in [g for g, _ in groups] + (["other"] if other > 0 else []):
+        lines.append(f"| {name} | {share[name] / steps / 1e6:.2f} | "
+                     f"{alone[name] / steps / 1e6:.2f} |")
     iv = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in win)
     busy, (cs, ce) = 0, iv[0]
     for a, b in iv[1:]:
