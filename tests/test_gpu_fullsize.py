@@ -20,7 +20,8 @@ kernels' rounding points), plus the loss <out, G>.
     bf16; and the 7B stage path bench.py times, two layers over two steps
     (test_stage_full_size_7b);
   * cfg5: one Mistral-7B layer (GQA 32:8, FFN 14336, sliding window 4096),
-    seq 8192, bf16.
+    seq 8192, bf16;
+  * the stage path at cfg3 and cfg5 too (test_stage_full_size_gqa).
 """
 import pytest
 import torch
@@ -155,27 +156,39 @@ def test_stage_full_size_7b(dev):
     fp32 master equals the oracle's AdamW applied to the captured gradients
     (fp32 bar), the bf16 weights are the rounded master and the W^T copies
     are exact transposes."""
+    _stage_full_size(dev, "cfg4_7b_bf16", seed0=3000)
+
+
+@pytest.mark.parametrize("name", ["cfg3_1b_fp16", "cfg5_mistral7b_bf16"])
+def test_stage_full_size_gqa(dev, name):
+    """The stage path of test_stage_full_size_7b at the other layer
+    configurations: cfg3 (fp16, GQA 32:8, d 64, micro-batch 4 x seq 1024)
+    and cfg5 (Mistral-7B, GQA 32:8, sliding window 4096, seq 8192)."""
+    _stage_full_size(dev, name, seed0=4000 + 100 * list(FULL).index(name))
+
+
+def _stage_full_size(dev, name, seed0):
     from zorse_amd import llama_simple as L
     from zorse_amd.stage import StageRunner
-    dtype = torch.bfloat16
-    cfg = L.llama_config(hidden_size=4096, num_attention_heads=32, intermediate_size=11008,
-                         rope_theta=1e4)
-    print("stage 7b full size, 2 layers x 2 steps", flush=True)
+    kw, window, dtype, (B, S) = FULL[name]
+    h = kw["hidden_size"]
+    cfg = L.llama_config(**kw)
+    print(f"stage {name} full size, 2 layers x 2 steps", flush=True)
     layers = []
     for i in range(2):
         with torch.device("meta"):
-            layer = L.LlamaDecoderLayer(cfg, i, torch.bfloat16, param_dtype=dtype)
+            layer = L.LlamaDecoderLayer(cfg, i, dtype, sliding_window=window, param_dtype=dtype)
         layer.flat_param = torch.nn.Parameter(torch.empty(layer.spec.numel, dtype=dtype,
                                                           device=dev))
-        gd = torch.Generator(device=dev).manual_seed(3000 + i)
+        gd = torch.Generator(device=dev).manual_seed(seed0 + i)
         with torch.no_grad():
             layer.flat_param.normal_(0.0, 0.02, generator=gd)
             for ln in ("ln1", "ln2"):
-                layer.param_view(ln).copy_(1 + 0.1 * torch.randn(4096, generator=gd, device=dev))
+                layer.param_view(ln).copy_(1 + 0.1 * torch.randn(h, generator=gd, device=dev))
         layers.append(layer)
     s = layers[0].spec
     shape = O.LayerShape(hidden=s.hidden, heads=s.heads, kv_heads=s.kv_heads, head_dim=s.head_dim,
-                         ffn=s.ffn, eps=s.eps, theta=s.rope_theta)
+                         ffn=s.ffn, eps=s.eps, theta=s.rope_theta, window=s.window)
     captured = {}
     for i, l in enumerate(layers):   # registered before the runner's optimizer hooks
         l.flat_param.register_post_accumulate_grad_hook(
@@ -184,8 +197,8 @@ def test_stage_full_size_7b(dev):
     init = [l.flat_param.detach().float().clone() for l in layers]
     for step in range(2):
         print(f" step {step + 1}", flush=True)
-        x = _rand((1, 4096, 4096), dtype, 40 + step, dev)
-        dout = _rand((1, 4096, 4096), dtype, 50 + step, dev)
+        x = _rand((B, S, h), dtype, 40 + step, dev)
+        dout = _rand((B, S, h), dtype, 50 + step, dev)
         weights = [l.flat_param.detach().clone() for l in layers]
         runner.step(x, dout)
         runner.wait_optimizer()
@@ -193,21 +206,22 @@ def test_stage_full_size_7b(dev):
         if step == 1:
             for l in layers:
                 assert l._transposed_weights() is not None
-        # fp32 oracle and bf16 PyTorch of the two-layer stack at these weights
+        # fp32 oracle and plain PyTorch in the compute dtype of the two-layer
+        # stack at these weights
         refs = {}
-        for name, dt, attn in (("fp32", torch.float32, "eager"), ("bf16", dtype, "flash")):
+        for ref, dt, attn in (("fp32", torch.float32, "eager"), ("lowp", dtype, "flash")):
             xr = x.to(dt).requires_grad_(True)
             ps = [{k: v.to(dt).requires_grad_(True) for k, v in O.unflatten(w, shape).items()}
                   for w in weights]
             y = O.decoder_layer(O.decoder_layer(xr, ps[0], shape, attn=attn), ps[1], shape,
                                 attn=attn)
             y.backward(dout.to(dt))
-            refs[name] = [O.flatten({k: v.grad for k, v in p.items()}) for p in ps]
+            refs[ref] = [O.flatten({k: v.grad for k, v in p.items()}) for p in ps]
             del xr, ps, y
             torch.cuda.empty_cache()
         for i in range(2):
             _close(captured[i][step], refs["fp32"][i], dtype, f"step {step + 1} layer {i} grad",
-                   refs["bf16"][i])
+                   refs["lowp"][i])
         del refs
     for i, (l, opt) in enumerate(zip(layers, runner.optimizers)):
         p, m, v = init[i].clone(), torch.zeros_like(init[i]), torch.zeros_like(init[i])
@@ -218,7 +232,8 @@ def test_stage_full_size_7b(dev):
         assert torch.equal(l.flat_param.detach(), master.to(dtype))
         assert l.flat_param.grad is None
         o = s.offsets()
-        for name, (a, b), cols in (("qkv", (o["q"][0], o["v"][1]), 4096),
-                                   ("o", o["o"], 4096), ("gu", (o["gate"][0], o["up"][1]), 4096),
-                                   ("down", o["down"], 11008)):
-            assert torch.equal(l._wt[name], l.flat_param[a:b].view(-1, cols).t()), name
+        for wname, (a, b), cols in (("qkv", (o["q"][0], o["v"][1]), s.hidden),
+                                    ("o", o["o"], s.heads * s.head_dim),
+                                    ("gu", (o["gate"][0], o["up"][1]), s.hidden),
+                                    ("down", o["down"], s.ffn)):
+            assert torch.equal(l._wt[wname], l.flat_param[a:b].view(-1, cols).t()), wname
