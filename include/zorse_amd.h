@@ -321,8 +321,9 @@ int zk_transpose(const void* src, int64_t ld_src, void* dst, int64_t ld_dst,
                  int64_t rows, int64_t cols, int dtype, zk_stream_t stream);
 
 /* Device -> pinned-host copy of `bytes` bytes (host_dst from hipHostMalloc,
- * both pointers 16-byte aligned, both ranges inside their allocations;
- * ZK_EINVAL / ZK_EALIGN otherwise), issued from at most `blocks` workgroups
+ * both pointers 16-byte aligned, the host range inside its allocation, the
+ * device range the caller's to bound; ZK_EINVAL / ZK_EALIGN otherwise),
+ * issued from at most `blocks` workgroups
  * so that it leaves the CUs to the compute it overlaps.  Replaces the
  * activation store of the reference's pipeline schedule,
  * zorse_utils/pipeline_schedule_v2.py:127-136 (store_to_cpu_buffer: a
