@@ -188,9 +188,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv(AttnArgs a) {
     dload.issue(st ? dO1 : dO0, Dp, a.o_ss, qb0, a.Sq, kFull);
     int64_t qi = qb0 + lane;
     if (qi > a.Sq - 1) qi = a.Sq - 1;
-    const int64_t ri = (b * a.Hq + hq) * a.Sq + qi;
-    __builtin_amdgcn_global_load_lds((gmem_void*)(a.lse2 + ri), (lds_void*)&lse2s[st][wave][0], 4, 0, 0);
-    __builtin_amdgcn_global_load_lds((gmem_void*)(a.delta + ri), (lds_void*)&dels[st][wave][0], 4, 0, 0);
+    const int64_t r0 = (b * a.Hq + hq) * a.Sq + qb0;
+    const uint32_t off = static_cast<uint32_t>((qi - qb0) * 4);
+    dma_lds<4>(raw_rsrc(a.lse2 + r0), off, 0, &lse2s[st][wave][0]);
+    dma_lds<4>(raw_rsrc(a.delta + r0), off, 0, &dels[st][wave][0]);
   };
 
   // transposed MFMA operand of tile X for 16-query step kk (see lds_tr_operand)

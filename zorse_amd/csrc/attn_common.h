@@ -232,14 +232,37 @@ __device__ __forceinline__ typename Mfma<T>::vec8 lds_tr_operand(const T* tile, 
 
 // ---------------------------------------------------------------------------
 // Asynchronous tile loads: global memory -> LDS without staging registers
-// (gfx950 global_load_lds_dwordx4).  One wave instruction writes 64
+// (gfx950 buffer_load_dwordx4 ... lds).  One wave instruction writes 64
 // consecutive 16-byte LDS chunks (LDS address = wave-uniform base + 16 lane);
 // each lane picks the global chunk that belongs at its LDS position, which is
 // how the XOR swizzle of tile_off is applied.  Rows at or past `nrows` are
 // clamped to the last row so that every lane reads valid, finite data (the
 // kernels mask those rows).  Completion is tracked by the wave's vmcnt.
+//
+// The loads use the buffer form (a resource over a wave-uniform base plus a
+// 32-bit per-lane offset), not global_load_lds: the compiler's wait insertion
+// counts a pending global-form LDS load as a second kind of LDS-counter event
+// and then waits for every outstanding LDS read (lgkmcnt(0)) before the first
+// use of any of them; with the buffer form it waits only for the read needed.
 typedef __attribute__((address_space(1))) void gmem_void;
 typedef __attribute__((address_space(3))) void lds_void;
+
+// Raw (stride 0) buffer resource over [base, base + 2 GiB); offsets at or past
+// the end read zeros instead of faulting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+
+// N bytes (4 or 16) per lane from base + voff + soff into LDS at dst + N lane.
+template <int N>
+__device__ __forceinline__ void dma_lds(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                        const void* dst) {
+  static_assert(N == 4 || N == 16, "4 or 16 bytes per lane");
+  if constexpr (N == 4)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 4, voff, soff, 0, 0);
+  else
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 16, voff, soff, 0, 0);
+}
 
 template <typename T, int D, int ROWS, int NT = 256>
 __device__ __forceinline__ void tile_load_async(T* tile, const T* gbase, int64_t ld,
@@ -248,6 +271,8 @@ __device__ __forceinline__ void tile_load_async(T* tile, const T* gbase, int64_t
   static_assert(CH % NT == 0, "tile must be a multiple of NT chunks");
   const int tid = threadIdx.x;
   const int wave_chunk0 = tid & ~63;
+  // offsets from the tile's first row (< ROWS rows, so 32 bits suffice)
+  const __amdgpu_buffer_rsrc_t r = raw_rsrc(gbase + g0 * ld);
 #pragma unroll
   for (int i = 0; i < CH / NT; ++i) {
     const int p = i * NT + tid;
@@ -255,9 +280,8 @@ __device__ __forceinline__ void tile_load_async(T* tile, const T* gbase, int64_t
     const int c = (p % (D / 8)) ^ tile_sw<D>(row);
     int64_t gr = g0 + row;
     if (gr > nrows - 1) gr = nrows - 1;
-    const T* src = gbase + gr * ld + c * 8;
-    T* dst = tile + (i * NT + wave_chunk0) * 8;
-    __builtin_amdgcn_global_load_lds((gmem_void*)src, (lds_void*)dst, 16, 0, 0);
+    const uint32_t off = static_cast<uint32_t>(((gr - g0) * ld + c * 8) * static_cast<int64_t>(sizeof(T)));
+    dma_lds<16>(r, off, 0, tile + (i * NT + wave_chunk0) * 8);
   }
 }
 
@@ -267,8 +291,8 @@ __device__ __forceinline__ void tile_load_async(T* tile, const T* gbase, int64_t
 // position (t % (D / 8)) ^ sw(row), and since RSTEP is a multiple of 16 the
 // swizzle (a function of row % 16) is the same for every i.  The per-lane
 // byte offset inside the tile is therefore one 32-bit value, and each
-// instruction's global address is a wave-uniform base (scalar registers)
-// plus that offset.  Tiles that run past `nrows` take the clamped path.
+// instruction's address is a wave-uniform base and row offset (scalar
+// registers) plus that offset.  Tiles that run past `nrows` take the clamped path.
 template <typename T, int D, int ROWS, int NT = 256>
 struct TileLoader {
   static constexpr int NI = ROWS * D / 8 / NT;
@@ -287,13 +311,12 @@ struct TileLoader {
   __device__ __forceinline__ void issue_full(T* tile, const T* gbase, int64_t ld,
                                              int64_t g0) const {
     const int wave_chunk0 = static_cast<int>(threadIdx.x) & ~63;
-    const char* sb = reinterpret_cast<const char*>(gbase + g0 * ld);
+    const __amdgpu_buffer_rsrc_t r = raw_rsrc(gbase + g0 * ld);
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const char* src =
-          sb + static_cast<int64_t>(i) * RSTEP * ld * static_cast<int64_t>(sizeof(T)) + lane_off;
-      T* dst = tile + (i * NT + wave_chunk0) * 8;
-      __builtin_amdgcn_global_load_lds((gmem_void*)src, (lds_void*)dst, 16, 0, 0);
+      const uint32_t soff =
+          static_cast<uint32_t>(static_cast<int64_t>(i) * RSTEP * ld * static_cast<int64_t>(sizeof(T)));
+      dma_lds<16>(r, lane_off, soff, tile + (i * NT + wave_chunk0) * 8);
     }
   }
 
