@@ -372,6 +372,7 @@ struct DqCfg {
   static constexpr int NT = 64 * NW;
   static constexpr int BM = 32 * NW;          // queries per workgroup (32 per wave)
   static constexpr int BN = 64;               // keys per tile
+  static constexpr int PF = 2;                // LDS operand reads in flight
 };
 
 // kFull: Skv is a multiple of the key tile, so no tile runs past the end.
@@ -503,50 +504,75 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(AttnArgs a, int64_t n_qt) 
     int rb = rbase, tb = tbase;  // opaque per-step copies (addresses derived in the step)
     asm volatile("" : "+v"(rb), "+v"(tb));
 
-    // S^T and dP^T: block tt covers keys kb0 + 32 tt .. +31
-    f32x16 s[BN / 32], dp[BN / 32];
+    // one 32-key block at a time: S^T and dP^T of keys kb0 + 32 tt .. +31,
+    // its dS^T, then its two 16-key steps of dQ^T += K^T dS^T
 #pragma unroll
     for (int tt = 0; tt < BN / 32; ++tt) {
-      s[tt] = f32x16{};
-      dp[tt] = f32x16{};
+      f32x16 s = f32x16{}, dp = f32x16{};
+      // LDS operands are read PF MFMA steps ahead, each step fenced so that
+      // the reads stay where they are placed (left alone, the compiler reads
+      // each operand just before its MFMA and waits out the LDS latency)
+      constexpr int PF = C::PF;
+      auto rowread = [&](const T* X, int ks) __attribute__((always_inline)) {
+        const int ro = (rb ^ (ks << 5)) + tt * 32 * D * 2;
+        return *reinterpret_cast<const V8*>(reinterpret_cast<const char*>(X) + ro);
+      };
+      V8 kq[PF], vq[PF];
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        kq[i] = rowread(Kt, i);
+        vq[i] = rowread(Vt, i);
+      }
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
-        const int ro = (rb ^ (ks << 5)) + tt * 32 * D * 2;
-        const V8 kA = *reinterpret_cast<const V8*>(reinterpret_cast<const char*>(Kt) + ro);
-        s[tt] = M::mma(kA, qreg[ks], s[tt]);
-        const V8 vA = *reinterpret_cast<const V8*>(reinterpret_cast<const char*>(Vt) + ro);
-        dp[tt] = M::mma(vA, dreg[ks], dp[tt]);
+        __builtin_amdgcn_sched_barrier(0);
+        const V8 kA = kq[ks % PF], vA = vq[ks % PF];
+        if (ks + PF < D / 16) {
+          kq[ks % PF] = rowread(Kt, ks + PF);
+          vq[ks % PF] = rowread(Vt, ks + PF);
+        }
+        s = M::mma(kA, qreg[ks], s);
+        dp = M::mma(vA, dreg[ks], dp);
       }
-    }
-    // dS^T, packed per 16-key MFMA step (key = kb0 + 32 tt + 8 (j/4) + 4 g + j%4)
-    V8 sb[BN / 16];
-#pragma unroll
-    for (int tt = 0; tt < BN / 32; ++tt)
+      __builtin_amdgcn_sched_barrier(0);
+      // dS^T packed per 16-key MFMA step (key = kb0 + 32 tt + 8 (j/4) + 4 g + j%4)
+      V8 sb[2];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        float p = __builtin_amdgcn_exp2f(fmaf(s[tt][j], c2, -lse2));
+        float p = __builtin_amdgcn_exp2f(fmaf(s[j], c2, -lse2));
         if (need_mask) {
           const int rel = static_cast<int>(kb0) - vis_lo + 32 * tt + 8 * (j >> 2) + 4 * g + (j & 3);
           if (static_cast<unsigned>(rel) > static_cast<unsigned>(vis_span)) p = 0.f;
         }
-        sb[2 * tt + (j >> 3)][j & 7] = static_cast<T>(p * (dp[tt][j] - del));
+        sb[j >> 3][j & 7] = static_cast<T>(p * (dp[j] - del));
       }
-    // dQ^T += K^T dS^T  (K^T read transposed from the row-major K tile)
-#pragma unroll
-    for (int kk = 0; kk < BN / 16; ++kk) {
-#pragma unroll
-      for (int nt = 0; nt < D / 32; ++nt) {
+      // dQ^T += K^T dS^T  (K^T read transposed from the row-major K tile),
+      // operands read PF MFMAs ahead
+      auto trread = [&](int m) __attribute__((always_inline)) {
         typedef short s16x4 __attribute__((ext_vector_type(4)));
         typedef short s16x8 __attribute__((ext_vector_type(8)));
         typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+        const int kk = 2 * tt + m / (D / 32), nt = m % (D / 32);
         const char* kb = reinterpret_cast<const char*>(Kt) + kk * 16 * D * 2;
         const int off = tb ^ (nt << 6);
         const s16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(kb + off));
         const s16x4 x1 =
             __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(kb + 8 * D * 2 + (off ^ 32)));
         const s16x8 w = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-        dq[nt] = M::mma(__builtin_bit_cast(V8, w), sb[kk], dq[nt]);
+        return __builtin_bit_cast(V8, w);
+      };
+      constexpr int NM = 2 * (D / 32);
+      V8 tq[PF];
+#pragma unroll
+      for (int i = 0; i < PF; ++i) tq[i] = trread(i);
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        __builtin_amdgcn_sched_barrier(0);
+        const V8 w = tq[m % PF];
+        if (m + PF < NM) tq[m % PF] = trread(m + PF);
+        dq[m % (D / 32)] = M::mma(w, sb[m / (D / 32)], dq[m % (D / 32)]);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
