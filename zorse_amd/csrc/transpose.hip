@@ -6,9 +6,15 @@
 // layout whose operands stream along the reduction (the one the other
 // projection GEMMs use), which more than pays for this pass.
 //
-// A workgroup moves one 64 x 64 tile through LDS: 16-byte row loads, a
-// padded LDS tile (row pitch 66 elements, so the column reads of a wave
+// A workgroup moves one TR x TC tile through LDS: 16-byte row loads, a
+// padded LDS tile (row pitch TC + 2 elements, so the column reads of a wave
 // spread over the banks), and 16-byte stores of 8 consecutive source rows.
+// Two shapes: 128 x 128 tiles from 512 threads (256-byte row segments each
+// way and 32 KB in flight per workgroup) when the source has at least as many
+// rows as columns -- the activations' [T, h] and the taller weights -- and
+// 64 x 64 tiles from 256 threads otherwise, where the large tile measured
+// slower (4096 x 4096: 16.2 -> 13.8 us; 22016 x 4096: 75.8 -> 74.1 us;
+// 4096 x 11008: 37.4 -> 39.8 us).
 #include "zk_common.h"
 
 namespace zk {
@@ -20,24 +26,27 @@ struct Pack8<bf16> { typedef bf16x8 type; };
 template <>
 struct Pack8<f16> { typedef f16x8 type; };
 
-static constexpr int kTile = 64;
-static constexpr int kPitch = kTile + 2;
+static constexpr int kTile = 64;  // tile of the element-wise kernel
 
-template <typename T>
-__global__ __launch_bounds__(256) void transpose2_kernel(const T* __restrict__ src, int64_t ld_src,
-                                                         T* __restrict__ dst, int64_t ld_dst,
-                                                         int64_t rows, int64_t cols) {
+template <typename T, int TR, int TC, int NT>
+__global__ __launch_bounds__(NT) void transpose2_kernel(const T* __restrict__ src, int64_t ld_src,
+                                                        T* __restrict__ dst, int64_t ld_dst,
+                                                        int64_t rows, int64_t cols) {
   typedef typename Pack8<T>::type P8;
-  __shared__ T tile[kTile * kPitch];
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kTile;
-  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kTile;
+  constexpr int P = TC + 2;      // LDS row pitch
+  constexpr int CR = TC / 8;     // 16-byte chunks per source row of the tile
+  constexpr int CW = TR / 8;     // 16-byte chunks per destination row
+  static_assert((TR * CR) % NT == 0 && (TC * CW) % NT == 0, "tile / thread mismatch");
+  __shared__ T tile[TR * P];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * TR;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * TC;
   const int tid = threadIdx.x;
-  const bool full = r0 + kTile <= rows && c0 + kTile <= cols;
-  // load: 64 rows x 8 chunks of 8 elements, two chunks per thread
+  const bool full = r0 + TR <= rows && c0 + TC <= cols;
+  // load: TR rows x CR chunks of 8 elements
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int q = tid + 256 * i;
-    const int r = q >> 3, ch = q & 7;
+  for (int i = 0; i < TR * CR / NT; ++i) {
+    const int q = tid + NT * i;
+    const int r = q / CR, ch = q % CR;
     T v[8];
     if (full) {
       const P8 w = *reinterpret_cast<const P8*>(src + (r0 + r) * ld_src + c0 + 8 * ch);
@@ -51,17 +60,17 @@ __global__ __launch_bounds__(256) void transpose2_kernel(const T* __restrict__ s
       }
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) tile[r * kPitch + 8 * ch + e] = v[e];
+    for (int e = 0; e < 8; ++e) tile[r * P + 8 * ch + e] = v[e];
   }
   __syncthreads();
-  // store: 64 destination rows (source columns) x 8 chunks of 8 source rows
+  // store: TC destination rows (source columns) x CW chunks of 8 source rows
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int q = tid + 256 * i;
-    const int c = q >> 3, ch = q & 7;
+  for (int i = 0; i < TC * CW / NT; ++i) {
+    const int q = tid + NT * i;
+    const int c = q / CW, ch = q % CW;
     P8 w;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) w[e] = tile[(8 * ch + e) * kPitch + c];
+    for (int e = 0; e < 8; ++e) w[e] = tile[(8 * ch + e) * P + c];
     if (full) {
       *reinterpret_cast<P8*>(dst + (c0 + c) * ld_dst + r0 + 8 * ch) = w;
     } else {
@@ -72,6 +81,26 @@ __global__ __launch_bounds__(256) void transpose2_kernel(const T* __restrict__ s
       }
     }
   }
+}
+
+template <typename T, int TR, int TC, int NT>
+static void launch_transpose2(const T* src, int64_t ld_src, T* dst, int64_t ld_dst, int64_t rows,
+                              int64_t cols, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((cols + TC - 1) / TC),
+                  static_cast<unsigned>((rows + TR - 1) / TR));
+  hipLaunchKernelGGL((transpose2_kernel<T, TR, TC, NT>), grid, dim3(NT), 0, s, src, ld_src, dst,
+                     ld_dst, rows, cols);
+}
+
+template <typename T>
+static void transpose2(const void* src, int64_t ld_src, void* dst, int64_t ld_dst, int64_t rows,
+                       int64_t cols, hipStream_t s) {
+  if (rows >= cols)
+    launch_transpose2<T, 128, 128, 512>(static_cast<const T*>(src), ld_src, static_cast<T*>(dst),
+                                        ld_dst, rows, cols, s);
+  else
+    launch_transpose2<T, 64, 64, 256>(static_cast<const T*>(src), ld_src, static_cast<T*>(dst),
+                                      ld_dst, rows, cols, s);
 }
 
 // fp32 (and any unaligned case of the 2-byte types goes through here too):
@@ -117,11 +146,9 @@ extern "C" int zk_transpose(const void* src, int64_t ld_src, void* dst, int64_t 
   const bool vec = dtype != ZK_F32 && aligned(src, 16) && aligned(dst, 16) && ld_src % 8 == 0 &&
                    ld_dst % 8 == 0;
   if (vec && dtype == ZK_BF16)
-    hipLaunchKernelGGL(transpose2_kernel<bf16>, grid, dim3(256), 0, s, (const bf16*)src, ld_src,
-                       (bf16*)dst, ld_dst, rows, cols);
+    transpose2<bf16>(src, ld_src, dst, ld_dst, rows, cols, s);
   else if (vec)
-    hipLaunchKernelGGL(transpose2_kernel<f16>, grid, dim3(256), 0, s, (const f16*)src, ld_src,
-                       (f16*)dst, ld_dst, rows, cols);
+    transpose2<f16>(src, ld_src, dst, ld_dst, rows, cols, s);
   else if (dtype == ZK_BF16)
     hipLaunchKernelGGL(transpose_scalar_kernel<bf16>, grid, dim3(256), 0, s, (const bf16*)src,
                        ld_src, (bf16*)dst, ld_dst, rows, cols);
