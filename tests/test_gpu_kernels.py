@@ -505,10 +505,12 @@ def test_cast(dev):
 
 
 @pytest.mark.parametrize("dtype,rows,cols", [(torch.bfloat16, 4096, 12288), (torch.float16, 200, 72),
-                                             (torch.bfloat16, 65, 131), (torch.float32, 130, 67)])
+                                             (torch.bfloat16, 1032, 520), (torch.bfloat16, 65, 131),
+                                             (torch.float32, 130, 67)])
 def test_transpose(dev, dtype, rows, cols):
     """zk_transpose (the weight-gradient layout change) is an exact copy:
-    full tiles, ragged edges, the scalar path; also from a strided view."""
+    both tile shapes (64 x 64 when cols > rows, 128 x 128 otherwise) with full
+    tiles and ragged edges, the scalar path; also from a strided view."""
     from zorse_amd import kernels as K
     x = _rand((rows, cols), dtype, 61).to(dev)
     assert torch.equal(K.transpose(x), x.t())
