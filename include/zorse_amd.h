@@ -199,6 +199,17 @@ typedef struct zk_attn_desc {
 int zk_attn_fwd(const zk_attn_desc* desc, const void* q, const void* k,
                 const void* v, void* o, float* lse, zk_stream_t stream);
 
+/* zk_attn_fwd that also stores O transposed: o_t [Hq d, B Sq] (row = head * d
+ * + i, column = batch * Sq + position, rows ld_t elements apart), the same
+ * rounded values as o -- the X^T operand of the o_proj weight gradient (the
+ * backward of nn.Linear o_proj, models/llama_simple.py:221, 293-295), written
+ * from the attention kernel's epilogue instead of by a separate transpose of
+ * its output.  bf16 / fp16 only; Sq and ld_t multiples of 8, ld_t >= B * Sq,
+ * o_t 16-byte aligned. */
+int zk_attn_fwd_t(const zk_attn_desc* desc, const void* q, const void* k,
+                  const void* v, void* o, float* lse, void* o_t, int64_t ld_t,
+                  zk_stream_t stream);
+
 /* Bytes of workspace zk_attn_bwd needs: the fp32 row deltas rowsum(dO o O)
  * and the log2-domain LSE, [B, Hq, Sq] each. */
 int64_t zk_attn_bwd_workspace(const zk_attn_desc* desc);

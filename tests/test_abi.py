@@ -369,6 +369,32 @@ def test_fused_adamw_step_param_steps_one_parameter(monkeypatch):
         opt.step_param(torch.nn.Parameter(torch.zeros(8)))
 
 
+def test_attention_fwd_transposed_output_checks():
+    """zk_attn_fwd_t rejects a transposed output it cannot write (before
+    touching any pointer): a sequence length or row stride that is not a
+    multiple of 8, a row stride below B S, fp32, a missing buffer."""
+    from zorse_amd import _abi
+    lib = _abi.lib()
+    p = ctypes.c_void_p(256)
+
+    def desc(S, dtype=_abi.ZK_BF16):
+        d = _abi.AttnDesc(B=1, Sq=S, Skv=S, Hq=2, Hkv=2, d=64, scale=0.125, causal=1, window=0,
+                          dtype=dtype)
+        for f in ("q", "k", "v", "o"):
+            setattr(d, f + "_sb", S * 2 * 64); setattr(d, f + "_ss", 2 * 64)
+            setattr(d, f + "_sh", 64)
+        return d
+
+    def call(d, ld, o_t=p):
+        return lib.zk_attn_fwd_t(ctypes.byref(d), p, p, p, p, p, o_t, ld, None)
+    assert call(desc(12), 16) == -1            # S not a multiple of 8
+    assert call(desc(16), 12) == -1            # ld not a multiple of 8
+    assert call(desc(16), 8) == -1             # ld < B S
+    assert call(desc(16), 16, o_t=None) == -1
+    assert call(desc(16, _abi.ZK_F32), 16) == -4
+    assert "transposed" in lib.zk_last_error().decode()
+
+
 def test_attention_bwd_transposed_output_checks():
     """zk_attn_bwd_rope_t rejects transposed outputs it cannot write (before
     touching any pointer): a sequence length or row stride that is not a

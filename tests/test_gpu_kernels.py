@@ -332,6 +332,26 @@ def test_attention_bwd_transposed_outputs(dev, case):
     assert torch.equal(dq, pq) and torch.equal(dk, pk) and torch.equal(dv, pv)
 
 
+@pytest.mark.parametrize("case", TRANSPOSED_CASES, ids=lambda c: "-".join(str(v) for v in c))
+def test_attention_fwd_transposed_output(dev, case):
+    """zk_attn_fwd_t: the O^T written from the forward kernel's epilogue (into
+    a [Hq d, B S] buffer with a wider row stride) is exactly the transpose of
+    O, and O and the LSE equal those of the call without it."""
+    from zorse_amd import kernels as K
+    B, S, Hq, Hkv, d, window, _, dtype = case
+    print(f"attention fwd transposed output {case}", flush=True)
+    q = _rand((B, S, Hq, d), dtype, 74).to(dev)
+    k = _rand((B, S, Hkv, d), dtype, 75).to(dev)
+    v = _rand((B, S, Hkv, d), dtype, 76).to(dev)
+    T, qd = B * S, Hq * d
+    wide = torch.full((qd, T + 8), float("nan"), device=dev, dtype=dtype)
+    o, lse = K.attn_fwd(q, k, v, causal=True, window=window, out_t=wide[:, :T])
+    assert torch.equal(wide[:, :T], o.reshape(T, qd).t())
+    assert torch.isnan(wide[:, T:]).all()       # nothing past the token columns
+    po, plse = K.attn_fwd(q, k, v, causal=True, window=window)
+    assert torch.equal(o, po) and torch.equal(lse, plse)
+
+
 ROPE_BWD_CASES = [
     # B, S, Hq, Hkv, d, window, interleaved, explicit positions, dtype
     (1, 256, 4, 1, 128, 0, False, False, torch.bfloat16),

@@ -92,6 +92,8 @@ SIGNATURES = {
                        _int, _int, _ptr]),
     "zk_attn_fwd": (_int, [ctypes.POINTER(AttnDesc), _ptr, _ptr, _ptr, _ptr,
                            _ptr, _ptr]),
+    "zk_attn_fwd_t": (_int, [ctypes.POINTER(AttnDesc), _ptr, _ptr, _ptr, _ptr,
+                             _ptr, _ptr, _i64, _ptr]),
     "zk_attn_bwd_workspace": (_i64, [ctypes.POINTER(AttnDesc)]),
     "zk_attn_bwd": (_int, [ctypes.POINTER(AttnDesc), _ptr, _ptr, _ptr, _ptr,
                            _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr]),

@@ -42,16 +42,17 @@ struct AttnArgs {
   const int64_t* rope_pos;
   int64_t rope_npos;
   int rope_interleaved;
-  // backward only, optional: dQ / dK / dV also stored transposed, [H d, B S]
-  // (feature rows of t_ld elements, token b S + s along a row), the layout
-  // the projections' weight gradients read; null: not stored
+  // optional: the forward's O, the backward's dQ / dK / dV also stored
+  // transposed, [H d, B S] (feature rows of t_ld elements, token b S + s along
+  // a row), the layout the projections' weight gradients read; null: not stored
+  void* o_t;
   void* dq_t;
   void* dk_t;
   void* dv_t;
   int64_t t_ld;
 };
 
-// Transposed store of a workgroup's rows of gradient: lane l of wave w holds
+// Transposed store of a workgroup's rows (of O or a gradient): lane l of wave w holds
 // x[nt][j] = element 32 nt + 8 (j / 4) + 4 g + j % 4 (g = l / 32) of row
 // 32 w + l % 32 (the MFMA accumulator layout), NCOL = 32 x (waves) rows in
 // all; they go out as the columns 0 .. ncols - 1 (ncols a multiple of 8) of

@@ -253,6 +253,13 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
 
   const float l_tot = l_i + other_half(l_i);
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  // O rounded to the storage type once, so that the row store and the
+  // transposed store below write the same values (the compiler may round
+  // o * inv in one step, e.g. v_fma_mix for fp16, or in two)
+#pragma unroll
+  for (int nt = 0; nt < D / 32; ++nt)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) o[nt][j] = to_f32(static_cast<T>(o[nt][j] * inv));
   if (my_q < a.Sq) {
     T* Op = static_cast<T*>(a.out) + b * a.o_sb + hq * a.o_sh + my_q * a.o_ss;
 #pragma unroll
@@ -263,12 +270,22 @@ void attn_fwd_kernel(AttnArgs a, int64_t n_qt) {
         typedef T T4 __attribute__((ext_vector_type(4)));
         T4 w;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = static_cast<T>(o[nt][4 * a4 + e] * inv);
+        for (int e = 0; e < 4; ++e) w[e] = static_cast<T>(o[nt][4 * a4 + e]);
         *reinterpret_cast<T4*>(Op + d0) = w;
       }
     if (g == 0)
       a.lse_out[(b * a.Hq + hq) * a.Sq + my_q] =
           l_tot > 0.f ? m_ref * a.scale + logf(l_tot) : -INFINITY;
+  }
+  if (a.o_t != nullptr) {
+    // O^T rows hq D .. +D-1, token columns b Sq + q0 ..: the same rounded
+    // values as the row store, through an LDS tile in the K / V stages (free
+    // once every wave is past its last step)
+    __syncthreads();
+    const int64_t left = a.Sq - q0;
+    store_rows_transposed<T, D, BM, BN * D / BM>(
+        o, 1.f, K0, K1, V0, V1, static_cast<T*>(a.o_t) + hq * D * a.t_ld + b * a.Sq + q0, a.t_ld,
+        static_cast<int>(left < BM ? left : BM));
   }
 }
 
@@ -378,16 +395,27 @@ void fill_args(AttnArgs& a, const zk_attn_desc* d) {
 }
 }  // namespace zk
 
-extern "C" int zk_attn_fwd(const zk_attn_desc* desc, const void* q,
-                           const void* k, const void* v, void* o, float* lse,
-                           zk_stream_t stream) {
-  int rc = check_attn_desc(desc, "zk_attn_fwd", false);
+static int attn_fwd_impl(const char* who, const zk_attn_desc* desc, const void* q,
+                         const void* k, const void* v, void* o, float* lse, void* o_t,
+                         int64_t ld_t, zk_stream_t stream) {
+  int rc = check_attn_desc(desc, who, false);
   if (rc != ZK_OK) return rc;
+  if (o_t != nullptr) {
+    ZK_REQUIRE(desc->dtype != ZK_F32, ZK_EUNSUPPORTED,
+               "%s: the transposed output needs a 2-byte dtype", who);
+    ZK_REQUIRE(desc->Sq % 8 == 0 && ld_t % 8 == 0 && ld_t >= desc->B * desc->Sq, ZK_EINVAL,
+               "%s: the transposed output needs Sq, ld multiples of 8 and ld >= B Sq (ld %lld)",
+               who, (long long)ld_t);
+    ZK_REQUIRE(aligned(o_t, 16), ZK_EALIGN, "%s: the transposed output must be 16-byte aligned",
+               who);
+  }
   if (desc->B == 0 || desc->Sq == 0) return ZK_OK;
-  ZK_REQUIRE(q && k && v && o && lse, ZK_EINVAL, "zk_attn_fwd: null pointer");
+  ZK_REQUIRE(q && k && v && o && lse, ZK_EINVAL, "%s: null pointer", who);
   AttnArgs a = {};
   fill_args(a, desc);
   a.q = q; a.k = k; a.v = v; a.out = o; a.lse_out = lse;
+  a.o_t = o_t;
+  a.t_ld = ld_t;
   hipStream_t s = as_stream(stream);
   if (desc->dtype == ZK_F32) {
     const int64_t rows = desc->B * desc->Hq * desc->Sq;
@@ -396,10 +424,10 @@ extern "C" int zk_attn_fwd(const zk_attn_desc* desc, const void* q,
       hipLaunchKernelGGL(attn_fwd_f32_kernel<64>, grid, dim3(64), 0, s, a);
     else
       hipLaunchKernelGGL(attn_fwd_f32_kernel<128>, grid, dim3(64), 0, s, a);
-    return launch_status("zk_attn_fwd");
+    return launch_status(who);
   }
   ZK_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(o, 16),
-             ZK_EALIGN, "zk_attn_fwd: q/k/v/o must be 16-byte aligned");
+             ZK_EALIGN, "%s: q/k/v/o must be 16-byte aligned", who);
 #define ZK_FWD(T, D)                                                                    \
   do {                                                                                  \
     constexpr int BM = FwdCfg<T, D>::BM, NT = FwdCfg<T, D>::NT;                         \
@@ -416,5 +444,17 @@ extern "C" int zk_attn_fwd(const zk_attn_desc* desc, const void* q,
     if (desc->d == 128) ZK_FWD(f16, 128); else ZK_FWD(f16, 64);
   }
 #undef ZK_FWD
-  return launch_status("zk_attn_fwd");
+  return launch_status(who);
+}
+
+extern "C" int zk_attn_fwd(const zk_attn_desc* desc, const void* q, const void* k, const void* v,
+                           void* o, float* lse, zk_stream_t stream) {
+  return attn_fwd_impl("zk_attn_fwd", desc, q, k, v, o, lse, nullptr, 0, stream);
+}
+
+extern "C" int zk_attn_fwd_t(const zk_attn_desc* desc, const void* q, const void* k,
+                             const void* v, void* o, float* lse, void* o_t, int64_t ld_t,
+                             zk_stream_t stream) {
+  ZK_REQUIRE(o_t != nullptr, ZK_EINVAL, "zk_attn_fwd_t: null transposed output");
+  return attn_fwd_impl("zk_attn_fwd_t", desc, q, k, v, o, lse, o_t, ld_t, stream);
 }

@@ -345,10 +345,16 @@ def _attn_desc(q, k, v, o, scale, causal, window, dq=None, dk=None, dv=None):
 
 
 def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool = True,
-             window: int = 0, scale: float | None = None, out: torch.Tensor | None = None):
+             window: int = 0, scale: float | None = None, out: torch.Tensor | None = None,
+             out_t: torch.Tensor | None = None):
     """Flash attention forward on [B,S,H,d] views.  Returns (o, lse) with o
-    [B,Sq,Hq,d] (contiguous unless ``out`` is given) and lse fp32 [B,Hq,Sq]."""
-    dev = _require_gpu(q, k, v, out)
+    [B,Sq,Hq,d] (contiguous unless ``out`` is given) and lse fp32 [B,Hq,Sq].
+
+    ``out_t`` (2-byte types, Sq % 8 == 0): a [Hq d, >= B Sq] buffer with unit
+    column stride that also receives O transposed (row head * d + i, column
+    batch * Sq + position), from the kernel's epilogue -- the operand of the
+    o_proj weight gradient."""
+    dev = _require_gpu(q, k, v, out, out_t)
     B, Sq, Hq, d = q.shape
     if scale is None:
         scale = 1.0 / math.sqrt(d)
@@ -358,8 +364,16 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool 
         raise ValueError("out has the wrong shape")
     desc = _attn_desc(q, k, v, out, scale, causal, window)
     lse = torch.empty(B, Hq, Sq, device=dev, dtype=torch.float32)
-    check(lib().zk_attn_fwd(desc, ptr(q), ptr(k), ptr(v), ptr(out), ptr(lse),
-                            stream_handle(dev)), "zk_attn_fwd")
+    if out_t is None:
+        check(lib().zk_attn_fwd(desc, ptr(q), ptr(k), ptr(v), ptr(out), ptr(lse),
+                                stream_handle(dev)), "zk_attn_fwd")
+        return out, lse
+    if out_t.dtype != q.dtype or out_t.dim() != 2 or out_t.stride(1) != 1:
+        raise ValueError("out_t must be a 2-D q-dtype buffer with unit column stride")
+    if out_t.shape[0] != Hq * d or out_t.shape[1] < B * Sq:
+        raise ValueError(f"out_t must be [{Hq * d}, >= {B * Sq}], got {tuple(out_t.shape)}")
+    check(lib().zk_attn_fwd_t(desc, ptr(q), ptr(k), ptr(v), ptr(out), ptr(lse), ptr(out_t),
+                              out_t.stride(0), stream_handle(dev)), "zk_attn_fwd_t")
     return out, lse
 
 

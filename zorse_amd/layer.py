@@ -106,8 +106,10 @@ _TRANSPOSE_MIN_TOKENS = 1024
 
 
 # The attention backward writes dqkv^T (the q|k|v weight gradient's operand)
-# from its epilogues instead of a separate transpose of dqkv.
+# from its epilogues instead of a separate transpose of dqkv, and the forward
+# writes O^T (the o_proj weight gradient's) next to O.
 _ATTN_WRITES_DQKV_T = True
+_ATTN_WRITES_O_T = True
 
 
 def _transposing(t):
@@ -186,11 +188,16 @@ def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=Non
     K.rope_(q, k, cos, sin, positions=positions, interleaved=spec.interleaved_rope)
     hit = attn_cache.take() if attn_cache is not None else None
     if hit is not None:
-        o, lse = hit
+        o, lse, o2t = hit
     else:
-        o, lse = K.attn_fwd(q, k, v, causal=spec.causal, window=spec.window)
+        # O^T [Hq d, T] for the o_proj weight gradient when it takes the
+        # transposed form (see _wgrad)
+        o2t = None
+        if _ATTN_WRITES_O_T and _transposing(x2) and S % 8 == 0:
+            o2t = torch.empty(spec.q_dim, T, device=x.device, dtype=x.dtype)
+        o, lse = K.attn_fwd(q, k, v, causal=spec.causal, window=spec.window, out_t=o2t)
         if attn_cache is not None:
-            attn_cache.put(o, lse)
+            attn_cache.put(o, lse, o2t)
     o2 = o.view(T, spec.q_dim)
     # o_proj, then residual add fused into the second RMSNorm (one pass writes
     # hdn = x + round(o_proj) and its normalisation, the reference's order)
@@ -206,7 +213,7 @@ def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=Non
         z = zs = K.swiglu_fwd(gu[:, :F], gu[:, F:])
     out = torch.addmm(hdn, z, w.down.t())            # residual + down(z)
     del z
-    saved = (x2, n1, rstd1, qkv, o2, lse, hdn, n2, rstd2, gu, zs, positions)
+    saved = (x2, n1, rstd1, qkv, o2, o2t, lse, hdn, n2, rstd2, gu, zs, positions)
     return out.view(B, S, h), saved
 
 
@@ -223,7 +230,7 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
     (compute dtype, flat layout) and returns dx.  ``wt`` (optional): W^T of
     the qkv, o, gu and down weights, current with ``w``."""
     wt = wt or {}
-    x2, n1, rstd1, qkv, o2, lse, hdn, n2, rstd2, gu, zs, positions = saved
+    x2, n1, rstd1, qkv, o2, o2t, lse, hdn, n2, rstd2, gu, zs, positions = saved
     T, h = x2.shape
     B = dout.shape[0]
     S = T // B
@@ -254,7 +261,7 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
 
     # attention: hdn = x + o W_o^T
     do2 = _dgrad(dh, w.o, True, wt.get("o"))         # [T, Hq d]
-    _wgrad(dh, o2, g.o)
+    _wgrad(dh, o2, g.o, xt=o2t)
     q = qkv[:, :spec.q_dim].view(B, S, Hq, d)
     k = qkv[:, spec.q_dim:spec.q_dim + spec.kv_dim].view(B, S, Hkv, d)
     v = qkv[:, spec.q_dim + spec.kv_dim:].view(B, S, Hkv, d)
@@ -329,14 +336,16 @@ class AttentionCache:
                      x._version) + wkey
 
     def take(self):
+        """(o, lse, o_t) of the bound key's entry, removed, or None."""
         hit = self._entries.pop(self._key, None)
         if hit is None:
             return None
         self._storage = None  # the input's storage is no longer needed here
         return hit[1:]
 
-    def put(self, o, lse):
-        self._entries[self._key] = (self._storage, o, lse)
+    def put(self, o, lse, o_t=None):
+        """Records O, its LSE and (when the forward wrote it) O^T."""
+        self._entries[self._key] = (self._storage, o, lse, o_t)
 
 
 class DecoderLayerFunction(torch.autograd.Function):
