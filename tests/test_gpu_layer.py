@@ -464,19 +464,22 @@ def test_stage_transposed_weights(dev):
         assert_close(out[True][1][i], out[False][1][i].double(), dtype, f"layer {i} weights")
 
 
-def test_stage_recompute_attention_cache(dev):
+@pytest.mark.parametrize("S", [256, 1024])
+def test_stage_recompute_attention_cache(dev, S):
     """Recompute mode (the reference pipeline's second forward inside the
     backward, zorse_utils/pipeline_schedule_v2.py:157-200): with the attention
     cache the re-forward launches no attention kernel, and every layer
     gradient is bit-identical to recompute without the cache and to the
-    single-forward path (the kernels are deterministic)."""
+    single-forward path (the kernels are deterministic).  At 1024 tokens the
+    backward takes its transposed-operand form, so the cache also carries the
+    O^T the forward wrote."""
     from zorse_amd import layer as L
     from zorse_amd.stage import StageRunner
     kw = dict(hidden_size=256, num_attention_heads=2, intermediate_size=512, rope_theta=1e4)
     dtype = torch.bfloat16
     g = torch.Generator().manual_seed(5)
-    x = torch.randn(1, 256, 256, generator=g).to(dtype).to(dev)
-    dout = torch.randn(1, 256, 256, generator=g).to(dtype).to(dev)
+    x = torch.randn(1, S, 256, generator=g).to(dtype).to(dev)
+    dout = torch.randn(1, S, 256, generator=g).to(dtype).to(dev)
     calls = {"n": 0}
     real = L.K.attn_fwd
 
