@@ -155,6 +155,32 @@ def test_layer_fwd_bwd_vs_oracle(dev, name):
     _check_layer(layer, x, dout, dtype, name)
 
 
+# Token counts at or above the layer's threshold for transposed backward
+# operands, with sequence lengths that are not multiples of 8: the attention
+# kernels then write no transposed copies, so the backward takes the explicit
+# transposes of ragged shapes instead (and, with an odd token count, of the
+# SwiGLU output and gradients as well).
+RAGGED_LONG = {
+    "cfg4_bf16_S1100": ("cfg4_bf16", None, (1, 1100)),  # T % 8 = 4: no transposed SwiGLU outputs
+    "cfg3_fp16_S516x2": ("cfg3_fp16_gqa", None, (2, 516)),  # T = 1032: SwiGLU _t kernels on
+    "cfg5_bf16_swa_S1027": ("cfg5_bf16_swa", 160, (1, 1027)),
+}
+
+
+@pytest.mark.parametrize("name", list(RAGGED_LONG))
+def test_layer_ragged_long_sequence(dev, name):
+    from zorse_amd import layer as LY
+    base, window, (B, S) = RAGGED_LONG[name]
+    kw, _, dtype, _ = CONFIGS[base]
+    assert B * S >= LY._TRANSPOSE_MIN_TOKENS and S % 8 != 0
+    print(f"layer {name}", flush=True)
+    layer = _layer(kw, dev, param_dtype=dtype, window=window, seed=211)
+    g = torch.Generator().manual_seed(17)
+    x = torch.randn(B, S, kw["hidden_size"], generator=g).to(dtype)
+    dout = torch.randn(B, S, kw["hidden_size"], generator=g).to(dtype)
+    _check_layer(layer, x, dout, dtype, name)
+
+
 def test_cfg1_head_and_cross_entropy_loss(dev):
     """BASELINE cfg1 end to end: layer + final RMSNorm + linear head + CE over
     integer labels (vocab 1000), fp32, all on this build's kernels (chunked
