@@ -97,7 +97,7 @@ class KernelCases:
     1 GiB), the calibration for the FETCH_SIZE / WRITE_SIZE counters."""
 
     NAMES = ("attn_fwd", "attn_bwd", "rmsnorm_fwd", "rmsnorm_bwd", "adamw", "adamw_t", "copy",
-             "gemm_gu", "gemm_wgrad_gu", "rope")
+             "gemm_gu", "gemm_wgrad_gu", "gemm_nt_gu", "gemm_nt_wgrad_gu", "rope")
 
     def __init__(self, dev, spec, S):
         self.dev, self.spec, self.S = dev, spec, S
@@ -199,19 +199,25 @@ class KernelCases:
                 K.rope_(qkv[:, :H * d].view(B, S, H, d), qkv[:, H * d:2 * H * d].view(B, S, H, d),
                         cos, sin)
             return run, 2 * 2 * T * H * d * 2
-        if name in ("gemm_gu", "gemm_wgrad_gu"):
+        if name in ("gemm_gu", "gemm_wgrad_gu", "gemm_nt_gu", "gemm_nt_wgrad_gu"):
             # the layer's largest projection GEMM as the stage runs it (hipBLASLt
-            # through torch.mm with the recorded solutions): forward gate|up =
+            # through torch.mm with the recorded solutions; gemm_nt_*: the
+            # hand-written zk_gemm_nt on the same operands): forward gate|up =
             # n2 [T, h] x W_gu^T, and its weight gradient dgu^T [2F, T] x n2^T^T
             F2 = 2 * spec.ffn
+            hand = name.startswith("gemm_nt")
             a = torch.randn(T, h, device=dev, dtype=torch.bfloat16)
-            if name == "gemm_gu":
+            if name in ("gemm_gu", "gemm_nt_gu"):
                 w = 0.02 * torch.randn(F2, h, device=dev, dtype=torch.bfloat16)
                 y = torch.empty(T, F2, device=dev, dtype=torch.bfloat16)
+                if hand:
+                    return (lambda: K.gemm_nt(a, w, out=y)), 2 * T * h * F2
                 return (lambda: torch.mm(a, w.t(), out=y)), 2 * T * h * F2
             dyt = torch.randn(F2, T, device=dev, dtype=torch.bfloat16)
             at = a.t().contiguous()
             dw = torch.empty(F2, h, device=dev, dtype=torch.bfloat16)
+            if hand:
+                return (lambda: K.gemm_nt(dyt, at, out=dw)), 2 * T * h * F2
             return (lambda: torch.mm(dyt, at.t(), out=dw)), 2 * T * h * F2
         if name == "copy":
             src = torch.empty(1 << 28, device=dev, dtype=torch.float32).normal_()
@@ -237,6 +243,8 @@ def measure_kernels(dev, spec, S):
         "copy": ("device copy 1 GiB (HBM reference)", "hbm", 5),
         "gemm_gu": ("hipBLASLt gate|up GEMM 4096 x 22016 x 4096 (reference point)", "mfma", 10),
         "gemm_wgrad_gu": ("hipBLASLt gate|up weight-gradient GEMM (reference point)", "mfma", 10),
+        "gemm_nt_gu": ("zk_gemm_nt gate|up GEMM 4096 x 22016 x 4096 (hand-written)", "mfma", 10),
+        "gemm_nt_wgrad_gu": ("zk_gemm_nt gate|up weight-gradient GEMM (hand-written)", "mfma", 10),
     }
     for name, (kname, bound, iters) in spec_of.items():
         run, work = cases.make(name)
@@ -443,7 +451,8 @@ def summarize_mfma(root: str) -> str:
     lines = ["| kernel | dispatches | avg duration (us) | clock (GHz) | MFMA FLOPs executed (GF) "
              "| MFMA busy / active cycles | LDS conflict cycles / access cycles |",
              "|---|---|---|---|---|---|---|"]
-    for case in ("attn_fwd", "attn_bwd", "gemm_gu", "gemm_wgrad_gu"):
+    for case in ("attn_fwd", "attn_bwd", "gemm_gu", "gemm_wgrad_gu", "gemm_nt_gu",
+                 "gemm_nt_wgrad_gu"):
         path = os.path.join(root, case, "r_counter_collection.csv")
         if not os.path.exists(path):
             continue
@@ -535,6 +544,9 @@ def main():
                     help="launch only this kernel case --steps times (for rocprofv3 --pmc)")
     ap.add_argument("--default-gemm", action="store_true",
                     help="use hipBLASLt's default solution heuristic instead of the recorded table")
+    ap.add_argument("--gemm", choices=("hipblaslt", "hip"), default="hipblaslt",
+                    help="projection GEMMs of the stage: hipBLASLt (torch.mm / addmm) or the "
+                         "hand-written zk_gemm_nt")
     ap.add_argument("--summarize-mfma", metavar="DIR",
                     help="print the MFMA-counter summary of rocprofv3 runs under DIR and exit")
     ap.add_argument("--summarize-traffic", metavar="DIR",
@@ -568,6 +580,8 @@ def main():
     from zorse_amd.stage import StageRunner
 
     tuned = use_tuned_gemms(not args.default_gemm)
+    from zorse_amd import layer as _layer_mod
+    _layer_mod.set_gemm_backend(args.gemm)
 
     S, B = args.seq, 1
     if args.kernel:
@@ -634,9 +648,11 @@ def main():
                    "layers": args.layers, "hidden": spec.hidden, "heads": spec.heads,
                    "head_dim": spec.head_dim, "ffn": spec.ffn, "micro_batch": B, "seq_len": S,
                    "global_batch": B, "parallelism": "none (1 GPU)",
-                   "projection_gemms": "hipBLASLt via torch.mm/addmm" + (
+                   "projection_gemms": ("hand-written zk_gemm_nt (zorse_amd/csrc/gemm.hip)"
+                                        if args.gemm == "hip" else
+                                        "hipBLASLt via torch.mm/addmm" + (
                        " (recorded TunableOp solutions, zorse_amd/tunableop_gfx950.csv)"
-                       if tuned else " (default heuristic)"),
+                       if tuned else " (default heuristic)")),
                    "stage_tokens_per_s": round(B * S / (ms_step / 1e3), 1),
                    "layer_fwd_bwd_tflops": round(layer_tflops, 1)},
         "roofline": {"bound": a["bound"], "achieved": a["achieved"], "peak": a["peak"],

@@ -153,6 +153,23 @@ int zk_gemm_swiglu(const void* x, int64_t ld_x, const void* w_gate,
                    int64_t ld_gu, void* z, int64_t ld_z, void* zt, int64_t ld_zt,
                    int64_t M, int64_t F, int64_t K, int dtype, zk_stream_t stream);
 
+/* Projection GEMM: replaces the nn.Linear products of the decoder layer's
+ * q/k/v/o projections (models/llama_simple.py:206-221, 346, 375) and of the
+ * LlamaMLP built at models/llama_simple.py:418, forward and backward, when
+ * both operands are contiguous along the reduction:
+ *     c[M, N] = a[M, K] b[N, K]^T (+ r[M, N])
+ * (the forward x W^T; the backward's input and weight gradients on
+ * transposed operands, as the layer arranges them; r, when not NULL, is the
+ * residual of a fused add: one fp32 rounding of a b^T + r).  Row strides
+ * lda / ldb / ldc / ldr in elements, multiples of 8 and below 2^22; 2-byte
+ * dtypes; operands 16-byte aligned; M and N multiples of 256, K a multiple
+ * of 128 and at least 256 (ZK_EUNSUPPORTED otherwise:
+ * zk_gemm_nt_supported(M, N, K) says in advance). */
+int zk_gemm_nt_supported(int64_t M, int64_t N, int64_t K);
+int zk_gemm_nt(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
+               int64_t ldc, const void* r, int64_t ldr, int64_t M, int64_t N,
+               int64_t K, int dtype, zk_stream_t stream);
+
 /* ------------------------------------------------------------------- RoPE --
  * Replaces apply_rotary_pos_emb / rotate_half (models/llama_simple.py:27-58,
  * HF-style half-split pairing, per-op rounding in the act dtype) and

@@ -106,6 +106,19 @@ def test_validation_codes(lib):
     assert lib.zk_gemm_swiglu(ctypes.c_void_p(24), 64, p, p, 64, p, p, 8, p, 8, None, 0, 8, 8, 64,
                               2, None) == -3
     assert lib.zk_gemm_swiglu(p, 32, p, p, 64, p, p, 8, p, 8, None, 0, 8, 8, 64, 2, None) == -1
+    # gemm_nt: fp32, M not a multiple of 256, K below 256, misaligned b, ld_a < K,
+    # ld not a multiple of 8; the shape query agrees
+    assert lib.zk_gemm_nt(p, 256, p, 256, p, 256, None, 0, 256, 256, 256, 0, None) == -2
+    assert lib.zk_gemm_nt(p, 256, p, 256, p, 256, None, 0, 300, 256, 256, 2, None) == -4
+    assert lib.zk_gemm_nt(p, 256, p, 256, p, 256, None, 0, 256, 256, 128, 2, None) == -4
+    assert lib.zk_gemm_nt(p, 256, ctypes.c_void_p(24), 256, p, 256, None, 0, 256, 256, 256, 2,
+                          None) == -3
+    assert lib.zk_gemm_nt(p, 128, p, 256, p, 256, None, 0, 256, 256, 256, 2, None) == -1
+    assert lib.zk_gemm_nt(p, 260, p, 256, p, 256, None, 0, 256, 256, 256, 2, None) == -3
+    assert lib.zk_gemm_nt(None, 0, None, 0, None, 0, None, 0, 0, 0, 0, 2, None) == 0
+    assert lib.zk_gemm_nt_supported(4096, 22016, 4096) == 1
+    assert lib.zk_gemm_nt_supported(4096, 22016, 4160) == 0
+    assert lib.zk_gemm_nt_supported(4096, 1376, 4096) == 0
     # copy_to_host: negative size, zero size, null, block count, misaligned
     assert lib.zk_copy_to_host(p, p, -1, 16, None) == -1
     assert lib.zk_copy_to_host(None, None, 0, 16, None) == 0

@@ -113,6 +113,83 @@ def test_swiglu_transposed_outputs(dev, rows, cols, dtype):
     assert torch.equal(dgut, dgu.t())
 
 
+def _assert_within_ulp(got, ref, dtype, what):
+    """Every element within one unit in the last place (of the storage
+    dtype, at that element's magnitude) of the exact product: one rounding
+    of an fp32 sum whose order differs from the reference's."""
+    g = got.double().cpu()
+    r = ref.double().cpu()
+    assert torch.isfinite(g).all(), what
+    mant = {torch.bfloat16: 8, torch.float16: 11}[dtype]
+    # the ulp at the larger of the two magnitudes (a sum just below a power
+    # of two may round up across it)
+    _, ex = torch.frexp(torch.maximum(r.abs(), g.abs()).clamp_min(1e-30))
+    ulp = torch.ldexp(torch.ones_like(r), ex - mant)
+    floor = r.abs().max().item() * 2.0 ** -20
+    bad = (g - r).abs() > ulp + floor
+    assert not bad.any(), (f"{what}: {int(bad.sum())} elements beyond one ulp, max err "
+                           f"{(g - r).abs().max().item():.3g}")
+
+
+@pytest.mark.parametrize("M,N,K,dtype,res", [(256, 256, 256, torch.bfloat16, False),
+                                             (512, 768, 384, torch.bfloat16, True),
+                                             (1024, 512, 1280, torch.float16, False),
+                                             (768, 1024, 512, torch.float16, True),
+                                             (2048, 2560, 4096, torch.bfloat16, True)])
+def test_gemm_nt(dev, M, N, K, dtype, res):
+    """zk_gemm_nt (hand-written MFMA GEMM, a @ b^T [+ r]) against the fp64
+    product of the same rounded inputs: every element within one ulp of the
+    storage dtype; grids of one to 80 tiles, K of 2 to 64 steps (the
+    pipeline's prologue / tail paths), with and without the fused residual."""
+    from zorse_amd import kernels as K_
+    print(f"gemm_nt M={M} N={N} K={K} {dtype} residual={res}", flush=True)
+    a = _rand((M, K), dtype, 81)
+    b = _rand((N, K), dtype, 82, 0.05)
+    r = _rand((M, N), dtype, 83) if res else None
+    out = K_.gemm_nt(a.to(dev), b.to(dev), residual=r.to(dev) if res else None)
+    ref = a.double() @ b.double().t()
+    if res:
+        ref = ref + r.double()
+    _assert_within_ulp(out, ref, dtype, "gemm_nt")
+
+
+def test_gemm_nt_strided_views_and_unsupported(dev):
+    """Row-strided operand views (the layer's fused weight slices), an output
+    slice of a wider buffer; shapes off the tile grid are rejected."""
+    from zorse_amd import kernels as K_
+    M, N, K = 512, 512, 512
+    a = _rand((M, K + 64), torch.bfloat16, 84)
+    b = _rand((2 * N, K + 128), torch.bfloat16, 85, 0.05)
+    ad, bd = a.to(dev), b.to(dev)
+    wide = torch.zeros(M, N + 256, device=dev, dtype=torch.bfloat16)
+    K_.gemm_nt(ad[:, 64:], bd[N:, :K], out=wide[:, 256:])
+    ref = a[:, 64:].double() @ b[N:, :K].double().t()
+    _assert_within_ulp(wide[:, 256:], ref, torch.bfloat16, "strided gemm_nt")
+    assert torch.equal(wide[:, :256].cpu(), torch.zeros(M, 256, dtype=torch.bfloat16))
+    assert not K_.gemm_nt_supported(300, 512, 512)
+    with pytest.raises(RuntimeError, match="ZK_EUNSUPPORTED"):
+        K_.gemm_nt(ad[:300, :K], bd[:N, :K])
+
+
+def test_gemm_nt_llama7b_shapes(dev):
+    """The 7B layer's gate|up forward (4096 x 22016 x 4096) and down_proj
+    with its residual (4096 x 4096 x 11008) against a plain PyTorch fp64 GEMM
+    of the same rounded inputs on the GPU."""
+    from zorse_amd import kernels as K_
+    g = torch.Generator(device="cpu").manual_seed(86)
+    for M, N, K in ((4096, 22016, 4096), (4096, 4096, 11008)):
+        print(f"gemm_nt 7B shape {M}x{N}x{K}", flush=True)
+        a = torch.randn(M, K, generator=g).to(dev, torch.bfloat16)
+        b = (0.02 * torch.randn(N, K, generator=g)).to(dev, torch.bfloat16)
+        r = torch.randn(M, N, generator=g).to(dev, torch.bfloat16) if K != 4096 else None
+        out = K_.gemm_nt(a, b, residual=r)
+        ref = torch.mm(a.double(), b.double().t())
+        if r is not None:
+            ref += r.double()
+        _assert_within_ulp(out, ref, torch.bfloat16, f"gemm_nt {M}x{N}x{K}")
+        del a, b, r, out, ref
+
+
 @pytest.mark.parametrize("M,F,K,dtype", [(200, 72, 128, torch.bfloat16), (136, 200, 192, torch.float16),
                                           (8, 8, 64, torch.bfloat16), (1024, 704, 512, torch.bfloat16)])
 def test_gemm_swiglu(dev, M, F, K, dtype):

@@ -181,6 +181,44 @@ def test_layer_ragged_long_sequence(dev, name):
     _check_layer(layer, x, dout, dtype, name)
 
 
+# Layers whose every projection GEMM the hand-written kernel takes (tokens,
+# hidden, q|k|v width and FFN multiples of 256), run with the "hip" GEMM
+# backend: the four forward products and the eight backward ones all go
+# through zk_gemm_nt.
+HIP_GEMM = {
+    "cfg3_fp16_gqa": (CONFIGS["cfg3_fp16_gqa"][0], None, torch.float16, (2, 256)),
+    "cfg4_bf16_F1536": (dict(hidden_size=512, num_attention_heads=4, intermediate_size=1536,
+                             rope_theta=1e4), None, torch.bfloat16, (1, 512)),
+    "cfg5_bf16_swa": (CONFIGS["cfg5_bf16_swa"][0], 160, torch.bfloat16, (1, 512)),
+}
+
+
+@pytest.mark.parametrize("name", list(HIP_GEMM))
+def test_layer_hip_gemm_backend(dev, name, monkeypatch):
+    from zorse_amd import kernels as K
+    from zorse_amd import layer as LY
+    kw, window, dtype, (B, S) = HIP_GEMM[name]
+    print(f"layer {name} (hip GEMM backend)", flush=True)
+    calls = []
+    real = K.gemm_nt
+
+    def counting(*args, **kwargs):
+        calls.append(args[0].shape)
+        return real(*args, **kwargs)
+
+    monkeypatch.setattr(K, "gemm_nt", counting)
+    prev = LY.set_gemm_backend("hip")
+    try:
+        layer = _layer(kw, dev, param_dtype=dtype, window=window, seed=307)
+        g = torch.Generator().manual_seed(29)
+        x = torch.randn(B, S, kw["hidden_size"], generator=g).to(dtype)
+        dout = torch.randn(B, S, kw["hidden_size"], generator=g).to(dtype)
+        _check_layer(layer, x, dout, dtype, f"{name} hip GEMM")
+    finally:
+        LY.set_gemm_backend(prev)
+    assert len(calls) == 12, calls
+
+
 def test_cfg1_head_and_cross_entropy_loss(dev):
     """BASELINE cfg1 end to end: layer + final RMSNorm + linear head + CE over
     integer labels (vocab 1000), fp32, all on this build's kernels (chunked

@@ -81,6 +81,9 @@ SIGNATURES = {
     "zk_swiglu_fwd": (_int, [_ptr, _ptr, _i64, _ptr, _i64, _i64, _i64, _int, _ptr]),
     "zk_swiglu_bwd": (_int, [_ptr, _i64, _ptr, _ptr, _i64, _ptr, _ptr, _i64,
                              _i64, _i64, _int, _ptr]),
+    "zk_gemm_nt_supported": (_int, [_i64, _i64, _i64]),
+    "zk_gemm_nt": (_int, [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _i64,
+                          _int, _ptr]),
     "zk_gemm_swiglu": (_int, [_ptr, _i64, _ptr, _ptr, _i64, _ptr, _ptr, _i64, _ptr, _i64, _ptr,
                                _i64, _i64, _i64, _i64, _int, _ptr]),
     "zk_swiglu_fwd_t": (_int, [_ptr, _ptr, _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _int,

@@ -1,0 +1,331 @@
+// Projection GEMM for gfx950 (bf16 / fp16 storage, fp32 accumulation):
+//
+//   C[M, N] = A[M, K] B[N, K]^T  (+ R[M, N])
+//
+// both operands contiguous along the reduction (the nn.Linear forward
+// x W^T; the layer's backward GEMMs take this form on transposed operands).
+// One fp32 rounding of the accumulated sum (plus R) to the storage type.
+//
+// Workgroup = 4 waves, tile = 256 x 256, one workgroup per CU (160 KB LDS,
+// one wave per SIMD).  Each wave owns a 128 x 128 block: 4 x 4 MFMA blocks of
+// v_mfma_f32_32x32x16 whose 256 accumulators live in AGPRs, so the 256
+// architectural VGPRs hold up to four sets of operands (one per 16-deep
+// substep of a 64-deep K step) read ahead of their MFMAs.
+//
+// Tiles reach LDS through buffer_load_dwordx4 ... lds (16 bytes per lane,
+// 128-byte row segments, XOR-swizzled chunks, see tile_off).  A sits in a ring
+// of three stages and B in a ring of two, so A's loads run two K steps ahead
+// and B's one; the refill of each K step is spread one load per four MFMAs
+// over the whole step, because a burst of loads fills the texture unit's
+// command queue and stalls the issuing wave (counters: SQ_VMEM_TA_CMD_FIFO_FULL),
+// and the operand reads likewise go two per four MFMAs (SQ_LDS_CMD_FIFO_FULL).
+// The loads are issued from inline assembly: with an LDS DMA visible to it,
+// the compiler's wait insertion waits for every load in flight before any LDS
+// read; the kernel orders them itself with exact vmcnt waits (loads complete
+// in issue order) and one barrier per K step.
+//
+// Workgroups are remapped so that the 32 CUs of one XCD (dispatch order
+// round-robins XCDs) take consecutive tiles, ordered in groups of four M
+// tiles, so each XCD's L2 serves a 4 x 8 block of tiles.
+#include "attn_common.h"
+#include "vec.h"
+
+namespace zk {
+namespace gemm {
+
+constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int GROUP_M = 4;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource over [base, base + 2 GiB) as four scalar dwords.
+__device__ __forceinline__ v4i rsrc_words(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  v4i r;
+  r[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu));
+  r[1] = __builtin_amdgcn_readfirstlane(static_cast<int>((a >> 32) & 0xffffu));
+  r[2] = 0x7fffffff;
+  r[3] = 0x00020000;
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(const T* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const T*)(p)));
+}
+
+// 16 bytes per lane from r + voff + soff into LDS at lds + 16 lane.
+__device__ __forceinline__ void dma16(v4i r, uint32_t voff, uint32_t soff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :: "v"(voff), "s"(r), "s"(soff), "s"(lds) : "memory");
+}
+
+// A ROWS x 64 tile (128-byte rows, chunks swizzled by tile_sw<64>) in eight
+// instructions of 32 rows; instruction i of wave w fills LDS chunks
+// 256 i + 64 w .. +63, lane l the chunk of row 32 i + (64 w + l) / 8.
+template <typename T>
+struct TileDma {
+  static constexpr int D = BK, NT = 256, RSTEP = NT / (D / 8);
+  uint32_t lane_off;  // bytes from the tile's first row
+  int wave_el;        // wave-uniform
+  __device__ __forceinline__ void init(int64_t ld) {
+    const int tid = threadIdx.x;
+    const int row = tid / (D / 8);
+    const int c = (tid % (D / 8)) ^ tile_sw<D>(row);
+    lane_off = static_cast<uint32_t>(row * ld * static_cast<int64_t>(sizeof(T)) + c * 16);
+    wave_el = __builtin_amdgcn_readfirstlane(tid >> 6) * 64 * 8;
+  }
+  // piece i (rows 32 i .. 32 i + 31) of the tile whose first row is `gbase`
+  __device__ __forceinline__ void issue(T* tile, const T* gbase, int64_t ld, int i) const {
+    const v4i r = rsrc_words(gbase);
+    const uint32_t soff =
+        static_cast<uint32_t>(static_cast<int64_t>(i) * RSTEP * ld * static_cast<int64_t>(sizeof(T)));
+    dma16(r, lane_off, soff, lds_addr(tile + wave_el) + i * NT * 16);
+  }
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_nt_kernel(const T* __restrict__ A, int64_t lda, const T* __restrict__ B, int64_t ldb,
+                    T* __restrict__ C, int64_t ldc, const T* __restrict__ R, int64_t ldr,
+                    int64_t M, int64_t N, int64_t K) {
+  typedef Mfma<T> Mm;
+  typedef typename Mm::vec8 V8;
+  __shared__ __attribute__((aligned(16))) T As[3 * BM * BK];  // ring of three
+  __shared__ __attribute__((aligned(16))) T Bs0[BN * BK];
+  __shared__ __attribute__((aligned(16))) T Bs1[BN * BK];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t n_m = M / BM, n_n = N / BN, nwg = n_m * n_n;
+  int64_t pid = blockIdx.x;
+  if ((nwg & 7) == 0) pid = (pid & 7) * (nwg >> 3) + (pid >> 3);
+  const int64_t per_group = static_cast<int64_t>(GROUP_M) * n_n;
+  const int64_t grp = pid / per_group;
+  const int64_t mf = grp * GROUP_M;
+  const int64_t gm = n_m - mf < GROUP_M ? n_m - mf : GROUP_M;
+  const int64_t in_grp = pid - grp * per_group;
+  const int64_t m0 = (mf + in_grp % gm) * BM, n0 = (in_grp / gm) * BN;
+  const T* Ab = A + m0 * lda;
+  const T* Bb = B + n0 * ldb;
+
+  TileDma<T> adma, bdma;
+  adma.init(lda);
+  bdma.init(ldb);
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+  // operand rows of substep 0; substep s XORs the chunk index with 2 s
+  int aoff[4], boff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    aoff[i] = tile_off<BK>(wm * 128 + 32 * i + l32, 8 * g);
+    boff[i] = tile_off<BK>(wn * 128 + 32 * i + l32, 8 * g);
+  }
+  V8 xa[4][4], xb[4][4];
+  auto Bs = [&](int st) __attribute__((always_inline)) -> T* { return st ? Bs1 : Bs0; };
+  // operand piece r (0..3: A rows, 4..7: B rows) of substep s into set q
+  auto rd_piece = [&](int sa, int sb, int s, int q, int r) __attribute__((always_inline)) {
+    if (r < 4)
+      xa[q][r] = *reinterpret_cast<const V8*>(&As[sa * (BM * BK) + (aoff[r] ^ (16 * s))]);
+    else
+      xb[q][r - 4] = *reinterpret_cast<const V8*>(&Bs(sb)[boff[r - 4] ^ (16 * s)]);
+  };
+  auto loadA = [&](int sa, int64_t k, int p) __attribute__((always_inline)) {
+    adma.issue(&As[sa * (BM * BK)], Ab + k * BK, lda, p);
+  };
+  auto loadB = [&](int sb, int64_t k, int p) __attribute__((always_inline)) {
+    bdma.issue(Bs(sb), Bb + k * BK, ldb, p);
+  };
+  // The 16 MFMAs of set q in rows of four.  After row c: the loads whose bits
+  // are set in LM (bit 2c: one, bit 2c + 1: another; LK 1: A pieces from p0
+  // on, step k, ring stage lst; LK 2: B pieces into B stage lst), then NR / 4
+  // operand reads (substep s0 of stages (ra, rb) into set q0, then substep
+  // s0 + 1 into set q0 + 1 when NR = 16).  The fences keep this order.
+  auto mm_ld = [&](int q, int lk, int lm, int lst, int64_t k, int p0, int nr, int ra, int rb,
+                   int s0, int q0) __attribute__((always_inline)) {
+    int p = p0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[c][j] = Mm::mma(xa[q][c], xb[q][j], acc[c][j]);
+#pragma unroll
+      for (int e = 0; e < nr / 4; ++e) {
+        const int r = c * (nr / 4) + e;
+        rd_piece(ra, rb, s0 + (r >> 3), q0 + (r >> 3), r & 7);
+      }
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        if (lm & (1 << (2 * c + e))) {
+          if (lk == 1) loadA(lst, k, p);
+          if (lk == 2) loadB(lst, k, p);
+          ++p;
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  const int64_t n_k = K / BK;  // even, >= 4
+  // prologue: steps 0 and 1 of A and B
+#pragma unroll
+  for (int p = 0; p < 8; ++p) loadA(0, 0, p);
+#pragma unroll
+  for (int p = 0; p < 8; ++p) loadB(0, 0, p);
+#pragma unroll
+  for (int p = 0; p < 8; ++p) loadA(1, 1, p);
+#pragma unroll
+  for (int p = 0; p < 8; ++p) loadB(1, 1, p);
+  wait_vmcnt<16>();
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 8; ++r) rd_piece(0, 0, 0, 0, r);
+#pragma unroll
+  for (int r = 0; r < 8; ++r) rd_piece(0, 0, 1, 1, r);
+
+  // K step t: A ring stage sa = t % 3, B stage sb = t % 2; set s = substep s.
+  // Part A: sets 0..2 with A(t + 2) spread over them (into ring stage
+  // (t + 2) % 3, free since the previous barrier) and the reads of sets 2, 3.
+  // Part B: barrier (A(t + 1), B(t + 1) landed everywhere; this step's reads
+  // done), then set 3 with B(t + 2) into B stage sb and the reads of step
+  // t + 1's sets 0, 1.  The loop starts at a part B.
+  int sa = 0;
+  auto partA = [&](auto sb_tag, auto la_tag, int64_t t) __attribute__((always_inline)) {
+    constexpr int sb = decltype(sb_tag)::value;
+    constexpr bool LA = decltype(la_tag)::value;
+    const int sa2 = sa == 0 ? 2 : sa - 1;
+    mm_ld(0, LA ? 1 : 0, 0x11, sa2, t + 2, 0, 8, sa, sb, 2, 2);
+    mm_ld(1, LA ? 1 : 0, 0x25, sa2, t + 2, 2, 8, sa, sb, 3, 3);
+    mm_ld(2, LA ? 1 : 0, 0x45, sa2, t + 2, 5, 0, 0, 0, 0, 0);
+  };
+  // VM8: A(t + 2) was issued in the part A before, and may stay in flight
+  auto partB = [&](auto sb_tag, auto sync_tag, auto vm_tag, auto lb_tag, int64_t t) __attribute__((always_inline)) {
+    constexpr int sb = decltype(sb_tag)::value;
+    constexpr bool SYNC = decltype(sync_tag)::value, VM8 = decltype(vm_tag)::value,
+                   LB = decltype(lb_tag)::value;
+    const int sa1 = sa == 2 ? 0 : sa + 1;
+    if constexpr (SYNC) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      if constexpr (VM8)
+        wait_vmcnt<8>();
+      else
+        wait_vmcnt<0>();
+      __syncthreads();
+      mm_ld(3, LB ? 2 : 0, 0xff, sb, t + 2, 0, 16, sa1, sb ^ 1, 0, 0);
+    } else {
+      mm_ld(3, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0);
+    }
+    sa = sa1;
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using BT = std::true_type;
+  using BF = std::false_type;
+  partA(I0{}, BT{}, 0);
+  int64_t kt = 0;
+  for (; kt + 4 < n_k; kt += 2) {
+    partB(I0{}, BT{}, BT{}, BT{}, kt);
+    partA(I1{}, BT{}, kt + 1);
+    partB(I1{}, BT{}, BT{}, BT{}, kt + 1);
+    partA(I0{}, BT{}, kt + 2);
+  }
+  partB(I0{}, BT{}, BT{}, BT{}, kt);
+  partA(I1{}, BT{}, kt + 1);
+  partB(I1{}, BT{}, BT{}, BT{}, kt + 1);
+  partA(I0{}, BF{}, kt + 2);
+  partB(I0{}, BT{}, BF{}, BF{}, kt + 2);
+  partA(I1{}, BF{}, kt + 3);
+  partB(I1{}, BF{}, BF{}, BF{}, kt + 3);
+
+  // Epilogue, per wave and 32-row block: the fp32 [32][128] block through the
+  // wave's own LDS region (pitch 132 floats), then 16-byte row stores (with R
+  // added in fp32 before the single rounding).
+  __syncthreads();
+  int el = lane;
+  asm volatile("" : "+v"(el));  // keep the epilogue's index math after the loop
+  float* ws = reinterpret_cast<float*>(wave < 3 ? &As[wave * (BM * BK)] : Bs0);
+  const int el32 = el & 31, eg = el >> 5;
+  typedef T T8 __attribute__((ext_vector_type(8)));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        ws[(8 * (r >> 2) + 4 * eg + (r & 3)) * 132 + 32 * j + el32] = acc[i][j][r];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int c = q * 64 + el;
+      const int rr = c >> 4, ch = c & 15;
+      const float4 lo = *reinterpret_cast<const float4*>(&ws[rr * 132 + 8 * ch]);
+      const float4 hi = *reinterpret_cast<const float4*>(&ws[rr * 132 + 8 * ch + 4]);
+      float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      const int64_t grow = m0 + wm * 128 + 32 * i + rr;
+      const int64_t gcol = n0 + wn * 128 + 8 * ch;
+      if (R != nullptr) {
+        const T8 rv = *reinterpret_cast<const T8*>(R + grow * ldr + gcol);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] += to_f32(rv[e]);
+      }
+      T8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = static_cast<T>(v[e]);
+      *reinterpret_cast<T8*>(C + grow * ldc + gcol) = o;
+    }
+  }
+}
+
+}  // namespace gemm
+}  // namespace zk
+
+using namespace zk;
+
+extern "C" int zk_gemm_nt_supported(int64_t M, int64_t N, int64_t K) {
+  return M > 0 && N > 0 && M % gemm::BM == 0 && N % gemm::BN == 0 && K % (2 * gemm::BK) == 0 &&
+         K >= 4 * gemm::BK;
+}
+
+extern "C" int zk_gemm_nt(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
+                          int64_t ldc, const void* r, int64_t ldr, int64_t M, int64_t N,
+                          int64_t K, int dtype, zk_stream_t stream) {
+  ZK_REQUIRE(dtype == ZK_BF16 || dtype == ZK_F16, ZK_EDTYPE,
+             "zk_gemm_nt: 2-byte dtypes only (got %d)", dtype);
+  ZK_REQUIRE(M >= 0 && N >= 0 && K >= 0, ZK_EINVAL, "zk_gemm_nt: bad shape");
+  ZK_REQUIRE(lda >= K && ldb >= K && ldc >= N && (r == nullptr || ldr >= N), ZK_EINVAL,
+             "zk_gemm_nt: bad leading dimension");
+  if (M == 0 || N == 0) return ZK_OK;
+  ZK_REQUIRE(zk_gemm_nt_supported(M, N, K), ZK_EUNSUPPORTED,
+             "zk_gemm_nt: M, N must be multiples of 256 and K a multiple of 128, at least 256 "
+             "(got %lld x %lld x %lld)",
+             (long long)M, (long long)N, (long long)K);
+  const int64_t lds[] = {lda, ldb, ldc, r ? ldr : 8};
+  for (int64_t ld : lds) {
+    ZK_REQUIRE(ld % 8 == 0, ZK_EALIGN, "zk_gemm_nt: leading dimensions must be multiples of 8");
+    // a tile's 256 rows are addressed from one buffer resource (< 2 GiB)
+    ZK_REQUIRE(ld < (int64_t(1) << 22), ZK_EUNSUPPORTED,
+               "zk_gemm_nt: leading dimension out of range");
+  }
+  const void* ptrs[] = {a, b, c};
+  for (const void* p : ptrs) {
+    ZK_REQUIRE(p != nullptr, ZK_EINVAL, "zk_gemm_nt: null pointer");
+    ZK_REQUIRE(aligned(p, 16), ZK_EALIGN, "zk_gemm_nt: operands must be 16-byte aligned");
+  }
+  ZK_REQUIRE(r == nullptr || aligned(r, 16), ZK_EALIGN,
+             "zk_gemm_nt: operands must be 16-byte aligned");
+  const int64_t nwg = (M / gemm::BM) * (N / gemm::BN);
+  ZK_REQUIRE(nwg < 0x7fffffffLL, ZK_EINVAL, "zk_gemm_nt: grid too large");
+  hipStream_t s = as_stream(stream);
+  if (dtype == ZK_BF16)
+    hipLaunchKernelGGL(gemm::gemm_nt_kernel<bf16>, dim3(static_cast<unsigned>(nwg)), dim3(256), 0,
+                       s, (const bf16*)a, lda, (const bf16*)b, ldb, (bf16*)c, ldc,
+                       (const bf16*)r, ldr, M, N, K);
+  else
+    hipLaunchKernelGGL(gemm::gemm_nt_kernel<f16>, dim3(static_cast<unsigned>(nwg)), dim3(256), 0,
+                       s, (const f16*)a, lda, (const f16*)b, ldb, (f16*)c, ldc, (const f16*)r,
+                       ldr, M, N, K);
+  return launch_status("zk_gemm_nt");
+}

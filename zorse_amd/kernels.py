@@ -193,6 +193,44 @@ def swiglu_bwd(dz: torch.Tensor, gate: torch.Tensor, up: torch.Tensor,
                               stream_handle(dev)), "zk_swiglu_bwd")
 
 
+def gemm_nt_supported(M: int, N: int, K: int) -> bool:
+    """Whether zk_gemm_nt takes an [M, K] x [N, K]^T product (M, N multiples
+    of 256, K a multiple of 128 and at least 256)."""
+    return bool(lib().zk_gemm_nt_supported(M, N, K))
+
+
+def gemm_nt(a: torch.Tensor, b: torch.Tensor, residual: torch.Tensor | None = None,
+            out: torch.Tensor | None = None) -> torch.Tensor:
+    """a @ b.T (+ residual) from the hand-written MFMA GEMM: a [M, K] and
+    b [N, K] with unit column stride (contiguous along the reduction), 2-byte
+    dtypes; fp32 accumulation and one rounding.  ``out`` / ``residual``:
+    [M, N] with unit column stride."""
+    dev = _require_gpu(a, b, residual, out)
+    if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[1]:
+        raise ValueError(f"gemm_nt: a [M, K] and b [N, K] expected, got {tuple(a.shape)} and "
+                         f"{tuple(b.shape)}")
+    if a.dtype != b.dtype or a.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("gemm_nt: a and b must share a 2-byte dtype")
+    M, K = a.shape
+    N = b.shape[0]
+    lda = _row_view_check("a", a)
+    ldb = _row_view_check("b", b)
+    if out is None:
+        out = torch.empty(M, N, device=dev, dtype=a.dtype)
+    if out.shape != (M, N) or out.dtype != a.dtype:
+        raise ValueError("gemm_nt: out must be [M, N] of the operands' dtype")
+    ldc = _row_view_check("out", out)
+    ldr = 0
+    if residual is not None:
+        if residual.shape != (M, N) or residual.dtype != a.dtype:
+            raise ValueError("gemm_nt: residual must be [M, N] of the operands' dtype")
+        ldr = _row_view_check("residual", residual)
+    check(lib().zk_gemm_nt(ptr(a), lda, ptr(b), ldb, ptr(out), ldc,
+                           ptr(residual) if residual is not None else None, ldr, M, N, K,
+                           dtype_code(a.dtype), stream_handle(dev)), "zk_gemm_nt")
+    return out
+
+
 def gemm_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
                 gu_out: torch.Tensor | None = None, transposed: bool = False):
     """(gu, z[, z^T]) with gu = [x Wg^T | x Wu^T] ([M, 2F], kept for the
