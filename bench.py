@@ -547,6 +547,8 @@ def main():
     ap.add_argument("--gemm", choices=("hipblaslt", "hip"), default="hipblaslt",
                     help="projection GEMMs of the stage: hipBLASLt (torch.mm / addmm) or the "
                          "hand-written zk_gemm_nt")
+    ap.add_argument("--fused-mlp", action="store_true",
+                    help="gate|up GEMM with the SwiGLU epilogue (zk_gemm_swiglu) in the stage")
     ap.add_argument("--summarize-mfma", metavar="DIR",
                     help="print the MFMA-counter summary of rocprofv3 runs under DIR and exit")
     ap.add_argument("--summarize-traffic", metavar="DIR",
@@ -582,6 +584,8 @@ def main():
     tuned = use_tuned_gemms(not args.default_gemm)
     from zorse_amd import layer as _layer_mod
     _layer_mod.set_gemm_backend(args.gemm)
+    if args.fused_mlp:
+        _layer_mod.set_fused_gate_up(True)
 
     S, B = args.seq, 1
     if args.kernel:
@@ -648,6 +652,8 @@ def main():
                    "layers": args.layers, "hidden": spec.hidden, "heads": spec.heads,
                    "head_dim": spec.head_dim, "ffn": spec.ffn, "micro_batch": B, "seq_len": S,
                    "global_batch": B, "parallelism": "none (1 GPU)",
+                   "gate_up_swiglu": ("fused (zk_gemm_swiglu)" if _layer_mod._fused_gate_up
+                                      else "GEMM + zk_swiglu_fwd_t"),
                    "projection_gemms": ("hand-written zk_gemm_nt (zorse_amd/csrc/gemm.hip)"
                                         if args.gemm == "hip" else
                                         "hipBLASLt via torch.mm/addmm" + (

@@ -181,10 +181,10 @@ def test_layer_ragged_long_sequence(dev, name):
     _check_layer(layer, x, dout, dtype, name)
 
 
-# Layers whose every projection GEMM the hand-written kernel takes (tokens,
+# Layers whose every projection GEMM the hand-written kernels take (tokens,
 # hidden, q|k|v width and FFN multiples of 256), run with the "hip" GEMM
-# backend: the four forward products and the eight backward ones all go
-# through zk_gemm_nt.
+# backend: the four forward products (gate|up through zk_gemm_swiglu with its
+# SwiGLU epilogue, the others through zk_gemm_nt) and the eight backward ones.
 HIP_GEMM = {
     "cfg3_fp16_gqa": (CONFIGS["cfg3_fp16_gqa"][0], None, torch.float16, (2, 256)),
     "cfg4_bf16_F1536": (dict(hidden_size=512, num_attention_heads=4, intermediate_size=1536,
@@ -200,14 +200,17 @@ def test_layer_hip_gemm_backend(dev, name, monkeypatch):
     kw, window, dtype, (B, S) = HIP_GEMM[name]
     print(f"layer {name} (hip GEMM backend)", flush=True)
     calls = []
-    real = K.gemm_nt
 
-    def counting(*args, **kwargs):
-        calls.append(args[0].shape)
-        return real(*args, **kwargs)
+    def counting(real):
+        def fn(*args, **kwargs):
+            calls.append((real.__name__, tuple(args[0].shape)))
+            return real(*args, **kwargs)
+        return fn
 
-    monkeypatch.setattr(K, "gemm_nt", counting)
+    monkeypatch.setattr(K, "gemm_nt", counting(K.gemm_nt))
+    monkeypatch.setattr(K, "gemm_swiglu", counting(K.gemm_swiglu))
     prev = LY.set_gemm_backend("hip")
+    prev_fused = LY.set_fused_gate_up(True)
     try:
         layer = _layer(kw, dev, param_dtype=dtype, window=window, seed=307)
         g = torch.Generator().manual_seed(29)
@@ -216,7 +219,8 @@ def test_layer_hip_gemm_backend(dev, name, monkeypatch):
         _check_layer(layer, x, dout, dtype, f"{name} hip GEMM")
     finally:
         LY.set_gemm_backend(prev)
-    assert len(calls) == 12, calls
+        LY.set_fused_gate_up(prev_fused)
+    assert len(calls) == 12 and sum(c[0] == "gemm_swiglu" for c in calls) == 1, calls
 
 
 def test_cfg1_head_and_cross_entropy_loss(dev):

@@ -61,6 +61,28 @@ __device__ __forceinline__ void dma16(v4i r, uint32_t voff, uint32_t soff, uint3
                :: "v"(voff), "s"(r), "s"(soff), "s"(lds) : "memory");
 }
 
+// Operands and outputs of one launch.  EPI 0: c = a b^T (+ r); EPI 1 (the
+// gate|up projection with the SwiGLU epilogue): b = W_gate, b2 = W_up (each
+// [F, K]), N = 2F, c / c2 = g / u (row stride ldc), z = SwiGLU(g, u) and,
+// when zt is not NULL, zt = z^T.
+struct GemmArgs {
+  const void* a;
+  int64_t lda;
+  const void* b;
+  const void* b2;
+  int64_t ldb;
+  void* c;
+  void* c2;
+  int64_t ldc;
+  const void* r;
+  int64_t ldr;
+  void* z;
+  int64_t ldz;
+  void* zt;
+  int64_t ldzt;
+  int64_t M, N, K;
+};
+
 // A ROWS x 64 tile (128-byte rows, chunks swizzled by tile_sw<64>) in eight
 // instructions of 32 rows; instruction i of wave w fills LDS chunks
 // 256 i + 64 w .. +63, lane l the chunk of row 32 i + (64 w + l) / 8.
@@ -76,6 +98,10 @@ struct TileDma {
     lane_off = static_cast<uint32_t>(row * ld * static_cast<int64_t>(sizeof(T)) + c * 16);
     wave_el = __builtin_amdgcn_readfirstlane(tid >> 6) * 64 * 8;
   }
+  // piece i (tile rows 32 i .. 32 i + 31) from 32 source rows starting at src
+  __device__ __forceinline__ void issue_rows(T* tile, const T* src, int i) const {
+    dma16(rsrc_words(src), lane_off, 0, lds_addr(tile + wave_el) + i * NT * 16);
+  }
   // piece i (rows 32 i .. 32 i + 31) of the tile whose first row is `gbase`
   __device__ __forceinline__ void issue(T* tile, const T* gbase, int64_t ld, int i) const {
     const v4i r = rsrc_words(gbase);
@@ -85,11 +111,23 @@ struct TileDma {
   }
 };
 
-template <typename T>
+// silu(g) = g / (1 + e^-g) from the hardware exp2 and reciprocal (about one
+// fp32 ulp each): the epilogue's four waves per CU evaluate it for every
+// output element of the tile while the CU's MFMAs wait, so the IEEE exp and
+// division (about four times the instructions) would cost ~10 % of the GEMM.
+// Rounded to bf16 / fp16 right after, it differs from the IEEE form in about
+// one element in 10^4, by one ulp of the storage type.
+__device__ __forceinline__ float silu_fast(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
+}
+
+template <typename T, int EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void gemm_nt_kernel(const T* __restrict__ A, int64_t lda, const T* __restrict__ B, int64_t ldb,
-                    T* __restrict__ C, int64_t ldc, const T* __restrict__ R, int64_t ldr,
-                    int64_t M, int64_t N, int64_t K) {
+void gemm_nt_kernel(GemmArgs args) {
+  const T* __restrict__ A = static_cast<const T*>(args.a);
+  const T* __restrict__ B = static_cast<const T*>(args.b);
+  const int64_t lda = args.lda, ldb = args.ldb;
+  const int64_t M = args.M, N = args.N, K = args.K;
   typedef Mfma<T> Mm;
   typedef typename Mm::vec8 V8;
   __shared__ __attribute__((aligned(16))) T As[3 * BM * BK];  // ring of three
@@ -110,6 +148,10 @@ void gemm_nt_kernel(const T* __restrict__ A, int64_t lda, const T* __restrict__ 
   const int64_t m0 = (mf + in_grp % gm) * BM, n0 = (in_grp / gm) * BN;
   const T* Ab = A + m0 * lda;
   const T* Bb = B + n0 * ldb;
+  // EPI 1: the tile's 128 features f0 .. f0 + 127 of both halves; wave half
+  // wn holds features f0 + 64 wn .. +63 as MFMA blocks gate 0-31, up 0-31,
+  // gate 32-63, up 32-63, so g and u of one element sit in one lane
+  const int64_t f0 = n0 / 2;
 
   TileDma<T> adma, bdma;
   adma.init(lda);
@@ -139,7 +181,13 @@ void gemm_nt_kernel(const T* __restrict__ A, int64_t lda, const T* __restrict__ 
     adma.issue(&As[sa * (BM * BK)], Ab + k * BK, lda, p);
   };
   auto loadB = [&](int sb, int64_t k, int p) __attribute__((always_inline)) {
-    bdma.issue(Bs(sb), Bb + k * BK, ldb, p);
+    if constexpr (EPI == 0) {
+      bdma.issue(Bs(sb), Bb + k * BK, ldb, p);
+    } else {
+      const int j = p & 3;
+      const T* w = static_cast<const T*>(j & 1 ? args.b2 : args.b);
+      bdma.issue_rows(Bs(sb), w + (f0 + (p >> 2) * 64 + (j >> 1) * 32) * ldb + k * BK, p);
+    }
   };
   // The 16 MFMAs of set q in rows of four.  After row c: the loads whose bits
   // are set in LM (bit 2c: one, bit 2c + 1: another; LK 1: A pieces from p0
@@ -242,8 +290,7 @@ void gemm_nt_kernel(const T* __restrict__ A, int64_t lda, const T* __restrict__ 
   partB(I1{}, BF{}, BF{}, BF{}, kt + 3);
 
   // Epilogue, per wave and 32-row block: the fp32 [32][128] block through the
-  // wave's own LDS region (pitch 132 floats), then 16-byte row stores (with R
-  // added in fp32 before the single rounding).
+  // wave's own LDS region (pitch 132 floats), then 16-byte row stores.
   __syncthreads();
   int el = lane;
   asm volatile("" : "+v"(el));  // keep the epilogue's index math after the loop
@@ -257,24 +304,75 @@ void gemm_nt_kernel(const T* __restrict__ A, int64_t lda, const T* __restrict__ 
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         ws[(8 * (r >> 2) + 4 * eg + (r & 3)) * 132 + 32 * j + el32] = acc[i][j][r];
+    const int64_t row0 = m0 + wm * 128 + 32 * i;
+    if constexpr (EPI == 0) {
+      // c = acc (+ r), one rounding
+      T* C = static_cast<T*>(args.c);
+      const T* R = static_cast<const T*>(args.r);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int c = q * 64 + el;
-      const int rr = c >> 4, ch = c & 15;
-      const float4 lo = *reinterpret_cast<const float4*>(&ws[rr * 132 + 8 * ch]);
-      const float4 hi = *reinterpret_cast<const float4*>(&ws[rr * 132 + 8 * ch + 4]);
-      float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-      const int64_t grow = m0 + wm * 128 + 32 * i + rr;
-      const int64_t gcol = n0 + wn * 128 + 8 * ch;
-      if (R != nullptr) {
-        const T8 rv = *reinterpret_cast<const T8*>(R + grow * ldr + gcol);
+      for (int q = 0; q < 8; ++q) {
+        const int c = q * 64 + el;
+        const int rr = c >> 4, ch = c & 15;
+        const float4 lo = *reinterpret_cast<const float4*>(&ws[rr * 132 + 8 * ch]);
+        const float4 hi = *reinterpret_cast<const float4*>(&ws[rr * 132 + 8 * ch + 4]);
+        float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        const int64_t grow = row0 + rr;
+        const int64_t gcol = n0 + wn * 128 + 8 * ch;
+        if (R != nullptr) {
+          const T8 rv = *reinterpret_cast<const T8*>(R + grow * args.ldr + gcol);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] += to_f32(rv[e]);
+          for (int e = 0; e < 8; ++e) v[e] += to_f32(rv[e]);
+        }
+        T8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = static_cast<T>(v[e]);
+        *reinterpret_cast<T8*>(C + grow * args.ldc + gcol) = o;
       }
-      T8 o;
+    } else {
+      // g, u rounded as the GEMM would store them; z = round(round(silu(g)) u)
+      // (the SwiGLU kernel's rounding points); z also into a feature-major
+      // tile (pitch 40) for the transposed store
+      T* G = static_cast<T*>(args.c);
+      T* U = static_cast<T*>(args.c2);
+      T* Z = static_cast<T*>(args.z);
+      T* zs = reinterpret_cast<T*>(ws + 32 * 132);
+      const int64_t fw0 = f0 + wn * 64;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = static_cast<T>(v[e]);
-      *reinterpret_cast<T8*>(C + grow * ldc + gcol) = o;
+      for (int q = 0; q < 4; ++q) {
+        const int it = q * 64 + el;
+        const int rr = it >> 3, jg = (it >> 2) & 1, c = it & 3;
+        const float* gp = &ws[rr * 132 + 64 * jg + 8 * c];
+        const float4 g0 = *reinterpret_cast<const float4*>(gp);
+        const float4 g1 = *reinterpret_cast<const float4*>(gp + 4);
+        const float4 u0 = *reinterpret_cast<const float4*>(gp + 32);
+        const float4 u1 = *reinterpret_cast<const float4*>(gp + 36);
+        const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+        T8 go, uo, zo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          go[e] = static_cast<T>(gv[e]);
+          uo[e] = static_cast<T>(uv[e]);
+          zo[e] = static_cast<T>(round_to<T>(silu_fast(to_f32(go[e]))) * to_f32(uo[e]));
+          zs[(32 * jg + 8 * c + e) * 40 + rr] = zo[e];
+        }
+        const int64_t grow = row0 + rr;
+        const int64_t f = fw0 + 32 * jg + 8 * c;
+        *reinterpret_cast<T8*>(G + grow * args.ldc + f) = go;
+        *reinterpret_cast<T8*>(U + grow * args.ldc + f) = uo;
+        *reinterpret_cast<T8*>(Z + grow * args.ldz + f) = zo;
+      }
+      if (args.zt != nullptr) {
+        T* ZT = static_cast<T*>(args.zt);
+        // 64 feature rows x 4 chunks of 8 tokens
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int ch = q * 64 + el;
+          const int fr = ch >> 2, tc = ch & 3;
+          const T8 v = *reinterpret_cast<const T8*>(&zs[fr * 40 + 8 * tc]);
+          *reinterpret_cast<T8*>(ZT + (fw0 + fr) * args.ldzt + row0 + 8 * tc) = v;
+        }
+      }
     }
   }
 }
@@ -318,14 +416,69 @@ extern "C" int zk_gemm_nt(const void* a, int64_t lda, const void* b, int64_t ldb
              "zk_gemm_nt: operands must be 16-byte aligned");
   const int64_t nwg = (M / gemm::BM) * (N / gemm::BN);
   ZK_REQUIRE(nwg < 0x7fffffffLL, ZK_EINVAL, "zk_gemm_nt: grid too large");
+  gemm::GemmArgs ga{};
+  ga.a = a;
+  ga.lda = lda;
+  ga.b = b;
+  ga.ldb = ldb;
+  ga.c = c;
+  ga.ldc = ldc;
+  ga.r = r;
+  ga.ldr = ldr;
+  ga.M = M;
+  ga.N = N;
+  ga.K = K;
   hipStream_t s = as_stream(stream);
   if (dtype == ZK_BF16)
-    hipLaunchKernelGGL(gemm::gemm_nt_kernel<bf16>, dim3(static_cast<unsigned>(nwg)), dim3(256), 0,
-                       s, (const bf16*)a, lda, (const bf16*)b, ldb, (bf16*)c, ldc,
-                       (const bf16*)r, ldr, M, N, K);
+    hipLaunchKernelGGL((gemm::gemm_nt_kernel<bf16, 0>), dim3(static_cast<unsigned>(nwg)),
+                       dim3(256), 0, s, ga);
   else
-    hipLaunchKernelGGL(gemm::gemm_nt_kernel<f16>, dim3(static_cast<unsigned>(nwg)), dim3(256), 0,
-                       s, (const f16*)a, lda, (const f16*)b, ldb, (f16*)c, ldc, (const f16*)r,
-                       ldr, M, N, K);
+    hipLaunchKernelGGL((gemm::gemm_nt_kernel<f16, 0>), dim3(static_cast<unsigned>(nwg)),
+                       dim3(256), 0, s, ga);
   return launch_status("zk_gemm_nt");
 }
+
+namespace zk {
+
+// The gate|up projection with the SwiGLU epilogue on the 256 x 256 pipeline
+// (zk_gemm_swiglu routes the shapes it takes here: M a multiple of 256, F of
+// 128, K of 128 and at least 256).  Arguments as zk_gemm_swiglu, already
+// validated.
+int zk_gemm_swiglu_tiled_supported(int64_t M, int64_t F, int64_t K) {
+  return zk_gemm_nt_supported(M, 2 * F, K);
+}
+
+int zk_gemm_swiglu_tiled(const void* x, int64_t ld_x, const void* w_gate, const void* w_up,
+                         int64_t ld_w, void* g_out, void* u_out, int64_t ld_gu, void* z,
+                         int64_t ld_z, void* zt, int64_t ld_zt, int64_t M, int64_t F, int64_t K,
+                         int dtype, zk_stream_t stream) {
+  ZK_REQUIRE(ld_x < (int64_t(1) << 22) && ld_w < (int64_t(1) << 22), ZK_EUNSUPPORTED,
+             "zk_gemm_swiglu: leading dimension out of range");
+  gemm::GemmArgs ga{};
+  ga.a = x;
+  ga.lda = ld_x;
+  ga.b = w_gate;
+  ga.b2 = w_up;
+  ga.ldb = ld_w;
+  ga.c = g_out;
+  ga.c2 = u_out;
+  ga.ldc = ld_gu;
+  ga.z = z;
+  ga.ldz = ld_z;
+  ga.zt = zt;
+  ga.ldzt = ld_zt;
+  ga.M = M;
+  ga.N = 2 * F;
+  ga.K = K;
+  const int64_t nwg = (M / gemm::BM) * (2 * F / gemm::BN);
+  hipStream_t s = as_stream(stream);
+  if (dtype == ZK_BF16)
+    hipLaunchKernelGGL((gemm::gemm_nt_kernel<bf16, 1>), dim3(static_cast<unsigned>(nwg)),
+                       dim3(256), 0, s, ga);
+  else
+    hipLaunchKernelGGL((gemm::gemm_nt_kernel<f16, 1>), dim3(static_cast<unsigned>(nwg)),
+                       dim3(256), 0, s, ga);
+  return launch_status("zk_gemm_swiglu");
+}
+
+}  // namespace zk

@@ -173,6 +173,15 @@ void gemm_swiglu_kernel(const T* __restrict__ x, int64_t ld_x, const T* __restri
 
 }  // namespace zk
 
+namespace zk {
+// the 256 x 256 pipeline of gemm.hip, for the shapes it takes
+int zk_gemm_swiglu_tiled_supported(int64_t M, int64_t F, int64_t K);
+int zk_gemm_swiglu_tiled(const void* x, int64_t ld_x, const void* w_gate, const void* w_up,
+                         int64_t ld_w, void* g_out, void* u_out, int64_t ld_gu, void* z,
+                         int64_t ld_z, void* zt, int64_t ld_zt, int64_t M, int64_t F, int64_t K,
+                         int dtype, zk_stream_t stream);
+}  // namespace zk
+
 using namespace zk;
 
 extern "C" int zk_gemm_swiglu(const void* x, int64_t ld_x, const void* w_gate,
@@ -205,6 +214,9 @@ extern "C" int zk_gemm_swiglu(const void* x, int64_t ld_x, const void* w_gate,
   // the tile loaders keep a 32-row span of one operand in a 32-bit byte offset
   ZK_REQUIRE(ld_x < (int64_t(1) << 26) && ld_w < (int64_t(1) << 26), ZK_EUNSUPPORTED,
              "zk_gemm_swiglu: leading dimension out of range");
+  if (zk_gemm_swiglu_tiled_supported(M, F, K))
+    return zk_gemm_swiglu_tiled(x, ld_x, w_gate, w_up, ld_w, g_out, u_out, ld_gu, z, ld_z, zt,
+                                ld_zt, M, F, K, dtype, stream);
   const int64_t n_wg = ((M + C::BM - 1) / C::BM) * ((F + C::BF - 1) / C::BF);
   ZK_REQUIRE(n_wg < 0x7fffffffLL, ZK_EINVAL, "zk_gemm_swiglu: grid too large");
   hipStream_t s = as_stream(stream);

@@ -104,6 +104,23 @@ if _gemm_backend not in _GEMM_BACKENDS:
     raise ValueError(f"ZORSE_GEMM must be one of {_GEMM_BACKENDS}, got {_gemm_backend!r}")
 
 
+# gate|up GEMM with the SwiGLU activation in its epilogue (zk_gemm_swiglu on
+# the 256 x 256 pipeline: writes g, u, z and z^T in one pass) wherever that
+# pipeline takes the shape; otherwise the GEMM and a separate SwiGLU pass.
+# Off by default: for the 7B layer the fused kernel takes 636 us against
+# 583 us for hipBLASLt's GEMM plus the SwiGLU pass (rotating operands), and
+# the 8-layer stage runs 0.5 ms/step slower with it.  ZORSE_FUSED_MLP=1 or
+# set_fused_gate_up(True) turns it on.
+_fused_gate_up = os.environ.get("ZORSE_FUSED_MLP", "0") != "0"
+
+
+def set_fused_gate_up(enable: bool) -> bool:
+    """Enable / disable the fused gate|up + SwiGLU GEMM; returns the previous setting."""
+    global _fused_gate_up
+    prev, _fused_gate_up = _fused_gate_up, bool(enable)
+    return prev
+
+
 def set_gemm_backend(name: str) -> str:
     """Select the projection GEMM ("hipblaslt" or "hip"); returns the previous one."""
     global _gemm_backend
@@ -255,14 +272,23 @@ def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=Non
     # hdn = x + round(o_proj) and its normalisation, the reference's order)
     attn_out = _mm(o2, w.o.t())
     n2, rstd2, hdn = K.rmsnorm_fwd(attn_out, w.ln2, spec.eps, residual=x2)
-    gu = _mm(n2, w.gu.t())                           # [T, 2F] = gate | up
     F = spec.ffn
-    if _swiglu_transposed(gu, F):
-        # z^T is what down_proj's weight gradient reads; z itself is only
-        # needed for the GEMM below
-        z, zs = K.swiglu_fwd_t(gu[:, :F], gu[:, F:])
+    if (_fused_gate_up and n2.dtype in (torch.bfloat16, torch.float16)
+            and K.gemm_nt_supported(T, 2 * F, h)):
+        # one GEMM writes gate | up (kept for the backward), z and, when the
+        # down projection's weight gradient takes the transposed form, z^T
+        want_t = _transposing(n2) and F % 8 == 0
+        res = K.gemm_swiglu(n2, w.gu[:F], w.gu[F:], transposed=want_t)
+        gu, z = res[0], res[1]
+        zs = res[2] if want_t else z
     else:
-        z = zs = K.swiglu_fwd(gu[:, :F], gu[:, F:])
+        gu = _mm(n2, w.gu.t())                       # [T, 2F] = gate | up
+        if _swiglu_transposed(gu, F):
+            # z^T is what down_proj's weight gradient reads; z itself is only
+            # needed for the GEMM below
+            z, zs = K.swiglu_fwd_t(gu[:, :F], gu[:, F:])
+        else:
+            z = zs = K.swiglu_fwd(gu[:, :F], gu[:, F:])
     out = _addmm(hdn, z, w.down.t())                 # residual + down(z)
     del z
     saved = (x2, n1, rstd1, qkv, o2, o2t, lse, hdn, n2, rstd2, gu, zs, positions)
