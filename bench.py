@@ -346,6 +346,8 @@ def summarize_stage(root: str, layers: int, steps: int, warmup: int) -> str:
     win = [r for r in trace
            if int(r["Start_Timestamp"]) >= t0 and int(r["End_Timestamp"]) <= t1]
     groups = [("hipBLASLt GEMMs", ("Cijk",)),
+              ("hand-written GEMMs (zk_gemm_nt / zk_gemm_swiglu)",
+               ("gemm_nt_kernel", "gemm_swiglu_kernel")),
               ("attention bwd: dq, dkdv", ("attn_bwd",)),
               ("AdamW (optimizer stream, overlapped)", ("adamw",)),
               ("attention fwd", ("attn_fwd",)),
