@@ -93,7 +93,7 @@ __device__ __forceinline__ void store_rows_transposed(const f32x16 (&x)[D / 32],
   __syncthreads();
 }
 
-// MFMA selection by storage type: 32x32x16 with fp32 accumulation.
+// MFMA selection by storage type: 32x32x16 (and 16x16x32) with fp32 accumulation.
 template <typename T>
 struct Mfma;
 
@@ -103,6 +103,9 @@ struct Mfma<bf16> {
   static __device__ __forceinline__ f32x16 mma(vec8 a, vec8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
+  static __device__ __forceinline__ f32x4 mma16(vec8 a, vec8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
 };
 
 template <>
@@ -110,6 +113,9 @@ struct Mfma<f16> {
   typedef f16x8 vec8;
   static __device__ __forceinline__ f32x16 mma(vec8 a, vec8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16(vec8 a, vec8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
 };
 

@@ -7,18 +7,20 @@
 // One fp32 rounding of the accumulated sum (plus R) to the storage type.
 //
 // Workgroup = 4 waves, tile = 256 x 256, one workgroup per CU (160 KB LDS,
-// one wave per SIMD).  Each wave owns a 128 x 128 block: 4 x 4 MFMA blocks of
-// v_mfma_f32_32x32x16 whose 256 accumulators live in AGPRs, so the 256
-// architectural VGPRs hold up to four sets of operands (one per 16-deep
-// substep of a 64-deep K step) read ahead of their MFMAs.
+// one wave per SIMD).  Each wave owns a 128 x 128 block: 8 x 8 MFMA blocks of
+// v_mfma_f32_16x16x32 whose 256 accumulators live in AGPRs, so the 256
+// architectural VGPRs hold two sets of operands (one per 32-deep substep of a
+// 64-deep K step), the next read during the current one's MFMAs.  (The same
+// pipeline on 4 x 4 blocks of v_mfma_f32_32x32x16 ran 6-10 % slower at the
+// 7B shapes.)
 //
 // Tiles reach LDS through buffer_load_dwordx4 ... lds (16 bytes per lane,
 // 128-byte row segments, XOR-swizzled chunks, see tile_off).  A sits in a ring
 // of three stages and B in a ring of two, so A's loads run two K steps ahead
-// and B's one; the refill of each K step is spread one load per four MFMAs
+// and B's one; the refill of each K step is spread one load per eight MFMAs
 // over the whole step, because a burst of loads fills the texture unit's
 // command queue and stalls the issuing wave (counters: SQ_VMEM_TA_CMD_FIFO_FULL),
-// and the operand reads likewise go two per four MFMAs (SQ_LDS_CMD_FIFO_FULL).
+// and the operand reads likewise go two per eight MFMAs (SQ_LDS_CMD_FIFO_FULL).
 // The loads are issued from inline assembly: with an LDS DMA visible to it,
 // the compiler's wait insertion waits for every load in flight before any LDS
 // read; the kernel orders them itself with exact vmcnt waits (loads complete
@@ -34,7 +36,7 @@ namespace zk {
 namespace gemm {
 
 constexpr int BM = 256, BN = 256, BK = 64;
-constexpr int GROUP_M = 4;
+constexpr int GROUP_M = 4;  // 8 and 16 measured slower in the 7B stage
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -89,18 +91,20 @@ struct GemmArgs {
 template <typename T>
 struct TileDma {
   static constexpr int D = BK, NT = 256, RSTEP = NT / (D / 8);
-  uint32_t lane_off;  // bytes from the tile's first row
-  int wave_el;        // wave-uniform
+  uint32_t lane_off;   // bytes from the tile's first row
+  uint32_t lane_off8;  // bytes from the wave's first row (8 rows per wave)
+  int wave_el;         // wave-uniform
   __device__ __forceinline__ void init(int64_t ld) {
     const int tid = threadIdx.x;
     const int row = tid / (D / 8);
     const int c = (tid % (D / 8)) ^ tile_sw<D>(row);
     lane_off = static_cast<uint32_t>(row * ld * static_cast<int64_t>(sizeof(T)) + c * 16);
+    lane_off8 = static_cast<uint32_t>((row & 7) * ld * static_cast<int64_t>(sizeof(T)) + c * 16);
     wave_el = __builtin_amdgcn_readfirstlane(tid >> 6) * 64 * 8;
   }
-  // piece i (tile rows 32 i .. 32 i + 31) from 32 source rows starting at src
-  __device__ __forceinline__ void issue_rows(T* tile, const T* src, int i) const {
-    dma16(rsrc_words(src), lane_off, 0, lds_addr(tile + wave_el) + i * NT * 16);
+  // piece i: this wave's 8 tile rows (32 i + 8 w ..) from 8 source rows at src
+  __device__ __forceinline__ void issue_wave_rows(T* tile, const T* src, int i) const {
+    dma16(rsrc_words(src), lane_off8, 0, lds_addr(tile + wave_el) + i * NT * 16);
   }
   // piece i (rows 32 i .. 32 i + 31) of the tile whose first row is `gbase`
   __device__ __forceinline__ void issue(T* tile, const T* gbase, int64_t ld, int i) const {
@@ -135,7 +139,7 @@ void gemm_nt_kernel(GemmArgs args) {
   __shared__ __attribute__((aligned(16))) T Bs1[BN * BK];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l32 = lane & 31, g = lane >> 5;
+  const int l16 = lane & 15, q4 = lane >> 4;
   const int wm = wave >> 1, wn = wave & 1;
   const int64_t n_m = M / BM, n_n = N / BN, nwg = n_m * n_n;
   int64_t pid = blockIdx.x;
@@ -148,34 +152,37 @@ void gemm_nt_kernel(GemmArgs args) {
   const int64_t m0 = (mf + in_grp % gm) * BM, n0 = (in_grp / gm) * BN;
   const T* Ab = A + m0 * lda;
   const T* Bb = B + n0 * ldb;
-  // EPI 1: the tile's 128 features f0 .. f0 + 127 of both halves; wave half
-  // wn holds features f0 + 64 wn .. +63 as MFMA blocks gate 0-31, up 0-31,
-  // gate 32-63, up 32-63, so g and u of one element sit in one lane
+  // EPI 1: the tile's 128 features f0 .. f0 + 127 of both halves.  Tile row
+  // block b (16 rows) holds, for wave half wn = b / 8 and jj = b % 8, the gate
+  // (jj even) or up (jj odd) rows of features f0 + 64 wn + 16 (jj / 2) ..
+  // +15, so a lane's MFMA blocks jj and jj + 1 are g and u of one element.
   const int64_t f0 = n0 / 2;
 
   TileDma<T> adma, bdma;
   adma.init(lda);
   bdma.init(ldb);
-  f32x16 acc[4][4];
+  f32x4 acc[8][8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-  // operand rows of substep 0; substep s XORs the chunk index with 2 s
-  int aoff[4], boff[4];
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{};
+  // operand row blocks of substep 0 (16 rows; lane: row l % 16, 16-byte
+  // chunk l / 16); substep s XORs the chunk index with 4 s
+  int aoff[8], boff[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    aoff[i] = tile_off<BK>(wm * 128 + 32 * i + l32, 8 * g);
-    boff[i] = tile_off<BK>(wn * 128 + 32 * i + l32, 8 * g);
+  for (int i = 0; i < 8; ++i) {
+    aoff[i] = tile_off<BK>(wm * 128 + 16 * i + l16, 8 * q4);
+    boff[i] = tile_off<BK>(wn * 128 + 16 * i + l16, 8 * q4);
   }
-  V8 xa[4][4], xb[4][4];
+  V8 xa[2][8], xb[2][8];
   auto Bs = [&](int st) __attribute__((always_inline)) -> T* { return st ? Bs1 : Bs0; };
-  // operand piece r (0..3: A rows, 4..7: B rows) of substep s into set q
+  // operand piece r (0..7: A row blocks, 8..15: B row blocks) of substep s
+  // into set q
   auto rd_piece = [&](int sa, int sb, int s, int q, int r) __attribute__((always_inline)) {
-    if (r < 4)
-      xa[q][r] = *reinterpret_cast<const V8*>(&As[sa * (BM * BK) + (aoff[r] ^ (16 * s))]);
+    if (r < 8)
+      xa[q][r] = *reinterpret_cast<const V8*>(&As[sa * (BM * BK) + (aoff[r] ^ (32 * s))]);
     else
-      xb[q][r - 4] = *reinterpret_cast<const V8*>(&Bs(sb)[boff[r - 4] ^ (16 * s)]);
+      xb[q][r - 8] = *reinterpret_cast<const V8*>(&Bs(sb)[boff[r - 8] ^ (32 * s)]);
   };
   auto loadA = [&](int sa, int64_t k, int p) __attribute__((always_inline)) {
     adma.issue(&As[sa * (BM * BK)], Ab + k * BK, lda, p);
@@ -184,36 +191,30 @@ void gemm_nt_kernel(GemmArgs args) {
     if constexpr (EPI == 0) {
       bdma.issue(Bs(sb), Bb + k * BK, ldb, p);
     } else {
-      const int j = p & 3;
-      const T* w = static_cast<const T*>(j & 1 ? args.b2 : args.b);
-      bdma.issue_rows(Bs(sb), w + (f0 + (p >> 2) * 64 + (j >> 1) * 32) * ldb + k * BK, p);
+      // this wave's rows 32 p + 8 w .. +7 lie in row block 2 p + w / 2
+      const int bk = 2 * p + (wave >> 1);
+      const int jj = bk & 7;
+      const T* w = static_cast<const T*>(jj & 1 ? args.b2 : args.b);
+      const int64_t frow = f0 + (bk >> 3) * 64 + (jj >> 1) * 16 + 8 * (wave & 1);
+      bdma.issue_wave_rows(Bs(sb), w + frow * ldb + k * BK, p);
     }
   };
-  // The 16 MFMAs of set q in rows of four.  After row c: the loads whose bits
-  // are set in LM (bit 2c: one, bit 2c + 1: another; LK 1: A pieces from p0
-  // on, step k, ring stage lst; LK 2: B pieces into B stage lst), then NR / 4
-  // operand reads (substep s0 of stages (ra, rb) into set q0, then substep
-  // s0 + 1 into set q0 + 1 when NR = 16).  The fences keep this order.
-  auto mm_ld = [&](int q, int lk, int lm, int lst, int64_t k, int p0, int nr, int ra, int rb,
-                   int s0, int q0) __attribute__((always_inline)) {
-    int p = p0;
+  // The 64 MFMAs of set q in rows of eight.  After row c: one load (LK 1: A
+  // piece c of step k into ring stage lst; LK 2: B piece c into B stage lst)
+  // and, when RD, operand pieces 2c, 2c + 1 of substep s0 of stages (ra, rb)
+  // into set q0.  The fences keep this order.
+  auto mm_ld = [&](int q, int lk, int lst, int64_t k, bool rd, int ra, int rb, int s0,
+                   int q0) __attribute__((always_inline)) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < 8; ++c) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[c][j] = Mm::mma(xa[q][c], xb[q][j], acc[c][j]);
-#pragma unroll
-      for (int e = 0; e < nr / 4; ++e) {
-        const int r = c * (nr / 4) + e;
-        rd_piece(ra, rb, s0 + (r >> 3), q0 + (r >> 3), r & 7);
+      for (int j = 0; j < 8; ++j) acc[c][j] = Mm::mma16(xa[q][c], xb[q][j], acc[c][j]);
+      if (rd) {
+        rd_piece(ra, rb, s0, q0, 2 * c);
+        rd_piece(ra, rb, s0, q0, 2 * c + 1);
       }
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        if (lm & (1 << (2 * c + e))) {
-          if (lk == 1) loadA(lst, k, p);
-          if (lk == 2) loadB(lst, k, p);
-          ++p;
-        }
-      }
+      if (lk == 1) loadA(lst, k, c);
+      if (lk == 2) loadB(lst, k, c);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -231,24 +232,20 @@ void gemm_nt_kernel(GemmArgs args) {
   wait_vmcnt<16>();
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < 8; ++r) rd_piece(0, 0, 0, 0, r);
-#pragma unroll
-  for (int r = 0; r < 8; ++r) rd_piece(0, 0, 1, 1, r);
+  for (int r = 0; r < 16; ++r) rd_piece(0, 0, 0, 0, r);
 
   // K step t: A ring stage sa = t % 3, B stage sb = t % 2; set s = substep s.
-  // Part A: sets 0..2 with A(t + 2) spread over them (into ring stage
-  // (t + 2) % 3, free since the previous barrier) and the reads of sets 2, 3.
-  // Part B: barrier (A(t + 1), B(t + 1) landed everywhere; this step's reads
-  // done), then set 3 with B(t + 2) into B stage sb and the reads of step
-  // t + 1's sets 0, 1.  The loop starts at a part B.
+  // Part A: set 0 with A(t + 2) (into ring stage (t + 2) % 3, free since the
+  // previous barrier) and the reads of substep 1.  Part B: barrier (A(t + 1)
+  // and B(t + 1) landed everywhere; this step's reads done), then set 1 with
+  // B(t + 2) into B stage sb and the reads of step t + 1's substep 0.  The
+  // loop starts at a part B.
   int sa = 0;
   auto partA = [&](auto sb_tag, auto la_tag, int64_t t) __attribute__((always_inline)) {
     constexpr int sb = decltype(sb_tag)::value;
     constexpr bool LA = decltype(la_tag)::value;
     const int sa2 = sa == 0 ? 2 : sa - 1;
-    mm_ld(0, LA ? 1 : 0, 0x11, sa2, t + 2, 0, 8, sa, sb, 2, 2);
-    mm_ld(1, LA ? 1 : 0, 0x25, sa2, t + 2, 2, 8, sa, sb, 3, 3);
-    mm_ld(2, LA ? 1 : 0, 0x45, sa2, t + 2, 5, 0, 0, 0, 0, 0);
+    mm_ld(0, LA ? 1 : 0, sa2, t + 2, true, sa, sb, 1, 1);
   };
   // VM8: A(t + 2) was issued in the part A before, and may stay in flight
   auto partB = [&](auto sb_tag, auto sync_tag, auto vm_tag, auto lb_tag, int64_t t) __attribute__((always_inline)) {
@@ -263,9 +260,9 @@ void gemm_nt_kernel(GemmArgs args) {
       else
         wait_vmcnt<0>();
       __syncthreads();
-      mm_ld(3, LB ? 2 : 0, 0xff, sb, t + 2, 0, 16, sa1, sb ^ 1, 0, 0);
+      mm_ld(1, LB ? 2 : 0, sb, t + 2, true, sa1, sb ^ 1, 0, 0);
     } else {
-      mm_ld(3, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0);
+      mm_ld(1, 0, 0, 0, false, 0, 0, 0, 0);
     }
     sa = sa1;
   };
@@ -289,28 +286,29 @@ void gemm_nt_kernel(GemmArgs args) {
   partA(I1{}, BF{}, kt + 3);
   partB(I1{}, BF{}, BF{}, BF{}, kt + 3);
 
-  // Epilogue, per wave and 32-row block: the fp32 [32][128] block through the
+  // Epilogue, per wave and 16-row block: the fp32 [16][128] block through the
   // wave's own LDS region (pitch 132 floats), then 16-byte row stores.
+  // Accumulator layout: acc[i][j][e] is row 16 i + 4 (l / 16) + e, column
+  // 16 j + l % 16 of the wave's block.
   __syncthreads();
   int el = lane;
   asm volatile("" : "+v"(el));  // keep the epilogue's index math after the loop
   float* ws = reinterpret_cast<float*>(wave < 3 ? &As[wave * (BM * BK)] : Bs0);
-  const int el32 = el & 31, eg = el >> 5;
+  const int e16 = el & 15, eq = el >> 4;
   typedef T T8 __attribute__((ext_vector_type(8)));
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 8; ++i) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 8; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        ws[(8 * (r >> 2) + 4 * eg + (r & 3)) * 132 + 32 * j + el32] = acc[i][j][r];
-    const int64_t row0 = m0 + wm * 128 + 32 * i;
+      for (int e = 0; e < 4; ++e) ws[(4 * eq + e) * 132 + 16 * j + e16] = acc[i][j][e];
+    const int64_t row0 = m0 + wm * 128 + 16 * i;
     if constexpr (EPI == 0) {
-      // c = acc (+ r), one rounding
+      // c = acc (+ r), one rounding; 16 rows x 16 chunks of 8 columns
       T* C = static_cast<T*>(args.c);
       const T* R = static_cast<const T*>(args.r);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
+      for (int q = 0; q < 4; ++q) {
         const int c = q * 64 + el;
         const int rr = c >> 4, ch = c & 15;
         const float4 lo = *reinterpret_cast<const float4*>(&ws[rr * 132 + 8 * ch]);
@@ -331,21 +329,22 @@ void gemm_nt_kernel(GemmArgs args) {
     } else {
       // g, u rounded as the GEMM would store them; z = round(round(silu(g)) u)
       // (the SwiGLU kernel's rounding points); z also into a feature-major
-      // tile (pitch 40) for the transposed store
+      // tile (pitch 24) for the transposed store.  Columns 32 jp + 8 h of the
+      // staged block are gate features 16 jp + 8 h, 16 further the up ones.
       T* G = static_cast<T*>(args.c);
       T* U = static_cast<T*>(args.c2);
       T* Z = static_cast<T*>(args.z);
-      T* zs = reinterpret_cast<T*>(ws + 32 * 132);
+      T* zs = reinterpret_cast<T*>(ws + 16 * 132);
       const int64_t fw0 = f0 + wn * 64;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < 2; ++q) {
         const int it = q * 64 + el;
-        const int rr = it >> 3, jg = (it >> 2) & 1, c = it & 3;
-        const float* gp = &ws[rr * 132 + 64 * jg + 8 * c];
+        const int rr = it >> 3, jp = (it >> 1) & 3, h = it & 1;
+        const float* gp = &ws[rr * 132 + 32 * jp + 8 * h];
         const float4 g0 = *reinterpret_cast<const float4*>(gp);
         const float4 g1 = *reinterpret_cast<const float4*>(gp + 4);
-        const float4 u0 = *reinterpret_cast<const float4*>(gp + 32);
-        const float4 u1 = *reinterpret_cast<const float4*>(gp + 36);
+        const float4 u0 = *reinterpret_cast<const float4*>(gp + 16);
+        const float4 u1 = *reinterpret_cast<const float4*>(gp + 20);
         const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
         const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
         T8 go, uo, zo;
@@ -354,22 +353,22 @@ void gemm_nt_kernel(GemmArgs args) {
           go[e] = static_cast<T>(gv[e]);
           uo[e] = static_cast<T>(uv[e]);
           zo[e] = static_cast<T>(round_to<T>(silu_fast(to_f32(go[e]))) * to_f32(uo[e]));
-          zs[(32 * jg + 8 * c + e) * 40 + rr] = zo[e];
+          zs[(16 * jp + 8 * h + e) * 24 + rr] = zo[e];
         }
         const int64_t grow = row0 + rr;
-        const int64_t f = fw0 + 32 * jg + 8 * c;
+        const int64_t f = fw0 + 16 * jp + 8 * h;
         *reinterpret_cast<T8*>(G + grow * args.ldc + f) = go;
         *reinterpret_cast<T8*>(U + grow * args.ldc + f) = uo;
         *reinterpret_cast<T8*>(Z + grow * args.ldz + f) = zo;
       }
       if (args.zt != nullptr) {
         T* ZT = static_cast<T*>(args.zt);
-        // 64 feature rows x 4 chunks of 8 tokens
+        // 64 feature rows x 2 chunks of 8 tokens
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < 2; ++q) {
           const int ch = q * 64 + el;
-          const int fr = ch >> 2, tc = ch & 3;
-          const T8 v = *reinterpret_cast<const T8*>(&zs[fr * 40 + 8 * tc]);
+          const int fr = ch >> 1, tc = ch & 1;
+          const T8 v = *reinterpret_cast<const T8*>(&zs[fr * 24 + 8 * tc]);
           *reinterpret_cast<T8*>(ZT + (fw0 + fr) * args.ldzt + row0 + 8 * tc) = v;
         }
       }
