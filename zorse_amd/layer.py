@@ -96,7 +96,7 @@ class FlatViews:
 
 
 # Which GEMM runs the projections: "hipblaslt" (torch.mm / addmm, the default:
-# at the 7B shapes it is ~10 % faster than the hand-written kernel) or "hip"
+# in the 7B stage it is ~2 % faster than the hand-written kernel) or "hip"
 # (zk_gemm_nt for every product whose shape it takes, torch.mm otherwise).
 _GEMM_BACKENDS = ("hipblaslt", "hip")
 _gemm_backend = os.environ.get("ZORSE_GEMM", "hipblaslt")
@@ -107,9 +107,9 @@ if _gemm_backend not in _GEMM_BACKENDS:
 # gate|up GEMM with the SwiGLU activation in its epilogue (zk_gemm_swiglu on
 # the 256 x 256 pipeline: writes g, u, z and z^T in one pass) wherever that
 # pipeline takes the shape; otherwise the GEMM and a separate SwiGLU pass.
-# Off by default: for the 7B layer the fused kernel takes 636 us against
-# 583 us for hipBLASLt's GEMM plus the SwiGLU pass (rotating operands), and
-# the 8-layer stage runs 0.5 ms/step slower with it.  ZORSE_FUSED_MLP=1 or
+# Off by default: the 8-layer 7B stage runs 0.5-0.9 ms/step slower with it
+# than with hipBLASLt's GEMM plus the SwiGLU pass (its epilogue runs while the
+# CU's MFMAs wait).  ZORSE_FUSED_MLP=1 or
 # set_fused_gate_up(True) turns it on.
 _fused_gate_up = os.environ.get("ZORSE_FUSED_MLP", "0") != "0"
 
