@@ -546,9 +546,10 @@ def main():
                     help="launch only this kernel case --steps times (for rocprofv3 --pmc)")
     ap.add_argument("--default-gemm", action="store_true",
                     help="use hipBLASLt's default solution heuristic instead of the recorded table")
-    ap.add_argument("--gemm", choices=("hipblaslt", "hip"), default="hipblaslt",
-                    help="projection GEMMs of the stage: hipBLASLt (torch.mm / addmm) or the "
-                         "hand-written zk_gemm_nt")
+    ap.add_argument("--gemm", choices=("auto", "hip", "hipblaslt"), default="auto",
+                    help="projection GEMMs of the stage: auto (the hand-written zk_gemm_nt for the "
+                         "forward q|k|v, o and down products, hipBLASLt for the rest), hip "
+                         "(zk_gemm_nt for all) or hipblaslt (torch.mm / addmm for all)")
     ap.add_argument("--fused-mlp", action="store_true",
                     help="gate|up GEMM with the SwiGLU epilogue (zk_gemm_swiglu) in the stage")
     ap.add_argument("--summarize-mfma", metavar="DIR",
@@ -656,11 +657,13 @@ def main():
                    "global_batch": B, "parallelism": "none (1 GPU)",
                    "gate_up_swiglu": ("fused (zk_gemm_swiglu)" if _layer_mod._fused_gate_up
                                       else "GEMM + zk_swiglu_fwd_t"),
-                   "projection_gemms": ("hand-written zk_gemm_nt (zorse_amd/csrc/gemm.hip)"
-                                        if args.gemm == "hip" else
-                                        "hipBLASLt via torch.mm/addmm" + (
+                   "projection_gemms": {
+                       "hip": "hand-written zk_gemm_nt (zorse_amd/csrc/gemm.hip) for all twelve",
+                       "auto": "hand-written zk_gemm_nt for the forward q|k|v, o and down "
+                               "(+residual); hipBLASLt via torch.mm for gate|up and the backward",
+                       "hipblaslt": "hipBLASLt via torch.mm/addmm for all twelve"}[args.gemm] + (
                        " (recorded TunableOp solutions, zorse_amd/tunableop_gfx950.csv)"
-                       if tuned else " (default heuristic)")),
+                       if tuned and args.gemm != "hip" else ""),
                    "stage_tokens_per_s": round(B * S / (ms_step / 1e3), 1),
                    "layer_fwd_bwd_tflops": round(layer_tflops, 1)},
         "roofline": {"bound": a["bound"], "achieved": a["achieved"], "peak": a["peak"],

@@ -183,8 +183,10 @@ def test_layer_ragged_long_sequence(dev, name):
 
 # Layers whose every projection GEMM the hand-written kernels take (tokens,
 # hidden, q|k|v width and FFN multiples of 256), run with the "hip" GEMM
-# backend: the four forward products (gate|up through zk_gemm_swiglu with its
-# SwiGLU epilogue, the others through zk_gemm_nt) and the eight backward ones.
+# backend -- the four forward products (gate|up through zk_gemm_swiglu with its
+# SwiGLU epilogue, the others through zk_gemm_nt) and the eight backward ones
+# -- and with the default "auto" backend (zk_gemm_nt for the forward q|k|v, o
+# and down products).
 HIP_GEMM = {
     "cfg3_fp16_gqa": (CONFIGS["cfg3_fp16_gqa"][0], None, torch.float16, (2, 256)),
     "cfg4_bf16_F1536": (dict(hidden_size=512, num_attention_heads=4, intermediate_size=1536,
@@ -193,12 +195,13 @@ HIP_GEMM = {
 }
 
 
+@pytest.mark.parametrize("mode", ["hip", "auto"])
 @pytest.mark.parametrize("name", list(HIP_GEMM))
-def test_layer_hip_gemm_backend(dev, name, monkeypatch):
+def test_layer_hip_gemm_backend(dev, name, mode, monkeypatch):
     from zorse_amd import kernels as K
     from zorse_amd import layer as LY
     kw, window, dtype, (B, S) = HIP_GEMM[name]
-    print(f"layer {name} (hip GEMM backend)", flush=True)
+    print(f"layer {name} ({mode} GEMM backend)", flush=True)
     calls = []
 
     def counting(real):
@@ -209,8 +212,8 @@ def test_layer_hip_gemm_backend(dev, name, monkeypatch):
 
     monkeypatch.setattr(K, "gemm_nt", counting(K.gemm_nt))
     monkeypatch.setattr(K, "gemm_swiglu", counting(K.gemm_swiglu))
-    prev = LY.set_gemm_backend("hip")
-    prev_fused = LY.set_fused_gate_up(True)
+    prev = LY.set_gemm_backend(mode)
+    prev_fused = LY.set_fused_gate_up(mode == "hip")
     try:
         layer = _layer(kw, dev, param_dtype=dtype, window=window, seed=307)
         g = torch.Generator().manual_seed(29)
@@ -220,7 +223,10 @@ def test_layer_hip_gemm_backend(dev, name, monkeypatch):
     finally:
         LY.set_gemm_backend(prev)
         LY.set_fused_gate_up(prev_fused)
-    assert len(calls) == 12 and sum(c[0] == "gemm_swiglu" for c in calls) == 1, calls
+    if mode == "hip":
+        assert len(calls) == 12 and sum(c[0] == "gemm_swiglu" for c in calls) == 1, calls
+    else:  # the forward q|k|v, o and down products
+        assert [c[0] for c in calls] == ["gemm_nt"] * 3, calls
 
 
 def test_cfg1_head_and_cross_entropy_loss(dev):

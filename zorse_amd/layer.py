@@ -95,11 +95,17 @@ class FlatViews:
         self.ln2 = flat[o["ln2"][0]:o["ln2"][1]]
 
 
-# Which GEMM runs the projections: "hipblaslt" (torch.mm / addmm, the default:
-# in the 7B stage it is ~2 % faster than the hand-written kernel) or "hip"
-# (zk_gemm_nt for every product whose shape it takes, torch.mm otherwise).
-_GEMM_BACKENDS = ("hipblaslt", "hip")
-_gemm_backend = os.environ.get("ZORSE_GEMM", "hipblaslt")
+# Which GEMM runs the projections (zk_gemm_nt for the products whose shape it
+# takes, torch.mm / addmm -- hipBLASLt -- for the rest):
+#   "auto" (default): the hand-written kernel for the forward q|k|v, o_proj and
+#       down_proj (with its residual) products, hipBLASLt for gate|up and the
+#       backward -- in the 7B stage each of those three forwards measured equal
+#       on either kernel, each of the others faster on hipBLASLt;
+#   "hip": the hand-written kernel for every product (the stage ~2 % slower);
+#   "hipblaslt": hipBLASLt for every product.
+_GEMM_BACKENDS = ("auto", "hip", "hipblaslt")
+_AUTO_HIP_ROLES = ("qkv", "o", "down")
+_gemm_backend = os.environ.get("ZORSE_GEMM", "auto")
 if _gemm_backend not in _GEMM_BACKENDS:
     raise ValueError(f"ZORSE_GEMM must be one of {_GEMM_BACKENDS}, got {_gemm_backend!r}")
 
@@ -122,7 +128,8 @@ def set_fused_gate_up(enable: bool) -> bool:
 
 
 def set_gemm_backend(name: str) -> str:
-    """Select the projection GEMM ("hipblaslt" or "hip"); returns the previous one."""
+    """Select the projection GEMMs ("auto", "hip" or "hipblaslt"); returns the
+    previous setting."""
     global _gemm_backend
     if name not in _GEMM_BACKENDS:
         raise ValueError(f"GEMM backend must be one of {_GEMM_BACKENDS}, got {name!r}")
@@ -134,11 +141,15 @@ def gemm_backend() -> str:
     return _gemm_backend
 
 
-def _hip_nt(a, b_rows, residual=None, out=None):
-    """a @ b_rows^T (+ residual) through zk_gemm_nt when the "hip" backend is
-    selected and the kernel takes the shape and layout (2-byte dtype, both
-    operands contiguous along the reduction); None otherwise."""
-    if _gemm_backend != "hip" or a.dtype not in (torch.bfloat16, torch.float16):
+def _hip_nt(a, b_rows, residual=None, out=None, role="bwd"):
+    """a @ b_rows^T (+ residual) through zk_gemm_nt when the backend gives it
+    this product (``role``: "qkv", "o", "gu", "down" for the forward
+    projections, "bwd" for the backward's) and the kernel takes the shape and
+    layout (2-byte dtype, both operands contiguous along the reduction); None
+    otherwise."""
+    if _gemm_backend == "hipblaslt" or (_gemm_backend == "auto" and role not in _AUTO_HIP_ROLES):
+        return None
+    if a.dtype not in (torch.bfloat16, torch.float16):
         return None
     if a.stride(1) != 1 or b_rows.stride(1) != 1:
         return None
@@ -147,17 +158,17 @@ def _hip_nt(a, b_rows, residual=None, out=None):
     return K.gemm_nt(a, b_rows, residual=residual, out=out)
 
 
-def _mm(a, b, out=None):
-    """a @ b for the forward projections, b = W^T (a transposed view)."""
-    got = _hip_nt(a, b.t(), out=out)
+def _mm(a, b, role, out=None):
+    """a @ b for the forward projection ``role``, b = W^T (a transposed view)."""
+    got = _hip_nt(a, b.t(), out=out, role=role)
     if got is not None:
         return got
     return torch.mm(a, b) if out is None else torch.mm(a, b, out=out)
 
 
-def _addmm(r, a, b):
+def _addmm(r, a, b, role):
     """r + a @ b with one rounding (the down projection with the residual)."""
-    got = _hip_nt(a, b.t(), residual=r)
+    got = _hip_nt(a, b.t(), residual=r, role=role)
     if got is not None:
         return got
     return torch.addmm(r, a, b)
@@ -249,7 +260,7 @@ def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=Non
     d, Hq, Hkv = spec.head_dim, spec.heads, spec.kv_heads
     x2 = x.reshape(T, h)
     n1, rstd1, _ = K.rmsnorm_fwd(x2, w.ln1, spec.eps)
-    qkv = _mm(n1, w.qkv.t())                         # [T, (Hq + 2 Hkv) d]
+    qkv = _mm(n1, w.qkv.t(), "qkv")                  # [T, (Hq + 2 Hkv) d]
     q = qkv[:, :spec.q_dim].view(B, S, Hq, d)
     k = qkv[:, spec.q_dim:spec.q_dim + spec.kv_dim].view(B, S, Hkv, d)
     v = qkv[:, spec.q_dim + spec.kv_dim:].view(B, S, Hkv, d)
@@ -270,7 +281,7 @@ def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=Non
     o2 = o.view(T, spec.q_dim)
     # o_proj, then residual add fused into the second RMSNorm (one pass writes
     # hdn = x + round(o_proj) and its normalisation, the reference's order)
-    attn_out = _mm(o2, w.o.t())
+    attn_out = _mm(o2, w.o.t(), "o")
     n2, rstd2, hdn = K.rmsnorm_fwd(attn_out, w.ln2, spec.eps, residual=x2)
     F = spec.ffn
     if (_fused_gate_up and n2.dtype in (torch.bfloat16, torch.float16)
@@ -282,14 +293,14 @@ def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=Non
         gu, z = res[0], res[1]
         zs = res[2] if want_t else z
     else:
-        gu = _mm(n2, w.gu.t())                       # [T, 2F] = gate | up
+        gu = _mm(n2, w.gu.t(), "gu")                 # [T, 2F] = gate | up
         if _swiglu_transposed(gu, F):
             # z^T is what down_proj's weight gradient reads; z itself is only
             # needed for the GEMM below
             z, zs = K.swiglu_fwd_t(gu[:, :F], gu[:, F:])
         else:
             z = zs = K.swiglu_fwd(gu[:, :F], gu[:, F:])
-    out = _addmm(hdn, z, w.down.t())                 # residual + down(z)
+    out = _addmm(hdn, z, w.down.t(), "down")         # residual + down(z)
     del z
     saved = (x2, n1, rstd1, qkv, o2, o2t, lse, hdn, n2, rstd2, gu, zs, positions)
     return out.view(B, S, h), saved
