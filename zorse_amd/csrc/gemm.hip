@@ -329,13 +329,13 @@ void gemm_nt_kernel(GemmArgs args) {
     } else {
       // g, u rounded as the GEMM would store them; z = round(round(silu(g)) u)
       // (the SwiGLU kernel's rounding points); z also into a feature-major
-      // tile (pitch 24) for the transposed store.  Columns 32 jp + 8 h of the
+      // tile of the wave's 128 tokens (pitch 136), stored transposed after
+      // the last block in whole 256-byte rows.  Columns 32 jp + 8 h of the
       // staged block are gate features 16 jp + 8 h, 16 further the up ones.
       T* G = static_cast<T*>(args.c);
       T* U = static_cast<T*>(args.c2);
       T* Z = static_cast<T*>(args.z);
       T* zs = reinterpret_cast<T*>(ws + 16 * 132);
-      const int64_t fw0 = f0 + wn * 64;
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const int it = q * 64 + el;
@@ -353,24 +353,28 @@ void gemm_nt_kernel(GemmArgs args) {
           go[e] = static_cast<T>(gv[e]);
           uo[e] = static_cast<T>(uv[e]);
           zo[e] = static_cast<T>(round_to<T>(silu_fast(to_f32(go[e]))) * to_f32(uo[e]));
-          zs[(16 * jp + 8 * h + e) * 24 + rr] = zo[e];
+          zs[(16 * jp + 8 * h + e) * 136 + 16 * i + rr] = zo[e];
         }
         const int64_t grow = row0 + rr;
-        const int64_t f = fw0 + 16 * jp + 8 * h;
+        const int64_t f = f0 + wn * 64 + 16 * jp + 8 * h;
         *reinterpret_cast<T8*>(G + grow * args.ldc + f) = go;
         *reinterpret_cast<T8*>(U + grow * args.ldc + f) = uo;
         *reinterpret_cast<T8*>(Z + grow * args.ldz + f) = zo;
       }
-      if (args.zt != nullptr) {
-        T* ZT = static_cast<T*>(args.zt);
-        // 64 feature rows x 2 chunks of 8 tokens
+    }
+  }
+  if constexpr (EPI == 1) {
+    if (args.zt != nullptr) {
+      // 64 feature rows x 16 chunks of 8 tokens (the wave's 128 tokens)
+      T* ZT = static_cast<T*>(args.zt);
+      const T* zs = reinterpret_cast<const T*>(ws + 16 * 132);
+      const int64_t fw0 = f0 + wn * 64, t0 = m0 + wm * 128;
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const int ch = q * 64 + el;
-          const int fr = ch >> 1, tc = ch & 1;
-          const T8 v = *reinterpret_cast<const T8*>(&zs[fr * 24 + 8 * tc]);
-          *reinterpret_cast<T8*>(ZT + (fw0 + fr) * args.ldzt + row0 + 8 * tc) = v;
-        }
+      for (int q = 0; q < 16; ++q) {
+        const int ch = q * 64 + el;
+        const int fr = ch >> 4, tc = ch & 15;
+        const T8 v = *reinterpret_cast<const T8*>(&zs[fr * 136 + 8 * tc]);
+        *reinterpret_cast<T8*>(ZT + (fw0 + fr) * args.ldzt + t0 + 8 * tc) = v;
       }
     }
   }
