@@ -550,8 +550,9 @@ def main():
                     help="projection GEMMs of the stage: auto (the hand-written zk_gemm_nt for the "
                          "forward q|k|v, o and down products, hipBLASLt for the rest), hip "
                          "(zk_gemm_nt for all) or hipblaslt (torch.mm / addmm for all)")
-    ap.add_argument("--fused-mlp", action="store_true",
-                    help="gate|up GEMM with the SwiGLU epilogue (zk_gemm_swiglu) in the stage")
+    ap.add_argument("--fused-mlp", choices=("on", "off"), default="on",
+                    help="gate|up GEMM with the SwiGLU epilogue (zk_gemm_swiglu) in the stage "
+                         "(with --gemm auto / hip)")
     ap.add_argument("--summarize-mfma", metavar="DIR",
                     help="print the MFMA-counter summary of rocprofv3 runs under DIR and exit")
     ap.add_argument("--summarize-traffic", metavar="DIR",
@@ -587,8 +588,7 @@ def main():
     tuned = use_tuned_gemms(not args.default_gemm)
     from zorse_amd import layer as _layer_mod
     _layer_mod.set_gemm_backend(args.gemm)
-    if args.fused_mlp:
-        _layer_mod.set_fused_gate_up(True)
+    _layer_mod.set_fused_gate_up(args.fused_mlp == "on")
 
     S, B = args.seq, 1
     if args.kernel:
@@ -655,12 +655,14 @@ def main():
                    "layers": args.layers, "hidden": spec.hidden, "heads": spec.heads,
                    "head_dim": spec.head_dim, "ffn": spec.ffn, "micro_batch": B, "seq_len": S,
                    "global_batch": B, "parallelism": "none (1 GPU)",
-                   "gate_up_swiglu": ("fused (zk_gemm_swiglu)" if _layer_mod._fused_gate_up
+                   "gate_up_swiglu": ("fused (zk_gemm_swiglu)"
+                                      if _layer_mod._fused_gate_up and args.gemm != "hipblaslt"
                                       else "GEMM + zk_swiglu_fwd_t"),
                    "projection_gemms": {
                        "hip": "hand-written zk_gemm_nt (zorse_amd/csrc/gemm.hip) for all twelve",
-                       "auto": "hand-written zk_gemm_nt for the forward q|k|v, o and down "
-                               "(+residual); hipBLASLt via torch.mm for gate|up and the backward",
+                       "auto": "hand-written for the forward products (zk_gemm_nt: q|k|v, o, "
+                               "down + residual; zk_gemm_swiglu: gate|up + SwiGLU when "
+                               "--fused-mlp on); hipBLASLt via torch.mm for the backward",
                        "hipblaslt": "hipBLASLt via torch.mm/addmm for all twelve"}[args.gemm] + (
                        " (recorded TunableOp solutions, zorse_amd/tunableop_gfx950.csv)"
                        if tuned and args.gemm != "hip" else ""),

@@ -185,8 +185,7 @@ def test_layer_ragged_long_sequence(dev, name):
 # hidden, q|k|v width and FFN multiples of 256), run with the "hip" GEMM
 # backend -- the four forward products (gate|up through zk_gemm_swiglu with its
 # SwiGLU epilogue, the others through zk_gemm_nt) and the eight backward ones
-# -- and with the default "auto" backend (zk_gemm_nt for the forward q|k|v, o
-# and down products).
+# -- and with the default "auto" backend (the four forward products).
 HIP_GEMM = {
     "cfg3_fp16_gqa": (CONFIGS["cfg3_fp16_gqa"][0], None, torch.float16, (2, 256)),
     "cfg4_bf16_F1536": (dict(hidden_size=512, num_attention_heads=4, intermediate_size=1536,
@@ -213,7 +212,7 @@ def test_layer_hip_gemm_backend(dev, name, mode, monkeypatch):
     monkeypatch.setattr(K, "gemm_nt", counting(K.gemm_nt))
     monkeypatch.setattr(K, "gemm_swiglu", counting(K.gemm_swiglu))
     prev = LY.set_gemm_backend(mode)
-    prev_fused = LY.set_fused_gate_up(mode == "hip")
+    prev_fused = LY.set_fused_gate_up(True)
     try:
         layer = _layer(kw, dev, param_dtype=dtype, window=window, seed=307)
         g = torch.Generator().manual_seed(29)
@@ -225,8 +224,8 @@ def test_layer_hip_gemm_backend(dev, name, mode, monkeypatch):
         LY.set_fused_gate_up(prev_fused)
     if mode == "hip":
         assert len(calls) == 12 and sum(c[0] == "gemm_swiglu" for c in calls) == 1, calls
-    else:  # the forward q|k|v, o and down products
-        assert [c[0] for c in calls] == ["gemm_nt"] * 3, calls
+    else:  # the forward products: q|k|v, o, gate|up (fused with the SwiGLU), down
+        assert [c[0] for c in calls] == ["gemm_nt", "gemm_nt", "gemm_swiglu", "gemm_nt"], calls
 
 
 def test_cfg1_head_and_cross_entropy_loss(dev):

@@ -102,9 +102,11 @@ struct TileDma {
     lane_off8 = static_cast<uint32_t>((row & 7) * ld * static_cast<int64_t>(sizeof(T)) + c * 16);
     wave_el = __builtin_amdgcn_readfirstlane(tid >> 6) * 64 * 8;
   }
-  // piece i: this wave's 8 tile rows (32 i + 8 w ..) from 8 source rows at src
-  __device__ __forceinline__ void issue_wave_rows(T* tile, const T* src, int i) const {
-    dma16(rsrc_words(src), lane_off8, 0, lds_addr(tile + wave_el) + i * NT * 16);
+  // piece i: this wave's 8 tile rows (32 i + 8 w ..) from the 8 source rows
+  // at src + soff bytes (src wave-uniform)
+  __device__ __forceinline__ void issue_wave_rows(T* tile, const T* src, uint32_t soff,
+                                                  int i) const {
+    dma16(rsrc_words(src), lane_off8, soff, lds_addr(tile + wave_el) + i * NT * 16);
   }
   // piece i (rows 32 i .. 32 i + 31) of the tile whose first row is `gbase`
   __device__ __forceinline__ void issue(T* tile, const T* gbase, int64_t ld, int i) const {
@@ -157,6 +159,11 @@ void gemm_nt_kernel(GemmArgs args) {
   // (jj even) or up (jj odd) rows of features f0 + 64 wn + 16 (jj / 2) ..
   // +15, so a lane's MFMA blocks jj and jj + 1 are g and u of one element.
   const int64_t f0 = n0 / 2;
+  // EPI 1: piece p of wave w holds rows 8 (w % 2) .. +7 of features
+  // f0 + 16 p .. +15, gate rows for waves 0, 1 and up rows for waves 2, 3
+  // (row block 2 p + w / 2); the wave's first source row, kept scalar
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const T* bwave = static_cast<const T*>((wv >> 1) ? args.b2 : args.b) + (f0 + 8 * (wv & 1)) * ldb;
 
   TileDma<T> adma, bdma;
   adma.init(lda);
@@ -191,12 +198,8 @@ void gemm_nt_kernel(GemmArgs args) {
     if constexpr (EPI == 0) {
       bdma.issue(Bs(sb), Bb + k * BK, ldb, p);
     } else {
-      // this wave's rows 32 p + 8 w .. +7 lie in row block 2 p + w / 2
-      const int bk = 2 * p + (wave >> 1);
-      const int jj = bk & 7;
-      const T* w = static_cast<const T*>(jj & 1 ? args.b2 : args.b);
-      const int64_t frow = f0 + (bk >> 3) * 64 + (jj >> 1) * 16 + 8 * (wave & 1);
-      bdma.issue_wave_rows(Bs(sb), w + frow * ldb + k * BK, p);
+      bdma.issue_wave_rows(Bs(sb), bwave + k * BK,
+                           static_cast<uint32_t>(16 * p * ldb * static_cast<int64_t>(sizeof(T))), p);
     }
   };
   // The 64 MFMAs of set q in rows of eight.  After row c: one load (LK 1: A

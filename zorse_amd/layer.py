@@ -98,11 +98,12 @@ class FlatViews:
 # Which GEMM runs the projections (zk_gemm_nt for the products whose shape it
 # takes, torch.mm / addmm -- hipBLASLt -- for the rest):
 #   "auto" (default): the hand-written kernel for the forward q|k|v, o_proj and
-#       down_proj (with its residual) products, hipBLASLt for gate|up and the
-#       backward -- in the 7B stage each of those three forwards measured equal
-#       on either kernel, each of the others faster on hipBLASLt;
+#       down_proj (with its residual) products -- and gate|up, through the
+#       fused SwiGLU GEMM below -- hipBLASLt for the backward: in the 7B stage
+#       each of those forwards measured equal on either kernel, each backward
+#       product faster on hipBLASLt;
 #   "hip": the hand-written kernel for every product (the stage ~2 % slower);
-#   "hipblaslt": hipBLASLt for every product.
+#   "hipblaslt": hipBLASLt for every product (and a separate SwiGLU pass).
 _GEMM_BACKENDS = ("auto", "hip", "hipblaslt")
 _AUTO_HIP_ROLES = ("qkv", "o", "down")
 _gemm_backend = os.environ.get("ZORSE_GEMM", "auto")
@@ -112,12 +113,12 @@ if _gemm_backend not in _GEMM_BACKENDS:
 
 # gate|up GEMM with the SwiGLU activation in its epilogue (zk_gemm_swiglu on
 # the 256 x 256 pipeline: writes g, u, z and z^T in one pass) wherever that
-# pipeline takes the shape; otherwise the GEMM and a separate SwiGLU pass.
-# Off by default: the 8-layer 7B stage runs 0.5-0.9 ms/step slower with it
-# than with hipBLASLt's GEMM plus the SwiGLU pass (its epilogue runs while the
-# CU's MFMAs wait).  ZORSE_FUSED_MLP=1 or
-# set_fused_gate_up(True) turns it on.
-_fused_gate_up = os.environ.get("ZORSE_FUSED_MLP", "0") != "0"
+# pipeline takes the shape, with the "auto" and "hip" GEMM backends; otherwise
+# the GEMM and a separate SwiGLU pass.  On by default: in the 7B stage it
+# measured equal to hipBLASLt's GEMM plus the SwiGLU pass (43.28 / 43.30
+# against 43.25 / 43.26 ms/step); ZORSE_FUSED_MLP=0 or set_fused_gate_up(False)
+# turns it off.
+_fused_gate_up = os.environ.get("ZORSE_FUSED_MLP", "1") != "0"
 
 
 def set_fused_gate_up(enable: bool) -> bool:
@@ -284,8 +285,8 @@ def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=Non
     attn_out = _mm(o2, w.o.t(), "o")
     n2, rstd2, hdn = K.rmsnorm_fwd(attn_out, w.ln2, spec.eps, residual=x2)
     F = spec.ffn
-    if (_fused_gate_up and n2.dtype in (torch.bfloat16, torch.float16)
-            and K.gemm_nt_supported(T, 2 * F, h)):
+    if (_fused_gate_up and _gemm_backend != "hipblaslt"
+            and n2.dtype in (torch.bfloat16, torch.float16) and K.gemm_nt_supported(T, 2 * F, h)):
         # one GEMM writes gate | up (kept for the backward), z and, when the
         # down projection's weight gradient takes the transposed form, z^T
         want_t = _transposing(n2) and F % 8 == 0
