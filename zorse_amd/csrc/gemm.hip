@@ -448,8 +448,8 @@ namespace zk {
 
 // The gate|up projection with the SwiGLU epilogue on the 256 x 256 pipeline
 // (zk_gemm_swiglu routes the shapes it takes here: M a multiple of 256, F of
-// 128, K of 128 and at least 256).  Arguments as zk_gemm_swiglu, already
-// validated.
+// 128, K of 128 and at least 256, ld_x and ld_w below 2^22).  Arguments as
+// zk_gemm_swiglu, already validated.
 int zk_gemm_swiglu_tiled_supported(int64_t M, int64_t F, int64_t K) {
   return zk_gemm_nt_supported(M, 2 * F, K);
 }
@@ -458,8 +458,6 @@ int zk_gemm_swiglu_tiled(const void* x, int64_t ld_x, const void* w_gate, const 
                          int64_t ld_w, void* g_out, void* u_out, int64_t ld_gu, void* z,
                          int64_t ld_z, void* zt, int64_t ld_zt, int64_t M, int64_t F, int64_t K,
                          int dtype, zk_stream_t stream) {
-  ZK_REQUIRE(ld_x < (int64_t(1) << 22) && ld_w < (int64_t(1) << 22), ZK_EUNSUPPORTED,
-             "zk_gemm_swiglu: leading dimension out of range");
   gemm::GemmArgs ga{};
   ga.a = x;
   ga.lda = ld_x;

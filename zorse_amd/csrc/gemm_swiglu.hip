@@ -214,7 +214,8 @@ extern "C" int zk_gemm_swiglu(const void* x, int64_t ld_x, const void* w_gate,
   // the tile loaders keep a 32-row span of one operand in a 32-bit byte offset
   ZK_REQUIRE(ld_x < (int64_t(1) << 26) && ld_w < (int64_t(1) << 26), ZK_EUNSUPPORTED,
              "zk_gemm_swiglu: leading dimension out of range");
-  if (zk_gemm_swiglu_tiled_supported(M, F, K))
+  if (zk_gemm_swiglu_tiled_supported(M, F, K) && ld_x < (int64_t(1) << 22) &&
+      ld_w < (int64_t(1) << 22))
     return zk_gemm_swiglu_tiled(x, ld_x, w_gate, w_up, ld_w, g_out, u_out, ld_gu, z, ld_z, zt,
                                 ld_zt, M, F, K, dtype, stream);
   const int64_t n_wg = ((M + C::BM - 1) / C::BM) * ((F + C::BF - 1) / C::BF);
