@@ -163,7 +163,9 @@ void gemm_nt_kernel(GemmArgs args) {
   // f0 + 16 p .. +15, gate rows for waves 0, 1 and up rows for waves 2, 3
   // (row block 2 p + w / 2); the wave's first source row, kept scalar
   const int wv = __builtin_amdgcn_readfirstlane(wave);
-  const T* bwave = static_cast<const T*>((wv >> 1) ? args.b2 : args.b) + (f0 + 8 * (wv & 1)) * ldb;
+  const T* bwave = EPI == 1 ? static_cast<const T*>((wv >> 1) ? args.b2 : args.b) +
+                                  (f0 + 8 * (wv & 1)) * ldb
+                            : B;
 
   TileDma<T> adma, bdma;
   adma.init(lda);
