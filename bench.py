@@ -97,7 +97,8 @@ class KernelCases:
     1 GiB), the calibration for the FETCH_SIZE / WRITE_SIZE counters."""
 
     NAMES = ("attn_fwd", "attn_bwd", "rmsnorm_fwd", "rmsnorm_bwd", "adamw", "adamw_t", "copy",
-             "gemm_gu", "gemm_wgrad_gu", "gemm_nt_gu", "gemm_nt_wgrad_gu", "rope")
+             "gemm_gu", "gemm_dgrad_gu", "gemm_wgrad_gu", "blas_gu", "blas_dgrad_gu",
+             "blas_wgrad_gu", "rope")
 
     def __init__(self, dev, spec, S):
         self.dev, self.spec, self.S = dev, spec, S
@@ -199,26 +200,34 @@ class KernelCases:
                 K.rope_(qkv[:, :H * d].view(B, S, H, d), qkv[:, H * d:2 * H * d].view(B, S, H, d),
                         cos, sin)
             return run, 2 * 2 * T * H * d * 2
-        if name in ("gemm_gu", "gemm_wgrad_gu", "gemm_nt_gu", "gemm_nt_wgrad_gu"):
-            # the layer's largest projection GEMM as the stage runs it (hipBLASLt
-            # through torch.mm with the recorded solutions; gemm_nt_*: the
-            # hand-written zk_gemm_nt on the same operands): forward gate|up =
-            # n2 [T, h] x W_gu^T, and its weight gradient dgu^T [2F, T] x n2^T^T
+        if name in ("gemm_gu", "gemm_dgrad_gu", "gemm_wgrad_gu", "blas_gu", "blas_dgrad_gu",
+                    "blas_wgrad_gu"):
+            # the layer's largest projection GEMM, its three products on the
+            # operands as the layer holds them: forward gate|up = n2 W_gu^T,
+            # input gradient dn2 = dgu W_gu, weight gradient dgu^T n2.  gemm_*:
+            # the hand-written zk_gemm the stage runs; blas_*: hipBLASLt through
+            # torch.mm on the same operands, a reference point only
             F2 = 2 * spec.ffn
-            hand = name.startswith("gemm_nt")
+            hand = name.startswith("gemm_")
             a = torch.randn(T, h, device=dev, dtype=torch.bfloat16)
-            if name in ("gemm_gu", "gemm_nt_gu"):
-                w = 0.02 * torch.randn(F2, h, device=dev, dtype=torch.bfloat16)
-                y = torch.empty(T, F2, device=dev, dtype=torch.bfloat16)
+            w = 0.02 * torch.randn(F2, h, device=dev, dtype=torch.bfloat16)
+            work = 2 * T * h * F2
+            if name.endswith("_dgrad_gu"):
+                dy = torch.randn(T, F2, device=dev, dtype=torch.bfloat16)
+                y = torch.empty(T, h, device=dev, dtype=torch.bfloat16)
                 if hand:
-                    return (lambda: K.gemm_nt(a, w, out=y)), 2 * T * h * F2
-                return (lambda: torch.mm(a, w.t(), out=y)), 2 * T * h * F2
-            dyt = torch.randn(F2, T, device=dev, dtype=torch.bfloat16)
-            at = a.t().contiguous()
-            dw = torch.empty(F2, h, device=dev, dtype=torch.bfloat16)
+                    return (lambda: K.gemm(dy, w, b_kmajor=True, out=y)), work
+                return (lambda: torch.mm(dy, w, out=y)), work
+            if name.endswith("_wgrad_gu"):
+                dy = torch.randn(T, F2, device=dev, dtype=torch.bfloat16)
+                dw = torch.empty(F2, h, device=dev, dtype=torch.bfloat16)
+                if hand:
+                    return (lambda: K.gemm(dy, a, a_kmajor=True, b_kmajor=True, out=dw)), work
+                return (lambda: torch.mm(dy.t(), a, out=dw)), work
+            y = torch.empty(T, F2, device=dev, dtype=torch.bfloat16)
             if hand:
-                return (lambda: K.gemm_nt(dyt, at, out=dw)), 2 * T * h * F2
-            return (lambda: torch.mm(dyt, at.t(), out=dw)), 2 * T * h * F2
+                return (lambda: K.gemm(a, w, out=y)), work
+            return (lambda: torch.mm(a, w.t(), out=y)), work
         if name == "copy":
             src = torch.empty(1 << 28, device=dev, dtype=torch.float32).normal_()
             dst = torch.empty_like(src)
@@ -241,10 +250,17 @@ def measure_kernels(dev, spec, S):
         "adamw_t": ("adamw_tile_t<bf16,bf16> (layer step with W^T copies)", "hbm", 10),
         "rope": ("rope_pos_kernel<bf16,128,half> (q and k of the q|k|v buffer)", "hbm", 20),
         "copy": ("device copy 1 GiB (HBM reference)", "hbm", 5),
-        "gemm_gu": ("hipBLASLt gate|up GEMM 4096 x 22016 x 4096 (reference point)", "mfma", 10),
-        "gemm_wgrad_gu": ("hipBLASLt gate|up weight-gradient GEMM (reference point)", "mfma", 10),
-        "gemm_nt_gu": ("zk_gemm_nt gate|up GEMM 4096 x 22016 x 4096 (hand-written)", "mfma", 10),
-        "gemm_nt_wgrad_gu": ("zk_gemm_nt gate|up weight-gradient GEMM (hand-written)", "mfma", 10),
+        "gemm_gu": ("gemm_tiled_kernel<bf16,0,false,false> gate|up fwd 4096 x 22016 x 4096",
+                    "mfma", 10),
+        "gemm_dgrad_gu": ("gemm_tiled_kernel<bf16,0,false,true> gate|up input grad "
+                          "4096 x 4096 x 22016", "mfma", 10),
+        "gemm_wgrad_gu": ("gemm_tiled_kernel<bf16,0,true,true> gate|up weight grad "
+                          "22016 x 4096 x 4096", "mfma", 10),
+        "blas_gu": ("hipBLASLt gate|up fwd, same operands (reference point)", "mfma", 10),
+        "blas_dgrad_gu": ("hipBLASLt gate|up input grad, same operands (reference point)",
+                          "mfma", 10),
+        "blas_wgrad_gu": ("hipBLASLt gate|up weight grad, same operands (reference point)",
+                          "mfma", 10),
     }
     for name, (kname, bound, iters) in spec_of.items():
         run, work = cases.make(name)
@@ -345,14 +361,14 @@ def summarize_stage(root: str, layers: int, steps: int, warmup: int) -> str:
     t0, t1 = int(adam[first]["End_Timestamp"]), int(adam[last]["End_Timestamp"])
     win = [r for r in trace
            if int(r["Start_Timestamp"]) >= t0 and int(r["End_Timestamp"]) <= t1]
-    groups = [("hipBLASLt GEMMs", ("Cijk",)),
-              ("hand-written GEMMs (zk_gemm_nt / zk_gemm_swiglu)",
-               ("gemm_nt_kernel", "gemm_swiglu_kernel")),
+    groups = [("library GEMMs (hipBLASLt)", ("Cijk",)),
+              ("hand-written GEMMs (zk_gemm / zk_gemm_swiglu)",
+               ("gemm_tiled_kernel", "gemm_gen_kernel", "gemm_swiglu_kernel")),
               ("attention bwd: dq, dkdv", ("attn_bwd",)),
               ("AdamW (optimizer stream, overlapped)", ("adamw",)),
               ("attention fwd", ("attn_fwd",)),
-              ("SwiGLU (with transposed outputs)", ("swiglu",)),
-              ("transposes (backward operands, optimizer W^T copies)", ("transpose",)),
+              ("SwiGLU bwd", ("swiglu",)),
+              ("transposes", ("transpose",)),
               ("RMSNorm fwd / bwd", ("rmsnorm",)), ("RoPE fwd / bwd", ("rope",)),
               ("device copies", ("copyBuffer",))]
     tot, other = collections.defaultdict(float), 0.0
@@ -408,11 +424,16 @@ def summarize_stage(root: str, layers: int, steps: int, warmup: int) -> str:
     busy += ce - cs
     lines += ["", f"GPU busy over the {steps} timed steps: {busy / steps / 1e6:.2f} ms per step "
                   f"(window {(t1 - t0) / steps / 1e6:.2f} ms per step)."]
+    staged = adam[first + 1:last + 1]
+    avg_in = sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in staged) / len(staged)
+    lines.append(f"`adamw_elem` in the stage (beside the attention backward and GEMMs): "
+                 f"{len(staged)} launches, {avg_in / 1e6:.3f} ms on average.")
     rest = adam[last + 1:]
     if rest:
         avg = sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rest) / len(rest)
-        lines.append(f"bench.py's `adamw` case after the stage: {len(rest)} launches of "
-                     f"`adamw_elem`, {avg / 1e6:.3f} ms on average.")
+        lines.append(f"`adamw_elem` alone (bench.py's `adamw` case after the stage): "
+                     f"{len(rest)} launches, {avg / 1e6:.3f} ms on average.  The kernel table "
+                     f"below averages both groups together.")
     lines += ["", "All kernels of the run (rocprofv3 `bench_kernel_stats.csv`, top 30):", "",
               "| kernel | calls | total ms | avg us | % |", "|---|---|---|---|---|"]
     stats = list(csv.DictReader(open(os.path.join(root, "bench_kernel_stats.csv"))))
@@ -453,8 +474,8 @@ def summarize_mfma(root: str) -> str:
     lines = ["| kernel | dispatches | avg duration (us) | clock (GHz) | MFMA FLOPs executed (GF) "
              "| MFMA busy / active cycles | LDS conflict cycles / access cycles |",
              "|---|---|---|---|---|---|---|"]
-    for case in ("attn_fwd", "attn_bwd", "gemm_gu", "gemm_wgrad_gu", "gemm_nt_gu",
-                 "gemm_nt_wgrad_gu"):
+    for case in ("attn_fwd", "attn_bwd", "gemm_gu", "gemm_dgrad_gu", "gemm_wgrad_gu",
+                 "blas_gu", "blas_dgrad_gu", "blas_wgrad_gu"):
         path = os.path.join(root, case, "r_counter_collection.csv")
         if not os.path.exists(path):
             continue
@@ -544,15 +565,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel", choices=KernelCases.NAMES,
                     help="launch only this kernel case --steps times (for rocprofv3 --pmc)")
-    ap.add_argument("--default-gemm", action="store_true",
-                    help="use hipBLASLt's default solution heuristic instead of the recorded table")
-    ap.add_argument("--gemm", choices=("auto", "hip", "hipblaslt"), default="auto",
-                    help="projection GEMMs of the stage: auto (the hand-written zk_gemm_nt for the "
-                         "forward q|k|v, o and down products, hipBLASLt for the rest), hip "
-                         "(zk_gemm_nt for all) or hipblaslt (torch.mm / addmm for all)")
     ap.add_argument("--fused-mlp", choices=("on", "off"), default="on",
-                    help="gate|up GEMM with the SwiGLU epilogue (zk_gemm_swiglu) in the stage "
-                         "(with --gemm auto / hip)")
+                    help="gate|up GEMM with the SwiGLU epilogue (zk_gemm_swiglu) in the stage")
     ap.add_argument("--summarize-mfma", metavar="DIR",
                     help="print the MFMA-counter summary of rocprofv3 runs under DIR and exit")
     ap.add_argument("--summarize-traffic", metavar="DIR",
@@ -582,12 +596,9 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda:0")
     from zorse_amd import flops
-    from zorse_amd.gemm_tuning import use_tuned_gemms
+    from zorse_amd import layer as _layer_mod
     from zorse_amd.stage import StageRunner
 
-    tuned = use_tuned_gemms(not args.default_gemm)
-    from zorse_amd import layer as _layer_mod
-    _layer_mod.set_gemm_backend(args.gemm)
     _layer_mod.set_fused_gate_up(args.fused_mlp == "on")
 
     S, B = args.seq, 1
@@ -627,12 +638,8 @@ def main():
     kern = measure_kernels(dev, spec, S)
     print("kernel timings done", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline(spec, S)
-    # the dominant hand-written kernel of the step (by time): the flat AdamW
-    # kernel alone, one launch over a layer's shard as the stage makes it.  The
-    # stage's optimizer step then also transposes the four projection matrices
-    # out of the kernel's compute copy (zk_transpose, ~0.8 GB more per layer
-    # step), which this figure leaves out (bench.py's adamw_t case measures
-    # the one-launch form that includes those copies).
+    # the roofline line: the flat AdamW kernel, one launch over a layer's shard
+    # exactly as the stage's optimizer step makes it
     a = kern["adamw"]
     af, ab = kern["attn_fwd"], kern["attn_bwd"]
     line = {
@@ -655,17 +662,10 @@ def main():
                    "layers": args.layers, "hidden": spec.hidden, "heads": spec.heads,
                    "head_dim": spec.head_dim, "ffn": spec.ffn, "micro_batch": B, "seq_len": S,
                    "global_batch": B, "parallelism": "none (1 GPU)",
-                   "gate_up_swiglu": ("fused (zk_gemm_swiglu)"
-                                      if _layer_mod._fused_gate_up and args.gemm != "hipblaslt"
-                                      else "GEMM + zk_swiglu_fwd_t"),
-                   "projection_gemms": {
-                       "hip": "hand-written zk_gemm_nt (zorse_amd/csrc/gemm.hip) for all twelve",
-                       "auto": "hand-written for the forward products (zk_gemm_nt: q|k|v, o, "
-                               "down + residual; zk_gemm_swiglu: gate|up + SwiGLU when "
-                               "--fused-mlp on); hipBLASLt via torch.mm for the backward",
-                       "hipblaslt": "hipBLASLt via torch.mm/addmm for all twelve"}[args.gemm] + (
-                       " (recorded TunableOp solutions, zorse_amd/tunableop_gfx950.csv)"
-                       if tuned and args.gemm != "hip" else ""),
+                   "gate_up_swiglu": ("fused (zk_gemm_swiglu)" if _layer_mod._fused_gate_up
+                                      else "zk_gemm + zk_swiglu_fwd"),
+                   "projection_gemms": "hand-written zk_gemm (zorse_amd/csrc/gemm.hip) for all "
+                                       "twelve products per layer, on untransposed operands",
                    "stage_tokens_per_s": round(B * S / (ms_step / 1e3), 1),
                    "layer_fwd_bwd_tflops": round(layer_tflops, 1)},
         "roofline": {"bound": a["bound"], "achieved": a["achieved"], "peak": a["peak"],
@@ -673,8 +673,9 @@ def main():
                      "traffic": a["traffic"],
                      "kernel": a["kernel"], "avg_ms": a["avg_ms"],
                      "algorithmic_bytes": a["work_per_launch"],
-                     "scope": "the AdamW kernel alone; the stage's four W^T transposes per "
-                              "layer step are not included"},
+                     "scope": "one launch over a layer's flat shard: the stage's whole "
+                              "optimizer step per layer; its 5.7 GB per launch is far larger "
+                              "than the Infinity Cache"},
         "attention_roofline": {
             "fwd": {"kernel": af["kernel"], "achieved": af["achieved"], "peak": af["peak"],
                     "unit": "TFLOP/s", "frac": af["frac"], "avg_ms": af["avg_ms"],

@@ -155,16 +155,40 @@ int zk_gemm_swiglu(const void* x, int64_t ld_x, const void* w_gate,
 
 /* Projection GEMM: replaces the nn.Linear products of the decoder layer's
  * q/k/v/o projections (models/llama_simple.py:206-221, 346, 375) and of the
- * LlamaMLP built at models/llama_simple.py:418, forward and backward, when
- * both operands are contiguous along the reduction:
- *     c[M, N] = a[M, K] b[N, K]^T (+ r[M, N])
- * (the forward x W^T; the backward's input and weight gradients on
- * transposed operands, as the layer arranges them; r, when not NULL, is the
- * residual of a fused add: one fp32 rounding of a b^T + r).  Row strides
- * lda / ldb / ldc / ldr in elements, multiples of 8 and below 2^22; 2-byte
- * dtypes; operands 16-byte aligned; M and N multiples of 256, K a multiple
- * of 128 and at least 256 (ZK_EUNSUPPORTED otherwise:
- * zk_gemm_nt_supported(M, N, K) says in advance). */
+ * LlamaMLP built at models/llama_simple.py:418 -- forward, and the input and
+ * weight gradients autograd forms for them in the backward the profiler
+ * times (utils/runtime_estimator.py:235-243) and the pipeline runs
+ * (zorse_utils/pipeline_schedule_v2.py:171-200):
+ *     c[M, N] = op(a) op(b)^T (+ r[M, N])
+ * a_kmajor == 0: a is [M, K] (row stride lda, contiguous along K);
+ * a_kmajor != 0: a is [K, M] (row stride lda, contiguous along M); likewise
+ * b ([N, K] or [K, N]).  The forward x W^T is (0, 0); the input gradient
+ * dY W is (0, 1) on W as stored; the weight gradient dY^T X is (1, 1) on the
+ * token-major activations as stored.  r, when not NULL, is the residual of a
+ * fused add: one fp32 rounding of the accumulated product plus r.  Any
+ * shape; bf16 / fp16 (fp32 accumulation) or fp32; every tensor shares
+ * `dtype`; pointers aligned to the element size.  Shapes on the 256 x 256
+ * grid of 2-byte types (zk_gemm_path) run the MFMA pipeline, the rest a
+ * masked 128 x 128 kernel. */
+int zk_gemm(const void* a, int64_t lda, int a_kmajor, const void* b, int64_t ldb,
+            int b_kmajor, void* c, int64_t ldc, const void* r, int64_t ldr, int64_t M,
+            int64_t N, int64_t K, int dtype, zk_stream_t stream);
+
+/* Which kernel zk_gemm runs for a launch with 16-byte aligned pointers
+ * (host-only, no GPU call): ZK_GEMM_TILED -- 2-byte type, M and N multiples
+ * of 256, K a multiple of 128 and at least 256, leading dimensions multiples
+ * of 8, and each operand's tile within one buffer resource (lda / ldb below
+ * 2^22 elements for a [rows, K] operand, 2^24 for a K-major one); otherwise
+ * ZK_GEMM_GENERAL.  ldr < 0: no residual. */
+enum zk_gemm_kernel { ZK_GEMM_GENERAL = 0, ZK_GEMM_TILED = 1 };
+int zk_gemm_path(int64_t M, int64_t N, int64_t K, int64_t lda, int a_kmajor, int64_t ldb,
+                 int b_kmajor, int64_t ldc, int64_t ldr, int dtype);
+
+/* zk_gemm with both operands contiguous along the reduction (a [M, K],
+ * b [N, K]): the nn.Linear forward x W^T of the projections above
+ * (models/llama_simple.py:206-221, 418).  zk_gemm_nt_supported(M, N, K)
+ * says whether the shape is on the MFMA pipeline's grid (M, N multiples of
+ * 256, K a multiple of 128 and at least 256); other shapes run too. */
 int zk_gemm_nt_supported(int64_t M, int64_t N, int64_t K);
 int zk_gemm_nt(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
                int64_t ldc, const void* r, int64_t ldr, int64_t M, int64_t N,

@@ -42,10 +42,42 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_error_text(lib):
-    assert lib.zk_abi_version() == 2
+    assert lib.zk_abi_version() == 3
     rc = lib.zk_rmsnorm_fwd(None, None, None, None, None, None, 4, 8, 1e-6, 7, 0, None)
     assert rc == -2  # ZK_EDTYPE
     assert b"dtype" in lib.zk_last_error()
+
+
+def test_gemm_kernel_choice(lib):
+    """zk_gemm_path (host-only): the 256 x 256 MFMA pipeline takes 2-byte
+    shapes on its grid in every layout -- the 7B layer's forward, input- and
+    weight-gradient products -- and leading dimensions whose tiles stay within
+    one buffer resource (2 GiB): 256 rows of a [rows, K] operand (ld < 2^22
+    elements) or 64 rows of a K-major one (ld < 2^24).  Everything else --
+    ragged shapes, fp32, leading dimensions off 8 or past the bound -- runs
+    the masked kernel."""
+    TILED, GEN = 1, 0
+    bf16, f32 = 2, 0
+    path = lib.zk_gemm_path
+    # (M, N, K, lda, a_kmajor, ldb, b_kmajor, ldc, ldr, dtype)
+    assert path(4096, 22016, 4096, 4096, 0, 4096, 0, 22016, -1, bf16) == TILED   # gate|up fwd
+    assert path(4096, 4096, 22016, 22016, 0, 4096, 1, 4096, -1, bf16) == TILED   # its dX
+    assert path(22016, 4096, 4096, 22016, 1, 4096, 1, 4096, -1, bf16) == TILED   # its dW
+    assert path(4096, 4096, 11008, 11008, 0, 11008, 0, 4096, 4096, bf16) == TILED  # down + r
+    assert path(384, 4096, 4096, 4096, 0, 4096, 0, 4096, -1, bf16) == GEN
+    assert path(4096, 4096, 4160, 4160, 0, 4160, 0, 4096, -1, bf16) == GEN
+    assert path(4096, 4096, 4096, 4096, 0, 4096, 0, 4096, -1, f32) == GEN
+    assert path(4096, 4096, 4096, 4100, 0, 4096, 0, 4096, -1, bf16) == GEN
+    assert path(4096, 4096, 4096, 4096, 0, 4096, 0, 4096, 4100, bf16) == GEN
+    # the buffer-resource bound: NT rows below 2^22, K-major rows below 2^24
+    assert path(256, 256, 256, (1 << 22) - 8, 0, 256, 0, 256, -1, bf16) == TILED
+    assert path(256, 256, 256, 1 << 22, 0, 256, 0, 256, -1, bf16) == GEN
+    assert path(256, 256, 256, 256, 0, 1 << 22, 0, 256, -1, bf16) == GEN
+    assert path(256, 256, 256, 1 << 22, 1, 256, 0, 256, -1, bf16) == TILED
+    assert path(256, 256, 256, (1 << 24) - 8, 1, (1 << 24) - 8, 1, 256, -1, bf16) == TILED
+    assert path(256, 256, 256, 1 << 24, 1, 256, 1, 256, -1, bf16) == GEN
+    assert path(256, 256, 256, 256, 1, 1 << 24, 1, 256, -1, bf16) == GEN
+    assert path(256, 256, 256, 256, 0, 256, 0, 256, -1, 9) == -2
 
 
 def test_validation_codes(lib):
@@ -106,16 +138,23 @@ def test_validation_codes(lib):
     assert lib.zk_gemm_swiglu(ctypes.c_void_p(24), 64, p, p, 64, p, p, 8, p, 8, None, 0, 8, 8, 64,
                               2, None) == -3
     assert lib.zk_gemm_swiglu(p, 32, p, p, 64, p, p, 8, p, 8, None, 0, 8, 8, 64, 2, None) == -1
-    # gemm_nt: fp32, M not a multiple of 256, K below 256, misaligned b, ld_a < K,
-    # ld not a multiple of 8; the shape query agrees
-    assert lib.zk_gemm_nt(p, 256, p, 256, p, 256, None, 0, 256, 256, 256, 0, None) == -2
-    assert lib.zk_gemm_nt(p, 256, p, 256, p, 256, None, 0, 300, 256, 256, 2, None) == -4
-    assert lib.zk_gemm_nt(p, 256, p, 256, p, 256, None, 0, 256, 256, 128, 2, None) == -4
-    assert lib.zk_gemm_nt(p, 256, ctypes.c_void_p(24), 256, p, 256, None, 0, 256, 256, 256, 2,
-                          None) == -3
+    # gemm: bad dtype, ld below the operand's row length (a [M, K]: ld >= K; a
+    # K-major [K, M]: ld >= M), null operand, an address not aligned to the
+    # element size; zero-size is a no-op.  Every shape is accepted (shapes off
+    # the MFMA pipeline's grid run the masked kernel), so no valid call is
+    # made here: these return before any HIP call
+    assert lib.zk_gemm_nt(p, 256, p, 256, p, 256, None, 0, 256, 256, 256, 7, None) == -2
     assert lib.zk_gemm_nt(p, 128, p, 256, p, 256, None, 0, 256, 256, 256, 2, None) == -1
-    assert lib.zk_gemm_nt(p, 260, p, 256, p, 256, None, 0, 256, 256, 256, 2, None) == -3
+    assert lib.zk_gemm_nt(p, 256, ctypes.c_void_p(25), 256, p, 256, None, 0, 256, 256, 256, 2,
+                          None) == -3
     assert lib.zk_gemm_nt(None, 0, None, 0, None, 0, None, 0, 0, 0, 0, 2, None) == 0
+    assert lib.zk_gemm(p, 200, 1, p, 256, 1, p, 256, None, 0, 256, 256, 512, 2, None) == -1
+    assert lib.zk_gemm(p, 512, 0, p, 200, 1, p, 256, None, 0, 256, 256, 512, 2, None) == -1
+    assert lib.zk_gemm(p, 512, 0, None, 512, 0, p, 256, None, 0, 256, 256, 512, 2, None) == -1
+    assert lib.zk_gemm(ctypes.c_void_p(18), 512, 0, p, 512, 0, p, 256, None, 0, 256, 256, 512,
+                       0, None) == -3
+    assert lib.zk_gemm(p, 512, 0, p, 512, 0, p, 256, p, 100, 256, 256, 512, 2, None) == -1
+    assert lib.zk_gemm(None, 0, 1, None, 0, 1, None, 0, None, 0, 0, 0, 64, 2, None) == 0
     assert lib.zk_gemm_nt_supported(4096, 22016, 4096) == 1
     assert lib.zk_gemm_nt_supported(4096, 22016, 4160) == 0
     assert lib.zk_gemm_nt_supported(4096, 1376, 4096) == 0

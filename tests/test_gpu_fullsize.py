@@ -147,15 +147,14 @@ def test_stage_full_size_7b(dev):
     them) at seq 4096 through StageRunner with its defaults -- AdamW (lr 1e-4,
     betas 0.9 / 0.95, wd 0.1) on each layer's flat shard inside the backward
     on the optimizer stream, held until the next layer's attention backward
-    is enqueued, and W^T copies written by each step for the next backward's
-    input-gradient GEMMs -- over two steps, so the second backward runs on
-    the optimizer-kept W^T (zorse_utils/pipeline_schedule_v2.py:138-200,
-    utils/patch.py:76-154).  Per step and layer: the gradient the optimizer
-    consumed against the fp32 oracle at the weights that step saw, and
-    against plain PyTorch in bf16 (precision-matched bar).  After the run: the
-    fp32 master equals the oracle's AdamW applied to the captured gradients
-    (fp32 bar), the bf16 weights are the rounded master and the W^T copies
-    are exact transposes."""
+    is enqueued -- over two steps, so the second step runs on the weights
+    the first one's optimizer wrote (zorse_utils/pipeline_schedule_v2.py:
+    138-200, utils/patch.py:76-154).  Per step, layer and each of the nine
+    parameter slices: the gradient the optimizer consumed against the fp32
+    oracle at the weights that step saw, and against plain PyTorch in bf16
+    (precision-matched bar), each slice held to its own scale.  After the
+    run: the fp32 master equals the oracle's AdamW applied to the captured
+    gradients (fp32 bar) and the bf16 weights are the rounded master."""
     _stage_full_size(dev, "cfg4_7b_bf16", seed0=3000)
 
 
@@ -203,9 +202,6 @@ def _stage_full_size(dev, name, seed0):
         runner.step(x, dout)
         runner.wait_optimizer()
         torch.cuda.synchronize()
-        if step == 1:
-            for l in layers:
-                assert l._transposed_weights() is not None
         # fp32 oracle and plain PyTorch in the compute dtype of the two-layer
         # stack at these weights
         refs = {}
@@ -219,9 +215,13 @@ def _stage_full_size(dev, name, seed0):
             refs[ref] = [O.flatten({k: v.grad for k, v in p.items()}) for p in ps]
             del xr, ps, y
             torch.cuda.empty_cache()
+        # each of the nine parameter slices against its own scale
+        offs = s.offsets()
         for i in range(2):
-            _close(captured[i][step], refs["fp32"][i], dtype, f"step {step + 1} layer {i} grad",
-                   refs["lowp"][i])
+            for k in O.PARAM_ORDER:
+                a, b = offs[k]
+                _close(captured[i][step][a:b], refs["fp32"][i][a:b], dtype,
+                       f"step {step + 1} layer {i} d{k}", refs["lowp"][i][a:b])
         del refs
     for i, (l, opt) in enumerate(zip(layers, runner.optimizers)):
         p, m, v = init[i].clone(), torch.zeros_like(init[i]), torch.zeros_like(init[i])
@@ -231,9 +231,3 @@ def _stage_full_size(dev, name, seed0):
         _close(master, p, torch.float32, f"layer {i} master after 2 steps")
         assert torch.equal(l.flat_param.detach(), master.to(dtype))
         assert l.flat_param.grad is None
-        o = s.offsets()
-        for wname, (a, b), cols in (("qkv", (o["q"][0], o["v"][1]), s.hidden),
-                                    ("o", o["o"], s.heads * s.head_dim),
-                                    ("gu", (o["gate"][0], o["up"][1]), s.hidden),
-                                    ("down", o["down"], s.ffn)):
-            assert torch.equal(l._wt[wname], l.flat_param[a:b].view(-1, cols).t()), wname

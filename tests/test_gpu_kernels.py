@@ -153,9 +153,9 @@ def test_gemm_nt(dev, M, N, K, dtype, res):
     _assert_within_ulp(out, ref, dtype, "gemm_nt")
 
 
-def test_gemm_nt_strided_views_and_unsupported(dev):
+def test_gemm_nt_strided_views(dev):
     """Row-strided operand views (the layer's fused weight slices), an output
-    slice of a wider buffer; shapes off the tile grid are rejected."""
+    slice of a wider buffer; a shape off the tile grid runs the masked kernel."""
     from zorse_amd import kernels as K_
     M, N, K = 512, 512, 512
     a = _rand((M, K + 64), torch.bfloat16, 84)
@@ -167,8 +167,85 @@ def test_gemm_nt_strided_views_and_unsupported(dev):
     _assert_within_ulp(wide[:, 256:], ref, torch.bfloat16, "strided gemm_nt")
     assert torch.equal(wide[:, :256].cpu(), torch.zeros(M, 256, dtype=torch.bfloat16))
     assert not K_.gemm_nt_supported(300, 512, 512)
-    with pytest.raises(RuntimeError, match="ZK_EUNSUPPORTED"):
-        K_.gemm_nt(ad[:300, :K], bd[:N, :K])
+    out = K_.gemm_nt(ad[:300, :K], bd[:N, :K])
+    _assert_within_ulp(out, a[:300, :K].double() @ b[:N, :K].double().t(), torch.bfloat16,
+                       "gemm_nt 300 x 512 x 512")
+
+
+def _layout_operands(M, N, Kd, dtype, a_km, b_km, seed, dev, pad=0):
+    """(a, b) on the device as the layouts store them -- row-strided views of
+    buffers ``pad`` columns wider -- and, on the CPU, the [M, K] / [N, K]
+    matrices they hold."""
+    a = _rand((Kd, M + pad) if a_km else (M, Kd + pad), dtype, seed)
+    b = _rand((Kd, N + pad) if b_km else (N, Kd + pad), dtype, seed + 1, 0.05)
+    ad, bd = a.to(dev), b.to(dev)
+    a, ad = (a[:, :M], ad[:, :M]) if a_km else (a[:, :Kd], ad[:, :Kd])
+    b, bd = (b[:, :N], bd[:, :N]) if b_km else (b[:, :Kd], bd[:, :Kd])
+    am = a.t() if a_km else a
+    bm = b.t() if b_km else b
+    return ad, bd, am, bm
+
+
+# (M, N, K): on the 256 x 256 grid (the tiled MFMA pipeline, one to 48 tiles,
+# 2 to 64 K steps) and off it (the masked kernel: ragged M, N and K)
+GEMM_SHAPES = [(256, 256, 256), (512, 768, 384), (768, 512, 1280), (1024, 2048, 4096),
+               (300, 200, 72), (136, 520, 1000), (1, 7, 5)]
+
+
+@pytest.mark.parametrize("layout", [(False, True), (True, True), (True, False), (False, False)],
+                         ids=["dY_W", "dYt_X", "At_B", "X_Wt"])
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+@pytest.mark.parametrize("dtype", ALL)
+def test_gemm_layouts(dev, layout, M, N, K, dtype):
+    """zk_gemm in every operand layout -- (0, 1) the input gradient dY W on W as
+    stored, (1, 1) the weight gradient dY^T X on token-major activations,
+    (1, 0), and (0, 0) the forward -- against the fp64 product of the same
+    rounded inputs: 2-byte types every element within one ulp (one rounding
+    of an fp32 sum), fp32 within 1e-5 normwise; with row-strided operand
+    views and, for the 2-byte types, a fused residual."""
+    from zorse_amd import kernels as K_
+    a_km, b_km = layout
+    print(f"gemm {M}x{N}x{K} a_kmajor={a_km} b_kmajor={b_km} {dtype}", flush=True)
+    a, b, am, bm = _layout_operands(M, N, K, dtype, a_km, b_km, 91, dev, pad=8)
+    res = dtype != torch.float32 and (M * N) % 2 == 0
+    r = _rand((M, N), dtype, 93) if res else None
+    out = K_.gemm(a, b, a_kmajor=a_km, b_kmajor=b_km, residual=r.to(dev) if res else None)
+    path = K_.gemm_path(M, N, K, a.stride(0), b.stride(0), N, dtype, a_km, b_km,
+                        N if res else -1)
+    assert path == ("tiled" if dtype != torch.float32 and K_.gemm_nt_supported(M, N, K)
+                    else "general")
+    ref = am.double() @ bm.double().t()
+    if res:
+        ref = ref + r.double()
+    if dtype == torch.float32:
+        assert_close(out, ref, dtype, "gemm fp32")
+    else:
+        _assert_within_ulp(out, ref, dtype, f"gemm {path}")
+
+
+def test_gemm_llama7b_backward_shapes(dev):
+    """The 7B layer's backward products on the tiled pipeline at full size:
+    the gate|up input gradient dgu W_gu (4096 x 4096 x 22016, W read as
+    stored) and weight gradient dgu^T n2 (22016 x 4096 x 4096, both
+    token-major), and the q|k|v weight gradient (12288 x 4096 x 4096),
+    against a plain PyTorch fp64 GEMM of the same rounded inputs on the GPU."""
+    from zorse_amd import kernels as K_
+    g = torch.Generator(device="cpu").manual_seed(87)
+    T, h, F2 = 4096, 4096, 22016
+    for what, (ra, ca), (rb, cb), a_km, b_km in (
+            ("dgu W_gu", (T, F2), (F2, h), False, True),
+            ("dgu^T n2", (T, F2), (T, h), True, True),
+            ("dqkv^T n1", (T, 12288), (T, h), True, True)):
+        print(f"gemm 7B backward {what}", flush=True)
+        a = torch.randn(ra, ca, generator=g).to(dev, torch.bfloat16)
+        b = (0.02 * torch.randn(rb, cb, generator=g)).to(dev, torch.bfloat16)
+        out = K_.gemm(a, b, a_kmajor=a_km, b_kmajor=b_km)
+        am = a.t() if a_km else a
+        bm = b if b_km else b.t()
+        ref = torch.mm(am.double(), bm.double())
+        _assert_within_ulp(out, ref, torch.bfloat16, f"gemm {what}")
+        del a, b, out, ref
+        torch.cuda.empty_cache()
 
 
 def test_gemm_nt_llama7b_shapes(dev):

@@ -155,14 +155,13 @@ def test_layer_fwd_bwd_vs_oracle(dev, name):
     _check_layer(layer, x, dout, dtype, name)
 
 
-# Token counts at or above the layer's threshold for transposed backward
-# operands, with sequence lengths that are not multiples of 8: the attention
-# kernels then write no transposed copies, so the backward takes the explicit
-# transposes of ragged shapes instead (and, with an odd token count, of the
-# SwiGLU output and gradients as well).
+# Sequence lengths that are not multiples of 8 (and token counts off the
+# GEMM pipeline's 256 grid): every projection product then runs on the masked
+# general GEMM kernel, and the fused gate|up GEMM on its ragged-tile kernel
+# where the token count is a multiple of 8.
 RAGGED_LONG = {
-    "cfg4_bf16_S1100": ("cfg4_bf16", None, (1, 1100)),  # T % 8 = 4: no transposed SwiGLU outputs
-    "cfg3_fp16_S516x2": ("cfg3_fp16_gqa", None, (2, 516)),  # T = 1032: SwiGLU _t kernels on
+    "cfg4_bf16_S1100": ("cfg4_bf16", None, (1, 1100)),
+    "cfg3_fp16_S516x2": ("cfg3_fp16_gqa", None, (2, 516)),
     "cfg5_bf16_swa_S1027": ("cfg5_bf16_swa", 160, (1, 1027)),
 }
 
@@ -172,7 +171,7 @@ def test_layer_ragged_long_sequence(dev, name):
     from zorse_amd import layer as LY
     base, window, (B, S) = RAGGED_LONG[name]
     kw, _, dtype, _ = CONFIGS[base]
-    assert B * S >= LY._TRANSPOSE_MIN_TOKENS and S % 8 != 0
+    assert S % 8 != 0 and (B * S) % 256 != 0
     print(f"layer {name}", flush=True)
     layer = _layer(kw, dev, param_dtype=dtype, window=window, seed=211)
     g = torch.Generator().manual_seed(17)
@@ -181,11 +180,8 @@ def test_layer_ragged_long_sequence(dev, name):
     _check_layer(layer, x, dout, dtype, name)
 
 
-# Layers whose every projection GEMM the hand-written kernels take (tokens,
-# hidden, q|k|v width and FFN multiples of 256), run with the "hip" GEMM
-# backend -- the four forward products (gate|up through zk_gemm_swiglu with its
-# SwiGLU epilogue, the others through zk_gemm_nt) and the eight backward ones
-# -- and with the default "auto" backend (the four forward products).
+# Layers whose every projection GEMM is on the MFMA pipeline's grid (tokens,
+# hidden, q|k|v width and FFN multiples of 256).
 HIP_GEMM = {
     "cfg3_fp16_gqa": (CONFIGS["cfg3_fp16_gqa"][0], None, torch.float16, (2, 256)),
     "cfg4_bf16_F1536": (dict(hidden_size=512, num_attention_heads=4, intermediate_size=1536,
@@ -194,38 +190,71 @@ HIP_GEMM = {
 }
 
 
-@pytest.mark.parametrize("mode", ["hip", "auto"])
+def _forbid_library_products(monkeypatch):
+    """Make every torch GEMM entry point the layer could reach raise."""
+    def forbidden(name):
+        def fn(*a, **k):
+            raise AssertionError(f"torch.{name} called on the layer's path")
+        return fn
+    for name in ("mm", "addmm", "matmul", "bmm", "baddbmm"):
+        monkeypatch.setattr(torch, name, forbidden(name))
+    monkeypatch.setattr(torch.Tensor, "__matmul__", forbidden("Tensor.__matmul__"))
+
+
 @pytest.mark.parametrize("name", list(HIP_GEMM))
-def test_layer_hip_gemm_backend(dev, name, mode, monkeypatch):
+def test_layer_every_product_hand_written(dev, name, monkeypatch):
+    """All twelve projection products of a layer step go through the
+    hand-written GEMMs -- the four forward ones (gate|up with the SwiGLU
+    epilogue), the four input gradients dY W and the four weight gradients
+    dY^T X on the operands as stored (no transposes) -- each on the MFMA
+    pipeline (zk_gemm_path "tiled"); no torch GEMM is called.  Parity against
+    the fp64 oracle as every layer test."""
     from zorse_amd import kernels as K
     from zorse_amd import layer as LY
     kw, window, dtype, (B, S) = HIP_GEMM[name]
-    print(f"layer {name} ({mode} GEMM backend)", flush=True)
+    print(f"layer {name} (every product hand-written)", flush=True)
+    layer = _layer(kw, dev, param_dtype=dtype, window=window, seed=307)
+    g = torch.Generator().manual_seed(29)
+    x = torch.randn(B, S, kw["hidden_size"], generator=g).to(dtype)
+    dout = torch.randn(B, S, kw["hidden_size"], generator=g).to(dtype)
     calls = []
+    real_gemm, real_swiglu = K.gemm, K.gemm_swiglu
 
-    def counting(real):
-        def fn(*args, **kwargs):
-            calls.append((real.__name__, tuple(args[0].shape)))
-            return real(*args, **kwargs)
-        return fn
+    def gemm(a, b, *, a_kmajor=False, b_kmajor=False, residual=None, out=None):
+        M, Kd = (a.shape[1], a.shape[0]) if a_kmajor else a.shape
+        N = b.shape[1] if b_kmajor else b.shape[0]
+        ldc = out.stride(0) if out is not None else N
+        calls.append(("gemm", a_kmajor, b_kmajor,
+                      K.gemm_path(M, N, Kd, a.stride(0), b.stride(0), ldc, a.dtype, a_kmajor,
+                                  b_kmajor, residual.stride(0) if residual is not None else -1)))
+        return real_gemm(a, b, a_kmajor=a_kmajor, b_kmajor=b_kmajor, residual=residual, out=out)
 
-    monkeypatch.setattr(K, "gemm_nt", counting(K.gemm_nt))
-    monkeypatch.setattr(K, "gemm_swiglu", counting(K.gemm_swiglu))
-    prev = LY.set_gemm_backend(mode)
-    prev_fused = LY.set_fused_gate_up(True)
-    try:
-        layer = _layer(kw, dev, param_dtype=dtype, window=window, seed=307)
-        g = torch.Generator().manual_seed(29)
-        x = torch.randn(B, S, kw["hidden_size"], generator=g).to(dtype)
-        dout = torch.randn(B, S, kw["hidden_size"], generator=g).to(dtype)
-        _check_layer(layer, x, dout, dtype, f"{name} hip GEMM")
-    finally:
-        LY.set_gemm_backend(prev)
-        LY.set_fused_gate_up(prev_fused)
-    if mode == "hip":
-        assert len(calls) == 12 and sum(c[0] == "gemm_swiglu" for c in calls) == 1, calls
-    else:  # the forward products: q|k|v, o, gate|up (fused with the SwiGLU), down
-        assert [c[0] for c in calls] == ["gemm_nt", "gemm_nt", "gemm_swiglu", "gemm_nt"], calls
+    def gemm_swiglu(*a, **k):
+        calls.append(("gemm_swiglu", False, False,
+                      "tiled" if K.gemm_nt_supported(a[0].shape[0], 2 * a[1].shape[0],
+                                                     a[0].shape[1]) else "general"))
+        return real_swiglu(*a, **k)
+
+    def no_transpose(*a, **k):
+        raise AssertionError("zk_transpose called on the layer's path")
+
+    monkeypatch.setattr(K, "gemm", gemm)
+    monkeypatch.setattr(K, "gemm_swiglu", gemm_swiglu)
+    monkeypatch.setattr(K, "transpose", no_transpose)
+    with monkeypatch.context() as m:
+        _forbid_library_products(m)
+        prev = LY.set_fused_gate_up(True)
+        try:
+            _check_layer(layer, x, dout, dtype, f"{name} hand-written GEMMs")
+        finally:
+            LY.set_fused_gate_up(prev)
+    # the layer step itself: 4 forward + 8 backward products (the oracle runs
+    # on the CPU, outside these wrappers)
+    assert len(calls) == 12, calls
+    assert sum(c[0] == "gemm_swiglu" for c in calls) == 1, calls
+    assert sum(c[1:3] == (False, True) for c in calls) == 4, calls   # dY W
+    assert sum(c[1:3] == (True, True) for c in calls) == 4, calls    # dY^T X
+    assert all(c[3] == "tiled" for c in calls), calls
 
 
 def test_cfg1_head_and_cross_entropy_loss(dev):
@@ -473,68 +502,33 @@ def test_stage_steps_each_parameter_once(dev):
         assert torch.equal(a, b)
 
 
-def test_stage_transposed_weights(dev):
-    """The optimizer step keeps W^T of the projections next to the bf16 weights
-    (StageRunner(transposed_weights=True)): after each step the copies are
-    exact transposes of the weights; the next backward reads them instead of
-    transposing W_o / W_down (two fewer transposes per layer) and its
-    gradients and updated weights agree with the run without them (only the
-    GEMMs' summation order differs).  1024 tokens, so the backward takes its
-    transposed-operand GEMM path."""
-    from zorse_amd import layer as L
+def test_stage_no_transposes_no_library_gemm(dev, monkeypatch):
+    """Two 2-layer stage steps at 1024 tokens with AdamW in the backward: no
+    transpose pass and no torch GEMM anywhere on the path (forward, backward,
+    optimizer step), and the step runs twice without error."""
+    from zorse_amd import kernels as K
     from zorse_amd.stage import StageRunner
     kw = dict(hidden_size=256, num_attention_heads=2, intermediate_size=512, rope_theta=1e4)
     dtype = torch.bfloat16
     g = torch.Generator().manual_seed(9)
     x = torch.randn(1, 1024, 256, generator=g).to(dtype).to(dev)
     dout = torch.randn(1, 1024, 256, generator=g).to(dtype).to(dev)
-    real = L.K.transpose
-    counts = {}
+    layers = [_layer(kw, dev, param_dtype=dtype, seed=s) for s in (1, 2)]
+    runner = StageRunner(layers, lr=1e-4)
 
-    def counting(*a, **k):
-        counts["n"] = counts.get("n", 0) + 1
-        return real(*a, **k)
+    def no_transpose(*a, **k):
+        raise AssertionError("zk_transpose called on the stage's path")
 
-    out = {}
-    try:
-        L.K.transpose = counting
-        for use_wt in (False, True):
-            layers = [_layer(kw, dev, param_dtype=dtype, seed=s) for s in (1, 2)]
-            grads = {}
-            for i, l in enumerate(layers):
-                l.flat_param.register_post_accumulate_grad_hook(
-                    lambda p, i=i: grads.__setitem__(i, p.grad.detach().clone()))
-            runner = StageRunner(layers, lr=1e-4, transposed_weights=use_wt)
-            per_step = []
-            for _ in range(2):
-                counts["n"] = 0
-                runner.step(x, dout)
-                runner.wait_optimizer()
-                torch.cuda.synchronize()
-                per_step.append(counts["n"])
-                if use_wt:
-                    for l in layers:
-                        assert l._transposed_weights() is not None
-                        for name, view in (("qkv", l.param_view("q")), ("o", l.param_view("o")),
-                                           ("down", l.param_view("down"))):
-                            if name == "qkv":
-                                a, b = l._offsets["q"][0], l._offsets["v"][1]
-                                view = l.flat_param[a:b].view(-1, 256)
-                            assert torch.equal(l._wt[name], view.t()), name
-                        a, b = l._offsets["gate"][0], l._offsets["up"][1]
-                        assert torch.equal(l._wt["gu"], l.flat_param[a:b].view(-1, 256).t())
-            out[use_wt] = (grads, [l.flat_param.detach().clone() for l in layers], per_step)
-    finally:
-        L.K.transpose = real
-    # step 1 has no copies yet; step 2 uses them: 2 transposes fewer per layer
-    # in the backward.  With copies, each layer's optimizer step also
-    # transposes its 4 matrices (qkv, o, gate|up, down) out of the compute copy.
-    opt = 4 * len(layers)
-    assert out[True][2][0] == out[False][2][0] + opt
-    assert out[True][2][1] == out[False][2][1] - 4 + opt
-    for i in (0, 1):
-        assert_close(out[True][0][i], out[False][0][i].double(), dtype, f"layer {i} grad")
-        assert_close(out[True][1][i], out[False][1][i].double(), dtype, f"layer {i} weights")
+    monkeypatch.setattr(K, "transpose", no_transpose)
+    before = [l.flat_param.detach().clone() for l in layers]
+    with monkeypatch.context() as m:
+        _forbid_library_products(m)
+        for _ in range(2):
+            runner.step(x, dout)
+        runner.wait_optimizer()
+        torch.cuda.synchronize()
+    for b, l in zip(before, layers):
+        assert torch.isfinite(l.flat_param).all() and not torch.equal(b, l.flat_param)
 
 
 @pytest.mark.parametrize("S", [256, 1024])

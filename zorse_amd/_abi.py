@@ -82,6 +82,9 @@ SIGNATURES = {
     "zk_swiglu_bwd": (_int, [_ptr, _i64, _ptr, _ptr, _i64, _ptr, _ptr, _i64,
                              _i64, _i64, _int, _ptr]),
     "zk_gemm_nt_supported": (_int, [_i64, _i64, _i64]),
+    "zk_gemm": (_int, [_ptr, _i64, _int, _ptr, _i64, _int, _ptr, _i64, _ptr, _i64, _i64, _i64,
+                       _i64, _int, _ptr]),
+    "zk_gemm_path": (_int, [_i64, _i64, _i64, _i64, _int, _i64, _int, _i64, _i64, _int]),
     "zk_gemm_nt": (_int, [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _i64,
                           _int, _ptr]),
     "zk_gemm_swiglu": (_int, [_ptr, _i64, _ptr, _ptr, _i64, _ptr, _ptr, _i64, _ptr, _i64, _ptr,

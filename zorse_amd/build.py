@@ -38,7 +38,10 @@ HIPCC_FLAGS = [
 # vectoriser forms two-wide fp32 negations that this compiler cannot select
 # (a backend "Cannot select: v2f32 bitcast" crash in the position-major
 # kernel); the kernels there are memory-bound, so scalar code costs nothing.
-FILE_FLAGS = {"rope.hip": ["-fno-slp-vectorize"]}
+# gemm.hip: its LDS-DMA asm declares M0 clobbered, which clang reports as a
+# clobber of a reserved register (the intent: the compiler keeps nothing in
+# M0 across the asm).
+FILE_FLAGS = {"rope.hip": ["-fno-slp-vectorize"], "gemm.hip": ["-Wno-inline-asm"]}
 
 
 def _hipcc() -> str:

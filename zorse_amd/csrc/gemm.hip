@@ -1,10 +1,15 @@
-// Projection GEMM for gfx950 (bf16 / fp16 storage, fp32 accumulation):
+// Projection GEMMs for gfx950 (bf16 / fp16 storage, fp32 accumulation):
 //
-//   C[M, N] = A[M, K] B[N, K]^T  (+ R[M, N])
+//   C[M, N] = op(A) op(B)^T (+ R[M, N])
 //
-// both operands contiguous along the reduction (the nn.Linear forward
-// x W^T; the layer's backward GEMMs take this form on transposed operands).
-// One fp32 rounding of the accumulated sum (plus R) to the storage type.
+// with each operand either contiguous along the reduction ("NT": A [M, K],
+// B [N, K], the nn.Linear forward x W^T) or along its output dimension
+// ("K-major": A [K, M], B [K, N]).  The layer's backward takes both forms
+// from the tensors as the forward left them: the input gradient dY W reads
+// dY [T, out] along the reduction and W [out, in] K-major; the weight
+// gradient dY^T X reads dY [T, out] and X [T, in] both K-major.  No operand
+// is ever transposed in memory.  One fp32 rounding of the accumulated sum
+// (plus R) to the storage type.
 //
 // Workgroup = 4 waves, tile = 256 x 256, one workgroup per CU (160 KB LDS,
 // one wave per SIMD).  Each wave owns a 128 x 128 block: 8 x 8 MFMA blocks of
@@ -14,21 +19,30 @@
 // pipeline on 4 x 4 blocks of v_mfma_f32_32x32x16 ran 6-10 % slower at the
 // 7B shapes.)
 //
-// Tiles reach LDS through buffer_load_dwordx4 ... lds (16 bytes per lane,
-// 128-byte row segments, XOR-swizzled chunks, see tile_off).  A sits in a ring
-// of three stages and B in a ring of two, so A's loads run two K steps ahead
-// and B's one; the refill of each K step is spread one load per eight MFMAs
-// over the whole step, because a burst of loads fills the texture unit's
-// command queue and stalls the issuing wave (counters: SQ_VMEM_TA_CMD_FIFO_FULL),
-// and the operand reads likewise go two per eight MFMAs (SQ_LDS_CMD_FIFO_FULL).
-// The loads are issued from inline assembly: with an LDS DMA visible to it,
-// the compiler's wait insertion waits for every load in flight before any LDS
-// read; the kernel orders them itself with exact vmcnt waits (loads complete
-// in issue order) and one barrier per K step.
+// Tiles reach LDS through buffer_load_dwordx4 ... lds (16 bytes per lane).
+// An NT operand tile is 256 rows x 64 k (128-byte row segments, chunks
+// XOR-swizzled by tile_off) read by ds_read_b128; a K-major operand tile is
+// 64 k-rows x 256 columns (512-byte row segments, swizzled by kmaj_sw) read
+// by ds_read_b64_tr_b16, which hands each lane 4 consecutive k of one column
+// -- two of them make the MFMA operand the b128 read gives an NT tile.  A
+// sits in a ring of three stages and B in a ring of two, so A's loads run
+// two K steps ahead and B's one; the refill of each K step is spread one
+// load per eight MFMAs over the whole step, because a burst of loads fills
+// the texture unit's command queue and stalls the issuing wave (counters:
+// SQ_VMEM_TA_CMD_FIFO_FULL), and the operand reads likewise go two per eight
+// MFMAs (SQ_LDS_CMD_FIFO_FULL).  The loads are issued from inline assembly:
+// with an LDS DMA visible to it, the compiler's wait insertion waits for
+// every load in flight before any LDS read; the kernel orders them itself
+// with exact vmcnt waits (loads complete in issue order) and one barrier per
+// K step.
 //
 // Workgroups are remapped so that the 32 CUs of one XCD (dispatch order
 // round-robins XCDs) take consecutive tiles, ordered in groups of four M
 // tiles, so each XCD's L2 serves a 4 x 8 block of tiles.
+//
+// Shapes off that grid, fp32 operands, and leading dimensions past the
+// buffer-resource range go to gemm_gen_kernel: 128 x 128 tiles staged
+// through registers with masked loads and stores (any M, N, K).
 #include "attn_common.h"
 #include "vec.h"
 
@@ -57,10 +71,17 @@ __device__ __forceinline__ uint32_t lds_addr(const T* p) {
       reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const T*)(p)));
 }
 
-// 16 bytes per lane from r + voff + soff into LDS at lds + 16 lane.
+// 16 bytes per lane from r + voff + soff into LDS at lds + 16 lane.  The
+// asm writes the LDS address into M0 and declares M0 clobbered, so the
+// compiler keeps nothing of its own there across it.  (clang warns that M0
+// is a reserved register -- the compiler sets it right before each of its
+// own uses -- and that a reserved register may not be preserved across the
+// asm, which is what the clobber says; binding the address to M0 as an
+// input operand instead made the register allocator shuttle accumulators
+// between AGPRs and VGPRs in the main loop.)
 __device__ __forceinline__ void dma16(v4i r, uint32_t voff, uint32_t soff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-               :: "v"(voff), "s"(r), "s"(soff), "s"(lds) : "memory");
+               :: "v"(voff), "s"(r), "s"(soff), "s"(lds) : "memory", "m0");
 }
 
 // Operands and outputs of one launch.  EPI 0: c = a b^T (+ r); EPI 1 (the
@@ -85,8 +106,8 @@ struct GemmArgs {
   int64_t M, N, K;
 };
 
-// A ROWS x 64 tile (128-byte rows, chunks swizzled by tile_sw<64>) in eight
-// instructions of 32 rows; instruction i of wave w fills LDS chunks
+// An NT tile: ROWS x 64 (128-byte rows, chunks swizzled by tile_sw<64>) in
+// eight instructions of 32 rows; instruction i of wave w fills LDS chunks
 // 256 i + 64 w .. +63, lane l the chunk of row 32 i + (64 w + l) / 8.
 template <typename T>
 struct TileDma {
@@ -117,6 +138,66 @@ struct TileDma {
   }
 };
 
+// A K-major tile: 64 k-rows x 256 columns (512-byte rows); the 16-byte chunk
+// c of row k sits at chunk position c ^ kmaj_sw(k).  One transposed operand
+// read of a 32-lane half touches the same 32-byte column pair of rows
+// {k0 .. k0 + 3, k0 + 8 .. k0 + 11} (k0 a multiple of 4 with bit 2 clear, or
+// k0 + 4 ..): kmaj_sw sends those eight rows to eight different 32-byte bank
+// groups of the 256-byte bank row, so the read is free of bank conflicts.
+__device__ __forceinline__ int kmaj_sw(int k) { return 2 * ((k & 3) | ((k >> 1) & 4)); }
+
+// Loads of a K-major tile, eight instructions of two rows: instruction i of
+// wave w fills rows 2 (w & 1) + 8 (w >> 1) + 4 (i & 1) + 16 (i >> 1) and the
+// row after it (lanes 0-31, 32-63), so each lane's row keeps the same
+// kmaj_sw in every instruction and its byte offset is one 32-bit value.
+template <typename T>
+struct TileDmaK {
+  uint32_t lane_off;  // bytes from the tile's first row
+  int wave_row;       // wave-uniform
+  __device__ __forceinline__ void init(int64_t ld) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    wave_row = 2 * (w & 1) + 8 * (w >> 1);
+    const int row = wave_row + (lane >> 5);
+    const int c = (lane & 31) ^ kmaj_sw(row);
+    lane_off = static_cast<uint32_t>(row * ld * static_cast<int64_t>(sizeof(T)) + c * 16);
+  }
+  // piece i of the tile whose first row (k) and column are at `gbase`
+  __device__ __forceinline__ void issue(T* tile, const T* gbase, int64_t ld, int i) const {
+    const int ri = 4 * (i & 1) + 16 * (i >> 1);
+    const uint32_t soff = static_cast<uint32_t>(ri * ld * static_cast<int64_t>(sizeof(T)));
+    dma16(rsrc_words(gbase), lane_off, soff, lds_addr(tile + (wave_row + ri) * 256));
+  }
+};
+
+// Element offset, in a K-major tile, of this lane's first transposed read
+// for the 16-column block at colw: row k = 8 (l / 16) + (l % 16) / 4, column
+// colw + 4 (l % 4).  The read of column block colw + 16 r at substep s (k +
+// 32 s) is at (base ^ 16 r) + 8192 s, and its second half (k + 4) 1024
+// elements further: the XOR touches the chunk bits 1-3, where the base holds
+// kmaj_sw; the base's k is below 32 with bit 2 clear, so the two steps are
+// plain adds (immediate offsets of the read) and neither changes kmaj_sw.
+__device__ __forceinline__ int kmaj_base(int colw) {
+  const int lane = threadIdx.x & 63;
+  const int k = 8 * (lane >> 4) + ((lane & 15) >> 2);
+  const int col = colw + 4 * (lane & 3);
+  return k * 256 + (((col >> 3) ^ kmaj_sw(k)) << 3) + (col & 7);
+}
+
+// The MFMA operand (lane l: 8 consecutive k from 8 (l / 16) of column
+// l % 16 of the block) from a K-major tile: two ds_read_b64_tr_b16, each of
+// which gives lane i of a 16-lane group element (i & 3) of the 8-byte runs
+// addressed by lanes (i >> 2) + 4 e, e = 0..3 -- i.e. column i of rows
+// k .. k + 3.
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::vec8 kmaj_operand(const T* tile, int off) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + off));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + off + 1024));
+  return __builtin_bit_cast(typename Mfma<T>::vec8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 // silu(g) = g / (1 + e^-g) from the hardware exp2 and reciprocal (about one
 // fp32 ulp each): the epilogue's four waves per CU evaluate it for every
 // output element of the tile while the CU's MFMAs wait, so the IEEE exp and
@@ -127,9 +208,12 @@ __device__ __forceinline__ float silu_fast(float g) {
   return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
 }
 
-template <typename T, int EPI>
+// AKM / BKM: operand A / B is K-major (see the top of the file).  EPI 1
+// takes NT operands only.
+template <typename T, int EPI, bool AKM, bool BKM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void gemm_nt_kernel(GemmArgs args) {
+void gemm_tiled_kernel(GemmArgs args) {
+  static_assert(EPI == 0 || (!AKM && !BKM), "the SwiGLU epilogue takes NT operands");
   const T* __restrict__ A = static_cast<const T*>(args.a);
   const T* __restrict__ B = static_cast<const T*>(args.b);
   const int64_t lda = args.lda, ldb = args.ldb;
@@ -152,8 +236,10 @@ void gemm_nt_kernel(GemmArgs args) {
   const int64_t gm = n_m - mf < GROUP_M ? n_m - mf : GROUP_M;
   const int64_t in_grp = pid - grp * per_group;
   const int64_t m0 = (mf + in_grp % gm) * BM, n0 = (in_grp / gm) * BN;
-  const T* Ab = A + m0 * lda;
-  const T* Bb = B + n0 * ldb;
+  // first element of the tile and the step between K steps, per layout
+  const T* Ab = AKM ? A + m0 : A + m0 * lda;
+  const T* Bb = BKM ? B + n0 : B + n0 * ldb;
+  const int64_t a_step = AKM ? BK * lda : BK, b_step = BKM ? BK * ldb : BK;
   // EPI 1: the tile's 128 features f0 .. f0 + 127 of both halves.  Tile row
   // block b (16 rows) holds, for wave half wn = b / 8 and jj = b % 8, the gate
   // (jj even) or up (jj odd) rows of features f0 + 64 wn + 16 (jj / 2) ..
@@ -168,37 +254,68 @@ void gemm_nt_kernel(GemmArgs args) {
                             : B;
 
   TileDma<T> adma, bdma;
-  adma.init(lda);
-  bdma.init(ldb);
+  TileDmaK<T> admak, bdmak;
+  if constexpr (AKM)
+    admak.init(lda);
+  else
+    adma.init(lda);
+  if constexpr (BKM)
+    bdmak.init(ldb);
+  else
+    bdma.init(ldb);
   f32x4 acc[8][8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{};
-  // operand row blocks of substep 0 (16 rows; lane: row l % 16, 16-byte
-  // chunk l / 16); substep s XORs the chunk index with 4 s
+  // operand row blocks of substep 0 (NT tiles: 16 rows, lane: row l % 16,
+  // 16-byte chunk l / 16; substep s XORs the chunk index with 4 s); K-major
+  // tiles: one base per operand, see kmaj_base
   int aoff[8], boff[8];
+  int abase = 0, bbase = 0;
+  if constexpr (AKM) {
+    abase = kmaj_base(wm * 128);
+  } else {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    aoff[i] = tile_off<BK>(wm * 128 + 16 * i + l16, 8 * q4);
-    boff[i] = tile_off<BK>(wn * 128 + 16 * i + l16, 8 * q4);
+    for (int i = 0; i < 8; ++i) aoff[i] = tile_off<BK>(wm * 128 + 16 * i + l16, 8 * q4);
+  }
+  if constexpr (BKM) {
+    bbase = kmaj_base(wn * 128);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) boff[i] = tile_off<BK>(wn * 128 + 16 * i + l16, 8 * q4);
   }
   V8 xa[2][8], xb[2][8];
   auto Bs = [&](int st) __attribute__((always_inline)) -> T* { return st ? Bs1 : Bs0; };
   // operand piece r (0..7: A row blocks, 8..15: B row blocks) of substep s
   // into set q
   auto rd_piece = [&](int sa, int sb, int s, int q, int r) __attribute__((always_inline)) {
-    if (r < 8)
-      xa[q][r] = *reinterpret_cast<const V8*>(&As[sa * (BM * BK) + (aoff[r] ^ (32 * s))]);
-    else
-      xb[q][r - 8] = *reinterpret_cast<const V8*>(&Bs(sb)[boff[r - 8] ^ (32 * s)]);
+    if (r < 8) {
+      const T* t = &As[sa * (BM * BK)];
+      if constexpr (AKM)
+        xa[q][r] = kmaj_operand<T>(t, (abase ^ (16 * r)) + 8192 * s);
+      else
+        xa[q][r] = *reinterpret_cast<const V8*>(&t[aoff[r] ^ (32 * s)]);
+    } else {
+      const T* t = Bs(sb);
+      if constexpr (BKM)
+        xb[q][r - 8] = kmaj_operand<T>(t, (bbase ^ (16 * (r - 8))) + 8192 * s);
+      else
+        xb[q][r - 8] = *reinterpret_cast<const V8*>(&t[boff[r - 8] ^ (32 * s)]);
+    }
   };
   auto loadA = [&](int sa, int64_t k, int p) __attribute__((always_inline)) {
-    adma.issue(&As[sa * (BM * BK)], Ab + k * BK, lda, p);
+    if constexpr (AKM)
+      admak.issue(&As[sa * (BM * BK)], Ab + k * a_step, lda, p);
+    else
+      adma.issue(&As[sa * (BM * BK)], Ab + k * a_step, lda, p);
   };
   auto loadB = [&](int sb, int64_t k, int p) __attribute__((always_inline)) {
     if constexpr (EPI == 0) {
-      bdma.issue(Bs(sb), Bb + k * BK, ldb, p);
+      if constexpr (BKM)
+        bdmak.issue(Bs(sb), Bb + k * b_step, ldb, p);
+      else
+        bdma.issue(Bs(sb), Bb + k * b_step, ldb, p);
     } else {
       bdma.issue_wave_rows(Bs(sb), bwave + k * BK,
                            static_cast<uint32_t>(16 * p * ldb * static_cast<int64_t>(sizeof(T))), p);
@@ -385,7 +502,146 @@ void gemm_nt_kernel(GemmArgs args) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Any shape and layout, bf16 / fp16 / fp32: 4 waves, a 128 x 128 tile (each
+// wave 64 x 64 as 4 x 4 MFMA blocks), K steps of 32.  Each step's operand
+// tiles are read from global memory into registers with every index checked
+// (out-of-range elements are zero), written to LDS as [128 rows][32 k] (k
+// contiguous, padded rows), and consumed by v_mfma_f32_16x16x32 (2-byte
+// types) or v_mfma_f32_16x16x4f32 (fp32, full fp32 products).  Stores are
+// masked per element.  This is the path for token counts off the 256 grid
+// and for fp32 layers; it needs no alignment beyond the element's.
+constexpr int GBM = 128, GBK = 32;
+
+template <typename T>
+struct GenCfg {
+  static constexpr int P = sizeof(T) == 2 ? GBK + 8 : GBK + 4;  // LDS row pitch (elements)
+};
+
+// One [128][32] operand tile (rows r0 .., k0 ..) into LDS at `t` (pitch P).
+// KM: the operand is stored [K][rows]; else [rows][K].
+template <typename T, bool KM>
+__device__ __forceinline__ void gen_stage(T* t, const T* __restrict__ src, int64_t ld, int64_t r0,
+                                          int64_t R, int64_t k0, int64_t K) {
+  constexpr int P = GenCfg<T>::P;
+  const int tid = threadIdx.x;
+  T v[16];
+  if constexpr (!KM) {
+    // thread: row tid / 2, 16 consecutive k from 16 (tid % 2)
+    const int r = tid >> 1, kk = (tid & 1) * 16;
+    const int64_t gr = r0 + r;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int64_t gk = k0 + kk + e;
+      v[e] = (gr < R && gk < K) ? src[gr * ld + gk] : static_cast<T>(0.0f);
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) t[r * P + kk + e] = v[e];
+  } else {
+    // thread: k = tid / 8, 16 consecutive rows from 16 (tid % 8)
+    const int k = tid >> 3, rr = (tid & 7) * 16;
+    const int64_t gk = k0 + k;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int64_t gr = r0 + rr + e;
+      v[e] = (gr < R && gk < K) ? src[gk * ld + gr] : static_cast<T>(0.0f);
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) t[(rr + e) * P + k] = v[e];
+  }
+}
+
+template <typename T, bool AKM, bool BKM>
+__global__ __launch_bounds__(256) void gemm_gen_kernel(GemmArgs args) {
+  constexpr int P = GenCfg<T>::P;
+  __shared__ __attribute__((aligned(16))) T As[GBM * P];
+  __shared__ __attribute__((aligned(16))) T Bs[GBM * P];
+  const T* __restrict__ A = static_cast<const T*>(args.a);
+  const T* __restrict__ B = static_cast<const T*>(args.b);
+  const int64_t M = args.M, N = args.N, K = args.K;
+  const int64_t n_n = (N + GBM - 1) / GBM;
+  const int64_t m0 = (blockIdx.x / n_n) * GBM, n0 = (blockIdx.x % n_n) * GBM;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1, l16 = lane & 15, q4 = lane >> 4;
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{};
+  for (int64_t k0 = 0; k0 < K; k0 += GBK) {
+    gen_stage<T, AKM>(As, A, args.lda, m0, M, k0, K);
+    gen_stage<T, BKM>(Bs, B, args.ldb, n0, N, k0, K);
+    __syncthreads();
+    if constexpr (sizeof(T) == 2) {
+      typedef typename Mfma<T>::vec8 V8;
+      V8 xa[4], xb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        xa[i] = *reinterpret_cast<const V8*>(&As[(wm * 64 + 16 * i + l16) * P + 8 * q4]);
+        xb[i] = *reinterpret_cast<const V8*>(&Bs[(wn * 64 + 16 * i + l16) * P + 8 * q4]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = Mfma<T>::mma16(xa[i], xb[j], acc[i][j]);
+    } else {
+      // lane l: row l % 16, k = 4 kk + l / 16
+#pragma unroll
+      for (int kk = 0; kk < GBK / 4; ++kk) {
+        float xa[4], xb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          xa[i] = As[(wm * 64 + 16 * i + l16) * P + 4 * kk + q4];
+          xb[i] = Bs[(wn * 64 + 16 * i + l16) * P + 4 * kk + q4];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i], xb[j], acc[i][j], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  // acc[i][j][e]: row 16 i + 4 (l / 16) + e, column 16 j + l % 16 of the
+  // wave's 64 x 64 block
+  T* C = static_cast<T*>(args.c);
+  const T* R = static_cast<const T*>(args.r);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t row = m0 + wm * 64 + 16 * i + 4 * q4 + e;
+        const int64_t col = n0 + wn * 64 + 16 * j + l16;
+        if (row < M && col < N) {
+          float v = acc[i][j][e];
+          if (R != nullptr) v += to_f32(R[row * args.ldr + col]);
+          C[row * args.ldc + col] = static_cast<T>(v);
+        }
+      }
+}
+
 }  // namespace gemm
+
+// Whether the 256 x 256 pipeline takes a launch: 2-byte type, M and N
+// multiples of 256, K a multiple of 128 and at least 256, leading dimensions
+// multiples of 8 (16-byte tile rows and stores), and every tile of an operand
+// within reach of one buffer resource: 256 rows of an NT operand or 64 rows
+// of a K-major one below 2 GiB (lda, ldb below 2^22 / 2^24 elements).
+// Pointer alignment is checked by the caller.
+static bool tiled_takes(int64_t M, int64_t N, int64_t K, int64_t lda, int a_km, int64_t ldb,
+                        int b_km, int64_t ldc, int64_t ldr, int dtype) {
+  if (dtype != ZK_BF16 && dtype != ZK_F16) return false;
+  if (!(M > 0 && N > 0 && M % gemm::BM == 0 && N % gemm::BN == 0 && K % (2 * gemm::BK) == 0 &&
+        K >= 4 * gemm::BK))
+    return false;
+  if (lda % 8 || ldb % 8 || ldc % 8 || ldr % 8) return false;
+  const int64_t lim_a = int64_t(1) << (a_km ? 24 : 22), lim_b = int64_t(1) << (b_km ? 24 : 22);
+  return lda < lim_a && ldb < lim_b;
+}
+
 }  // namespace zk
 
 using namespace zk;
@@ -395,35 +651,77 @@ extern "C" int zk_gemm_nt_supported(int64_t M, int64_t N, int64_t K) {
          K >= 4 * gemm::BK;
 }
 
-extern "C" int zk_gemm_nt(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
-                          int64_t ldc, const void* r, int64_t ldr, int64_t M, int64_t N,
-                          int64_t K, int dtype, zk_stream_t stream) {
-  ZK_REQUIRE(dtype == ZK_BF16 || dtype == ZK_F16, ZK_EDTYPE,
-             "zk_gemm_nt: 2-byte dtypes only (got %d)", dtype);
-  ZK_REQUIRE(M >= 0 && N >= 0 && K >= 0, ZK_EINVAL, "zk_gemm_nt: bad shape");
-  ZK_REQUIRE(lda >= K && ldb >= K && ldc >= N && (r == nullptr || ldr >= N), ZK_EINVAL,
-             "zk_gemm_nt: bad leading dimension");
+extern "C" int zk_gemm_path(int64_t M, int64_t N, int64_t K, int64_t lda, int a_kmajor,
+                            int64_t ldb, int b_kmajor, int64_t ldc, int64_t ldr, int dtype) {
+  ZK_REQUIRE(valid_dtype(dtype), ZK_EDTYPE, "zk_gemm_path: bad dtype %d", dtype);
+  return tiled_takes(M, N, K, lda, a_kmajor != 0, ldb, b_kmajor != 0, ldc, ldr < 0 ? 8 : ldr,
+                     dtype)
+             ? ZK_GEMM_TILED
+             : ZK_GEMM_GENERAL;
+}
+
+namespace {
+
+template <typename T, bool AKM, bool BKM>
+void launch_gemm(bool tiled, const gemm::GemmArgs& ga, hipStream_t s) {
+  if constexpr (sizeof(T) == 2) {
+    if (tiled) {
+      const int64_t nwg = (ga.M / gemm::BM) * (ga.N / gemm::BN);
+      hipLaunchKernelGGL((gemm::gemm_tiled_kernel<T, 0, AKM, BKM>),
+                         dim3(static_cast<unsigned>(nwg)), dim3(256), 0, s, ga);
+      return;
+    }
+  }
+  {
+    const int64_t nwg = ((ga.M + gemm::GBM - 1) / gemm::GBM) * ((ga.N + gemm::GBM - 1) / gemm::GBM);
+    hipLaunchKernelGGL((gemm::gemm_gen_kernel<T, AKM, BKM>), dim3(static_cast<unsigned>(nwg)),
+                       dim3(256), 0, s, ga);
+  }
+}
+
+template <typename T>
+void launch_layout(bool tiled, int a_km, int b_km, const gemm::GemmArgs& ga, hipStream_t s) {
+  if (!a_km && !b_km)
+    launch_gemm<T, false, false>(tiled, ga, s);
+  else if (!a_km && b_km)
+    launch_gemm<T, false, true>(tiled, ga, s);
+  else if (a_km && b_km)
+    launch_gemm<T, true, true>(tiled, ga, s);
+  else
+    launch_gemm<T, true, false>(tiled, ga, s);
+}
+
+}  // namespace
+
+extern "C" int zk_gemm(const void* a, int64_t lda, int a_kmajor, const void* b, int64_t ldb,
+                       int b_kmajor, void* c, int64_t ldc, const void* r, int64_t ldr, int64_t M,
+                       int64_t N, int64_t K, int dtype, zk_stream_t stream) {
+  ZK_REQUIRE(valid_dtype(dtype), ZK_EDTYPE, "zk_gemm: bad dtype %d", dtype);
+  ZK_REQUIRE(M >= 0 && N >= 0 && K >= 0, ZK_EINVAL, "zk_gemm: bad shape");
+  const int a_km = a_kmajor != 0, b_km = b_kmajor != 0;
+  // an [M, K] operand needs ld >= K, a K-major [K, M] one ld >= M
+  ZK_REQUIRE(lda >= (a_km ? M : K) && ldb >= (b_km ? N : K) && ldc >= N &&
+                 (r == nullptr || ldr >= N),
+             ZK_EINVAL, "zk_gemm: bad leading dimension");
   if (M == 0 || N == 0) return ZK_OK;
-  ZK_REQUIRE(zk_gemm_nt_supported(M, N, K), ZK_EUNSUPPORTED,
-             "zk_gemm_nt: M, N must be multiples of 256 and K a multiple of 128, at least 256 "
-             "(got %lld x %lld x %lld)",
-             (long long)M, (long long)N, (long long)K);
-  const int64_t lds[] = {lda, ldb, ldc, r ? ldr : 8};
-  for (int64_t ld : lds) {
-    ZK_REQUIRE(ld % 8 == 0, ZK_EALIGN, "zk_gemm_nt: leading dimensions must be multiples of 8");
-    // a tile's 256 rows are addressed from one buffer resource (< 2 GiB)
-    ZK_REQUIRE(ld < (int64_t(1) << 22), ZK_EUNSUPPORTED,
-               "zk_gemm_nt: leading dimension out of range");
-  }
-  const void* ptrs[] = {a, b, c};
-  for (const void* p : ptrs) {
-    ZK_REQUIRE(p != nullptr, ZK_EINVAL, "zk_gemm_nt: null pointer");
-    ZK_REQUIRE(aligned(p, 16), ZK_EALIGN, "zk_gemm_nt: operands must be 16-byte aligned");
-  }
-  ZK_REQUIRE(r == nullptr || aligned(r, 16), ZK_EALIGN,
-             "zk_gemm_nt: operands must be 16-byte aligned");
-  const int64_t nwg = (M / gemm::BM) * (N / gemm::BN);
-  ZK_REQUIRE(nwg < 0x7fffffffLL, ZK_EINVAL, "zk_gemm_nt: grid too large");
+  ZK_REQUIRE(c != nullptr && (K == 0 || (a != nullptr && b != nullptr)), ZK_EINVAL,
+             "zk_gemm: null pointer");
+  const int eb = dtype_bytes(dtype);
+  const void* ptrs[] = {a, b, c, r};
+  for (const void* p : ptrs)
+    ZK_REQUIRE(p == nullptr || aligned(p, eb), ZK_EALIGN,
+               "zk_gemm: operands must be aligned to their element size");
+  const int64_t rows_a = a_km ? K : M, rows_b = b_km ? K : N;
+  // every index the kernels form stays below 2^62
+  ZK_REQUIRE(lda < (int64_t(1) << 40) && ldb < (int64_t(1) << 40) && ldc < (int64_t(1) << 40) &&
+                 (r == nullptr || ldr < (int64_t(1) << 40)) && rows_a < (int64_t(1) << 40) &&
+                 rows_b < (int64_t(1) << 40) && M < (int64_t(1) << 40),
+             ZK_EINVAL, "zk_gemm: sizes out of range");
+  bool tiled = tiled_takes(M, N, K, lda, a_km, ldb, b_km, ldc, r ? ldr : 8, dtype);
+  for (const void* p : ptrs) tiled = tiled && (p == nullptr || aligned(p, 16));
+  const int64_t nwg = tiled ? (M / gemm::BM) * (N / gemm::BN)
+                            : ((M + gemm::GBM - 1) / gemm::GBM) * ((N + gemm::GBM - 1) / gemm::GBM);
+  ZK_REQUIRE(nwg < 0x7fffffffLL, ZK_EINVAL, "zk_gemm: grid too large");
   gemm::GemmArgs ga{};
   ga.a = a;
   ga.lda = lda;
@@ -438,12 +736,18 @@ extern "C" int zk_gemm_nt(const void* a, int64_t lda, const void* b, int64_t ldb
   ga.K = K;
   hipStream_t s = as_stream(stream);
   if (dtype == ZK_BF16)
-    hipLaunchKernelGGL((gemm::gemm_nt_kernel<bf16, 0>), dim3(static_cast<unsigned>(nwg)),
-                       dim3(256), 0, s, ga);
+    launch_layout<bf16>(tiled, a_km, b_km, ga, s);
+  else if (dtype == ZK_F16)
+    launch_layout<f16>(tiled, a_km, b_km, ga, s);
   else
-    hipLaunchKernelGGL((gemm::gemm_nt_kernel<f16, 0>), dim3(static_cast<unsigned>(nwg)),
-                       dim3(256), 0, s, ga);
-  return launch_status("zk_gemm_nt");
+    launch_layout<float>(false, a_km, b_km, ga, s);
+  return launch_status("zk_gemm");
+}
+
+extern "C" int zk_gemm_nt(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
+                          int64_t ldc, const void* r, int64_t ldr, int64_t M, int64_t N,
+                          int64_t K, int dtype, zk_stream_t stream) {
+  return zk_gemm(a, lda, 0, b, ldb, 0, c, ldc, r, ldr, M, N, K, dtype, stream);
 }
 
 namespace zk {
@@ -479,11 +783,11 @@ int zk_gemm_swiglu_tiled(const void* x, int64_t ld_x, const void* w_gate, const 
   const int64_t nwg = (M / gemm::BM) * (2 * F / gemm::BN);
   hipStream_t s = as_stream(stream);
   if (dtype == ZK_BF16)
-    hipLaunchKernelGGL((gemm::gemm_nt_kernel<bf16, 1>), dim3(static_cast<unsigned>(nwg)),
-                       dim3(256), 0, s, ga);
+    hipLaunchKernelGGL((gemm::gemm_tiled_kernel<bf16, 1, false, false>),
+                       dim3(static_cast<unsigned>(nwg)), dim3(256), 0, s, ga);
   else
-    hipLaunchKernelGGL((gemm::gemm_nt_kernel<f16, 1>), dim3(static_cast<unsigned>(nwg)),
-                       dim3(256), 0, s, ga);
+    hipLaunchKernelGGL((gemm::gemm_tiled_kernel<f16, 1, false, false>),
+                       dim3(static_cast<unsigned>(nwg)), dim3(256), 0, s, ga);
   return launch_status("zk_gemm_swiglu");
 }
 

@@ -194,23 +194,80 @@ def swiglu_bwd(dz: torch.Tensor, gate: torch.Tensor, up: torch.Tensor,
 
 
 def gemm_nt_supported(M: int, N: int, K: int) -> bool:
-    """Whether zk_gemm_nt takes an [M, K] x [N, K]^T product (M, N multiples
-    of 256, K a multiple of 128 and at least 256)."""
+    """Whether an [M, K] x [N, K]^T product is on the MFMA pipeline's grid
+    (M, N multiples of 256, K a multiple of 128 and at least 256)."""
     return bool(lib().zk_gemm_nt_supported(M, N, K))
+
+
+def _gemm_operand(name: str, t: torch.Tensor):
+    """(rows, cols, leading dimension) of a 2-D operand with unit column stride
+    and non-overlapping rows."""
+    if t.dim() != 2:
+        raise ValueError(f"gemm: {name} must be 2-D, got shape {tuple(t.shape)}")
+    rows, cols = t.shape
+    if t.stride(1) != 1 and cols > 1:
+        raise ValueError(f"gemm: {name} needs unit column stride")
+    ld = t.stride(0) if rows > 1 else max(cols, 1)
+    if ld < cols:
+        raise ValueError(f"gemm: {name} has overlapping rows (row stride {ld} < {cols})")
+    return rows, cols, max(ld, 1)
+
+
+def gemm(a: torch.Tensor, b: torch.Tensor, *, a_kmajor: bool = False, b_kmajor: bool = False,
+         residual: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """C = op(a) op(b)^T (+ residual) from the hand-written GEMMs (zk_gemm):
+    a is [M, K] (``a_kmajor``: [K, M]) and b is [N, K] (``b_kmajor``:
+    [K, N]), each with unit column stride -- so x W^T is gemm(x, W), dY W is
+    gemm(dY, W, b_kmajor=True) and dY^T X is gemm(dY, X, a_kmajor=True,
+    b_kmajor=True), all on the tensors as stored.  bf16 / fp16 (fp32
+    accumulation, one rounding) or fp32; every tensor shares the dtype.
+    ``out`` / ``residual``: [M, N] with unit column stride."""
+    dev = _require_gpu(a, b, residual, out)
+    if a.dtype != b.dtype or a.dtype not in (torch.float32, *_LOWP):
+        raise ValueError(f"gemm: a and b must share a float dtype, got {a.dtype} and {b.dtype}")
+    ra, ca, lda = _gemm_operand("a", a)
+    rb, cb, ldb = _gemm_operand("b", b)
+    M, K = (ca, ra) if a_kmajor else (ra, ca)
+    N, Kb = (cb, rb) if b_kmajor else (rb, cb)
+    if Kb != K:
+        raise ValueError(f"gemm: reduction sizes differ ({K} and {Kb}) for a {tuple(a.shape)} "
+                         f"(k-major {a_kmajor}) and b {tuple(b.shape)} (k-major {b_kmajor})")
+    if out is None:
+        out = torch.empty(M, N, device=dev, dtype=a.dtype)
+    if out.shape != (M, N) or out.dtype != a.dtype:
+        raise ValueError(f"gemm: out must be [{M}, {N}] of the operands' dtype")
+    _, _, ldc = _gemm_operand("out", out)
+    ldr = 0
+    if residual is not None:
+        if residual.shape != (M, N) or residual.dtype != a.dtype:
+            raise ValueError(f"gemm: residual must be [{M}, {N}] of the operands' dtype")
+        _, _, ldr = _gemm_operand("residual", residual)
+    check(lib().zk_gemm(ptr(a), lda, int(a_kmajor), ptr(b), ldb, int(b_kmajor), ptr(out), ldc,
+                        ptr(residual) if residual is not None else None, ldr, M, N, K,
+                        dtype_code(a.dtype), stream_handle(dev)), "zk_gemm")
+    return out
+
+
+def gemm_path(M: int, N: int, K: int, lda: int, ldb: int, ldc: int, dtype: torch.dtype,
+              a_kmajor: bool = False, b_kmajor: bool = False, ldr: int = -1) -> str:
+    """Which kernel zk_gemm runs for a launch with 16-byte aligned pointers:
+    "tiled" (the 256 x 256 MFMA pipeline) or "general" (host-only query)."""
+    code = lib().zk_gemm_path(M, N, K, lda, int(a_kmajor), ldb, int(b_kmajor), ldc, ldr,
+                              dtype_code(dtype))
+    check(code if code < 0 else 0, "zk_gemm_path")
+    return "tiled" if code == 1 else "general"
 
 
 def gemm_nt(a: torch.Tensor, b: torch.Tensor, residual: torch.Tensor | None = None,
             out: torch.Tensor | None = None) -> torch.Tensor:
-    """a @ b.T (+ residual) from the hand-written MFMA GEMM: a [M, K] and
-    b [N, K] with unit column stride (contiguous along the reduction), 2-byte
-    dtypes; fp32 accumulation and one rounding.  ``out`` / ``residual``:
-    [M, N] with unit column stride."""
+    """a @ b.T (+ residual): a [M, K] and b [N, K] with unit column stride
+    (contiguous along the reduction); zk_gemm_nt."""
     dev = _require_gpu(a, b, residual, out)
     if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[1]:
         raise ValueError(f"gemm_nt: a [M, K] and b [N, K] expected, got {tuple(a.shape)} and "
                          f"{tuple(b.shape)}")
-    if a.dtype != b.dtype or a.dtype not in (torch.bfloat16, torch.float16):
-        raise ValueError("gemm_nt: a and b must share a 2-byte dtype")
+    if a.dtype != b.dtype or a.dtype not in (torch.float32, *_LOWP):
+        raise ValueError("gemm_nt: a and b must share a float dtype")
     M, K = a.shape
     N = b.shape[0]
     lda = _row_view_check("a", a)

@@ -3,9 +3,9 @@
 One autograd node per layer: the whole of LlamaDecoderLayer.forward
 (models/llama_simple.py:456-479) -- RMSNorm, the q|k|v projection as ONE GEMM,
 RoPE, flash attention (GQA, causal / sliding window), o_proj, the residual
-add fused into the second RMSNorm, gate|up as ONE GEMM, SwiGLU, down with the
-residual folded into the GEMM (addmm) -- and its backward, which writes every weight
-gradient straight into one flat gradient buffer laid out like the flat
+add fused into the second RMSNorm, gate|up as ONE GEMM with SwiGLU in its
+epilogue, down with the residual folded into the GEMM -- and its backward, which
+writes every weight gradient straight into one flat gradient buffer laid out like the flat
 parameter (q, k, v, o, gate, up, down, ln1, ln2 -- the registration order the
 reference's FSDP flat parameter uses, zorse_utils/pipeline.py:120-148).
 
@@ -95,29 +95,35 @@ class FlatViews:
         self.ln2 = flat[o["ln2"][0]:o["ln2"][1]]
 
 
-# Which GEMM runs the projections (zk_gemm_nt for the products whose shape it
-# takes, torch.mm / addmm -- hipBLASLt -- for the rest):
-#   "auto" (default): the hand-written kernel for the forward q|k|v, o_proj and
-#       down_proj (with its residual) products -- and gate|up, through the
-#       fused SwiGLU GEMM below -- hipBLASLt for the backward: in the 7B stage
-#       each of those forwards measured equal on either kernel, each backward
-#       product faster on hipBLASLt;
-#   "hip": the hand-written kernel for every product (the stage ~2 % slower);
-#   "hipblaslt": hipBLASLt for every product (and a separate SwiGLU pass).
-_GEMM_BACKENDS = ("auto", "hip", "hipblaslt")
-_AUTO_HIP_ROLES = ("qkv", "o", "down")
-_gemm_backend = os.environ.get("ZORSE_GEMM", "auto")
-if _gemm_backend not in _GEMM_BACKENDS:
-    raise ValueError(f"ZORSE_GEMM must be one of {_GEMM_BACKENDS}, got {_gemm_backend!r}")
+# Every projection product runs on the hand-written GEMMs (zk_gemm) with the
+# operands as the layer holds them: the forward x W^T and the backward's
+# input gradients dY W (W read K-major) and weight gradients dY^T X (both
+# token-major activations read K-major) -- no operand is transposed in
+# memory, and no product goes to a library GEMM.
 
 
-# gate|up GEMM with the SwiGLU activation in its epilogue (zk_gemm_swiglu on
-# the 256 x 256 pipeline: writes g, u, z and z^T in one pass) wherever that
-# pipeline takes the shape, with the "auto" and "hip" GEMM backends; otherwise
-# the GEMM and a separate SwiGLU pass.  On by default: in the 7B stage it
-# measured equal to hipBLASLt's GEMM plus the SwiGLU pass (43.28 / 43.30
-# against 43.25 / 43.26 ms/step); ZORSE_FUSED_MLP=0 or set_fused_gate_up(False)
-# turns it off.
+def _linear(x, w, residual=None):
+    """x W^T (+ residual, one rounding): the nn.Linear forward."""
+    return K.gemm(x, w, residual=residual)
+
+
+def _dgrad(dy, w):
+    """dy W: the input gradient of y = x W^T, W [out, in] read as stored."""
+    return K.gemm(dy, w, b_kmajor=True)
+
+
+def _wgrad(dy, x, out):
+    """out = dy^T x: the weight gradient of y = x W^T, from the token-major
+    dy [T, out] and x [T, in] as stored."""
+    K.gemm(dy, x, a_kmajor=True, b_kmajor=True, out=out)
+
+
+# gate|up GEMM with the SwiGLU activation in its epilogue (zk_gemm_swiglu:
+# writes g, u and z in one pass) for 2-byte types; otherwise the GEMM and a
+# separate SwiGLU pass.  On by default: in the 7B stage it measured equal to
+# the GEMM plus the SwiGLU pass; ZORSE_FUSED_MLP=0 or set_fused_gate_up(False)
+# turns it off (the separate pass computes SiLU with the IEEE exp and
+# division, the fused epilogue with the hardware exp2 and reciprocal).
 _fused_gate_up = os.environ.get("ZORSE_FUSED_MLP", "1") != "0"
 
 
@@ -128,112 +134,12 @@ def set_fused_gate_up(enable: bool) -> bool:
     return prev
 
 
-def set_gemm_backend(name: str) -> str:
-    """Select the projection GEMMs ("auto", "hip" or "hipblaslt"); returns the
-    previous setting."""
-    global _gemm_backend
-    if name not in _GEMM_BACKENDS:
-        raise ValueError(f"GEMM backend must be one of {_GEMM_BACKENDS}, got {name!r}")
-    prev, _gemm_backend = _gemm_backend, name
-    return prev
-
-
-def gemm_backend() -> str:
-    return _gemm_backend
-
-
-def _hip_nt(a, b_rows, residual=None, out=None, role="bwd"):
-    """a @ b_rows^T (+ residual) through zk_gemm_nt when the backend gives it
-    this product (``role``: "qkv", "o", "gu", "down" for the forward
-    projections, "bwd" for the backward's) and the kernel takes the shape and
-    layout (2-byte dtype, both operands contiguous along the reduction); None
-    otherwise."""
-    if _gemm_backend == "hipblaslt" or (_gemm_backend == "auto" and role not in _AUTO_HIP_ROLES):
-        return None
-    if a.dtype not in (torch.bfloat16, torch.float16):
-        return None
-    if a.stride(1) != 1 or b_rows.stride(1) != 1:
-        return None
-    if not K.gemm_nt_supported(a.shape[0], b_rows.shape[0], a.shape[1]):
-        return None
-    return K.gemm_nt(a, b_rows, residual=residual, out=out)
-
-
-def _mm(a, b, role, out=None):
-    """a @ b for the forward projection ``role``, b = W^T (a transposed view)."""
-    got = _hip_nt(a, b.t(), out=out, role=role)
-    if got is not None:
-        return got
-    return torch.mm(a, b) if out is None else torch.mm(a, b, out=out)
-
-
-def _addmm(r, a, b, role):
-    """r + a @ b with one rounding (the down projection with the residual)."""
-    got = _hip_nt(a, b.t(), residual=r, role=role)
-    if got is not None:
-        return got
-    return torch.addmm(r, a, b)
-
-
-# Tokens from which backward GEMMs go through explicit transposes.  hipBLASLt's
-# fastest layout reads both operands along the reduction (K-contiguous); at
-# 7B shapes and 4096 tokens it runs 1.1-1.35x faster than the layouts with one
-# strided operand, more than the transposes cost.
-_TRANSPOSE_MIN_TOKENS = 1024
-
-
-# The attention backward writes dqkv^T (the q|k|v weight gradient's operand)
-# from its epilogues instead of a separate transpose of dqkv, and the forward
-# writes O^T (the o_proj weight gradient's) next to O.
-_ATTN_WRITES_DQKV_T = True
-_ATTN_WRITES_O_T = True
-
-
-def _transposing(t):
-    if t.dtype not in (torch.bfloat16, torch.float16):
-        return False
-    # the hand-written GEMM reads both operands along the reduction only
-    return t.shape[0] >= _TRANSPOSE_MIN_TOKENS or _gemm_backend == "hip"
-
-
-def _wgrad(dy, x, out, dyt=None, xt=None):
-    """out = dy^T x (the weight gradient of y = x W^T).  For 2-byte types and
-    long token counts dy^T and x^T are materialised first (zk_transpose, or
-    supplied by the kernel that produced them) so that the GEMM streams both
-    operands along the token reduction.  ``x`` may be None when ``xt`` is given."""
-    if _transposing(dy):
-        if dyt is None:
-            dyt = K.transpose(dy)
-        if xt is None:
-            xt = K.transpose(x)
-        if _hip_nt(dyt, xt, out=out) is None:
-            torch.mm(dyt, xt.t(), out=out)
-        del dyt, xt
-    else:
-        torch.mm(dy.t(), x, out=out)
-
-
-def _swiglu_transposed(gu, F):
-    """True when the SwiGLU kernels also write the transposed copies the MLP's
-    weight gradients use (token-contiguous operands, 2-byte types; the fused
-    kernels need rows and columns in multiples of 8)."""
-    return _transposing(gu) and gu.shape[0] % 8 == 0 and F % 8 == 0
-
-
-def _dgrad(dy, wmat, transpose_weight, wt=None):
-    """dy W (the input gradient of y = x W^T).  For 2-byte types and long
-    token counts the GEMM reads W^T [in, out] so that both operands stream
-    along the reduction: ``wt`` when the optimizer keeps it current, else, with
-    ``transpose_weight``, a transpose made here -- the layer asks for that
-    where the reduction is over the hidden size (o_proj, down_proj), for which
-    the transpose is cheap relative to the GEMM it speeds up."""
-    if _transposing(dy):
-        if wt is None and (transpose_weight or _gemm_backend == "hip"):
-            wt = K.transpose(wmat)
-        if wt is not None:
-            got = _hip_nt(dy, wt)
-            return got if got is not None else torch.mm(dy, wt.t())
-    return torch.mm(dy, wmat)
+def _fused_gate_up_takes(n2, F):
+    """zk_gemm_swiglu's conditions: 2-byte type, K a multiple of 64, tokens
+    and F multiples of 8."""
+    T, h = n2.shape
+    return (_fused_gate_up and n2.dtype in (torch.bfloat16, torch.float16)
+            and h % 64 == 0 and T % 8 == 0 and F % 8 == 0)
 
 
 def _rope_for(S, spec, dtype, device, positions):
@@ -261,7 +167,7 @@ def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=Non
     d, Hq, Hkv = spec.head_dim, spec.heads, spec.kv_heads
     x2 = x.reshape(T, h)
     n1, rstd1, _ = K.rmsnorm_fwd(x2, w.ln1, spec.eps)
-    qkv = _mm(n1, w.qkv.t(), "qkv")                  # [T, (Hq + 2 Hkv) d]
+    qkv = _linear(n1, w.qkv)                          # [T, (Hq + 2 Hkv) d]
     q = qkv[:, :spec.q_dim].view(B, S, Hq, d)
     k = qkv[:, spec.q_dim:spec.q_dim + spec.kv_dim].view(B, S, Hkv, d)
     v = qkv[:, spec.q_dim + spec.kv_dim:].view(B, S, Hkv, d)
@@ -269,41 +175,25 @@ def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=Non
     K.rope_(q, k, cos, sin, positions=positions, interleaved=spec.interleaved_rope)
     hit = attn_cache.take() if attn_cache is not None else None
     if hit is not None:
-        o, lse, o2t = hit
+        o, lse = hit
     else:
-        # O^T [Hq d, T] for the o_proj weight gradient when it takes the
-        # transposed form (see _wgrad)
-        o2t = None
-        if _ATTN_WRITES_O_T and _transposing(x2) and S % 8 == 0:
-            o2t = torch.empty(spec.q_dim, T, device=x.device, dtype=x.dtype)
-        o, lse = K.attn_fwd(q, k, v, causal=spec.causal, window=spec.window, out_t=o2t)
+        o, lse = K.attn_fwd(q, k, v, causal=spec.causal, window=spec.window)
         if attn_cache is not None:
-            attn_cache.put(o, lse, o2t)
+            attn_cache.put(o, lse)
     o2 = o.view(T, spec.q_dim)
     # o_proj, then residual add fused into the second RMSNorm (one pass writes
     # hdn = x + round(o_proj) and its normalisation, the reference's order)
-    attn_out = _mm(o2, w.o.t(), "o")
+    attn_out = _linear(o2, w.o)
     n2, rstd2, hdn = K.rmsnorm_fwd(attn_out, w.ln2, spec.eps, residual=x2)
     F = spec.ffn
-    if (_fused_gate_up and _gemm_backend != "hipblaslt"
-            and n2.dtype in (torch.bfloat16, torch.float16) and K.gemm_nt_supported(T, 2 * F, h)):
-        # one GEMM writes gate | up (kept for the backward), z and, when the
-        # down projection's weight gradient takes the transposed form, z^T
-        want_t = _transposing(n2) and F % 8 == 0
-        res = K.gemm_swiglu(n2, w.gu[:F], w.gu[F:], transposed=want_t)
-        gu, z = res[0], res[1]
-        zs = res[2] if want_t else z
+    if _fused_gate_up_takes(n2, F):
+        # one GEMM writes gate | up (kept for the backward) and z
+        gu, z = K.gemm_swiglu(n2, w.gu[:F], w.gu[F:])
     else:
-        gu = _mm(n2, w.gu.t(), "gu")                 # [T, 2F] = gate | up
-        if _swiglu_transposed(gu, F):
-            # z^T is what down_proj's weight gradient reads; z itself is only
-            # needed for the GEMM below
-            z, zs = K.swiglu_fwd_t(gu[:, :F], gu[:, F:])
-        else:
-            z = zs = K.swiglu_fwd(gu[:, :F], gu[:, F:])
-    out = _addmm(hdn, z, w.down.t(), "down")         # residual + down(z)
-    del z
-    saved = (x2, n1, rstd1, qkv, o2, o2t, lse, hdn, n2, rstd2, gu, zs, positions)
+        gu = _linear(n2, w.gu)                       # [T, 2F] = gate | up
+        z = K.swiglu_fwd(gu[:, :F], gu[:, F:])
+    out = _linear(z, w.down, residual=hdn)           # residual + down(z)
+    saved = (x2, n1, rstd1, qkv, o2, lse, hdn, n2, rstd2, gu, z, positions)
     return out.view(B, S, h), saved
 
 
@@ -315,12 +205,10 @@ BEFORE_ATTENTION_BACKWARD: list = []
 
 
 def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
-                   grad_flat: torch.Tensor, wt: dict | None = None) -> torch.Tensor:
+                   grad_flat: torch.Tensor) -> torch.Tensor:
     """Backward of layer_forward; writes weight grads into ``grad_flat``
-    (compute dtype, flat layout) and returns dx.  ``wt`` (optional): W^T of
-    the qkv, o, gu and down weights, current with ``w``."""
-    wt = wt or {}
-    x2, n1, rstd1, qkv, o2, o2t, lse, hdn, n2, rstd2, gu, zs, positions = saved
+    (compute dtype, flat layout) and returns dx."""
+    x2, n1, rstd1, qkv, o2, lse, hdn, n2, rstd2, gu, z, positions = saved
     T, h = x2.shape
     B = dout.shape[0]
     S = T // B
@@ -329,29 +217,20 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
     dout2 = dout.reshape(T, h)
 
     # MLP: out = hdn + z W_down^T
-    dz = _dgrad(dout2, w.down, True, wt.get("down"))  # [T, F]
-    fused_t = _swiglu_transposed(gu, F)
-    if fused_t:                                      # zs = z^T
-        _wgrad(dout2, None, g.down, xt=zs)
-    else:                                            # zs = z
-        _wgrad(dout2, zs, g.down)
+    dz = _dgrad(dout2, w.down)                       # [T, F]
+    _wgrad(dout2, z, g.down)
     dgu = torch.empty_like(gu)
-    dgut = None
-    if fused_t:
-        dgut = torch.empty(2 * F, T, device=gu.device, dtype=gu.dtype)
-        K.swiglu_bwd_t(dz, gu[:, :F], gu[:, F:], dgu[:, :F], dgu[:, F:], dgut[:F], dgut[F:])
-    else:
-        K.swiglu_bwd(dz, gu[:, :F], gu[:, F:], dgu[:, :F], dgu[:, F:])
+    K.swiglu_bwd(dz, gu[:, :F], gu[:, F:], dgu[:, :F], dgu[:, F:])
     del dz
-    dn2 = _dgrad(dgu, w.gu, False, wt.get("gu"))     # [T, h]
-    _wgrad(dgu, n2, g.gu, dyt=dgut)
-    del dgu, dgut
+    dn2 = _dgrad(dgu, w.gu)                          # [T, h]
+    _wgrad(dgu, n2, g.gu)
+    del dgu
     dh, _ = K.rmsnorm_bwd(dn2, hdn, w.ln2, rstd2, dres=dout2, dw=g.ln2)
     del dn2
 
     # attention: hdn = x + o W_o^T
-    do2 = _dgrad(dh, w.o, True, wt.get("o"))         # [T, Hq d]
-    _wgrad(dh, o2, g.o, xt=o2t)
+    do2 = _dgrad(dh, w.o)                            # [T, Hq d]
+    _wgrad(dh, o2, g.o)
     q = qkv[:, :spec.q_dim].view(B, S, Hq, d)
     k = qkv[:, spec.q_dim:spec.q_dim + spec.kv_dim].view(B, S, Hkv, d)
     v = qkv[:, spec.q_dim + spec.kv_dim:].view(B, S, Hkv, d)
@@ -359,24 +238,17 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
     dq = dqkv[:, :spec.q_dim].view(B, S, Hq, d)
     dk = dqkv[:, spec.q_dim:spec.q_dim + spec.kv_dim].view(B, S, Hkv, d)
     dv = dqkv[:, spec.q_dim + spec.kv_dim:].view(B, S, Hkv, d)
-    # dqkv^T (the weight gradient's operand) comes from the attention
-    # kernels' epilogues when the GEMM takes the transposed form
-    dqkvt = None
-    if _ATTN_WRITES_DQKV_T and _transposing(qkv) and S % 8 == 0:
-        dqkvt = torch.empty(qkv.shape[1], T, device=qkv.device, dtype=qkv.dtype)
     for fn in list(BEFORE_ATTENTION_BACKWARD):
         fn()
     # the attention backward also takes dq / dk back through RoPE's rotation
     cos, sin = _rope_for(S, spec, dout.dtype, dout.device, positions)
-    kv0, kv1 = spec.q_dim, spec.q_dim + spec.kv_dim
     K.attn_bwd(q, k, v, o2.view(B, S, Hq, d), do2.view(B, S, Hq, d), lse,
                causal=spec.causal, window=spec.window, dq=dq, dk=dk, dv=dv,
-               rope=(cos, sin, positions, spec.interleaved_rope),
-               transposed=None if dqkvt is None else (dqkvt[:kv0], dqkvt[kv0:kv1], dqkvt[kv1:]))
+               rope=(cos, sin, positions, spec.interleaved_rope))
     del do2
-    dn1 = _dgrad(dqkv, w.qkv, False, wt.get("qkv"))  # [T, h]
-    _wgrad(dqkv, n1, g.qkv, dyt=dqkvt)
-    del dqkv, dqkvt
+    dn1 = _dgrad(dqkv, w.qkv)                        # [T, h]
+    _wgrad(dqkv, n1, g.qkv)
+    del dqkv
     dx, _ = K.rmsnorm_bwd(dn1, x2, w.ln1, rstd1, dres=dh, dw=g.ln1)
     return dx.view(B, S, h)
 
@@ -426,24 +298,23 @@ class AttentionCache:
                      x._version) + wkey
 
     def take(self):
-        """(o, lse, o_t) of the bound key's entry, removed, or None."""
+        """(o, lse) of the bound key's entry, removed, or None."""
         hit = self._entries.pop(self._key, None)
         if hit is None:
             return None
         self._storage = None  # the input's storage is no longer needed here
         return hit[1:]
 
-    def put(self, o, lse, o_t=None):
-        """Records O, its LSE and (when the forward wrote it) O^T."""
-        self._entries[self._key] = (self._storage, o, lse, o_t)
+    def put(self, o, lse):
+        """Records O and its LSE."""
+        self._entries[self._key] = (self._storage, o, lse)
 
 
 class DecoderLayerFunction(torch.autograd.Function):
     """autograd node of one decoder layer: inputs (x, flat_param)."""
 
     @staticmethod
-    def forward(ctx, x, flat_param, spec, weights_lowp, attn_cache=None, wt=None,
-                positions=None):
+    def forward(ctx, x, flat_param, spec, weights_lowp, attn_cache=None, positions=None):
         w_flat = weights_lowp if weights_lowp is not None else flat_param
         w = FlatViews(spec, w_flat)
         if attn_cache is not None:
@@ -451,7 +322,6 @@ class DecoderLayerFunction(torch.autograd.Function):
         with torch.autocast("cuda", enabled=False):
             out, saved = layer_forward(x.contiguous(), w, spec, attn_cache, positions)
         ctx.spec = spec
-        ctx.wt = wt
         ctx.param_dtype = flat_param.dtype
         ctx.positions = saved[-1]
         ctx.save_for_backward(w_flat, *saved[:-1])
@@ -466,7 +336,7 @@ class DecoderLayerFunction(torch.autograd.Function):
         dout = dout.to(w_flat.dtype).contiguous()
         grad_flat = torch.empty(spec.numel, device=dout.device, dtype=w_flat.dtype)
         with torch.autocast("cuda", enabled=False):
-            dx = layer_backward(dout, saved, w, spec, grad_flat, ctx.wt)
+            dx = layer_backward(dout, saved, w, spec, grad_flat)
         if ctx.param_dtype != grad_flat.dtype:
             grad_flat = grad_flat.to(ctx.param_dtype)
-        return dx, grad_flat, None, None, None, None, None
+        return dx, grad_flat, None, None, None, None

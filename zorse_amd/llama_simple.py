@@ -163,38 +163,6 @@ class FlatDecoderLayer(nn.Module):
         # AttentionCache shared by the two forwards of a recomputed micro-batch
         # (set by the stage runner; None = always compute attention)
         self.attn_cache = None
-        # transposed compute copies of the projection weights, written by the
-        # optimizer step (enable_transposed_weights), and the parameter
-        # version they belong to
-        self._wt = None
-        self._wt_version = None
-
-    def enable_transposed_weights(self, optimizer) -> None:
-        """Have ``optimizer`` (a FusedAdamW holding ``flat_param``) write, in
-        its step, transposed copies of the q|k|v, o, gate|up and down weights
-        (W^T, [in, out]); the backward's input-gradient GEMMs then read both
-        operands along their reduction without transposing the weights.  Only
-        for a bf16 / fp16 flat parameter.  The copies are used while the
-        parameter's version is the one the last step left."""
-        p, sp, o = self.flat_param, self.spec, self._offsets
-        mats = {"qkv": (o["q"][0], sp.q_dim + 2 * sp.kv_dim, sp.hidden),
-                "o": (o["o"][0], sp.hidden, sp.q_dim),
-                "gu": (o["gate"][0], 2 * sp.ffn, sp.hidden),
-                "down": (o["down"][0], sp.hidden, sp.ffn)}
-        self._wt = {}
-        for name, (off, rows, cols) in mats.items():
-            self._wt[name] = torch.empty(cols, rows, dtype=p.dtype, device=p.device)
-            optimizer.add_transposed_copy(p, off, rows, cols, self._wt[name])
-        self._wt_version = None
-
-        def stepped(param, layer=self):
-            layer._wt_version = param._version
-        optimizer.add_step_hook(p, stepped)
-
-    def _transposed_weights(self):
-        if self._wt is not None and self._wt_version == self.flat_param._version:
-            return self._wt
-        return None
 
     # -- parameters -----------------------------------------------------------
     def param_view(self, name: str) -> torch.Tensor:
@@ -253,10 +221,8 @@ class FlatDecoderLayer(nn.Module):
         if cdt == torch.float32 and torch.is_autocast_enabled("cuda"):
             cdt = torch.get_autocast_dtype("cuda")
             x = x.to(cdt)
-        wt = self._transposed_weights() if cdt == self.flat_param.dtype else None
         return DecoderLayerFunction.apply(x, self.flat_param, self.spec,
-                                          self._compute_weights(cdt), self.attn_cache, wt,
-                                          positions)
+                                          self._compute_weights(cdt), self.attn_cache, positions)
 
     # position_ids tensors known to hold arange(S) (the Block's cached ids):
     # recognised by identity, so the common call costs no check

@@ -30,24 +30,7 @@ class FusedAdamW(torch.optim.Optimizer):
             raise ValueError(f"invalid betas {betas}")
         super().__init__(params, dict(lr=lr, betas=tuple(betas), eps=eps,
                                       weight_decay=weight_decay))
-        self._tcopies = {}      # param -> [(offset, rows, cols, out)]
         self._step_hooks = {}   # param -> [callable(param)]
-
-    def add_transposed_copy(self, p: torch.Tensor, offset: int, rows: int, cols: int,
-                            out: torch.Tensor) -> None:
-        """Each step also writes the updated elements offset .. offset + rows * cols
-        of ``p`` (a row-major [rows, cols] matrix), rounded to ``p``'s dtype,
-        transposed into ``out`` ([cols, rows]) -- in the same kernel pass that
-        updates them.  ``p`` must be a bf16 / fp16 compute copy (fp32 master in
-        the optimizer state); regions must not overlap."""
-        if p.dtype not in (torch.bfloat16, torch.float16):
-            raise ValueError("transposed copies are kept for bf16 / fp16 parameters only")
-        if out.shape != (cols, rows) or out.dtype != p.dtype or out.stride(1) != 1:
-            raise ValueError("out must be [cols, rows] of the parameter's dtype")
-        if offset < 0 or offset + rows * cols > p.numel():
-            raise ValueError("matrix region outside the parameter")
-        self._tcopies.setdefault(p, []).append((int(offset), int(rows), int(cols), out))
-        self._tcopies[p].sort(key=lambda r: r[0])
 
     def add_step_hook(self, p: torch.Tensor, fn) -> None:
         """``fn(p)`` runs after every step of ``p`` (after its version bump)."""
@@ -104,34 +87,15 @@ class FusedAdamW(torch.optim.Optimizer):
         master = st.get("master")
         hyper = dict(lr=group["lr"], beta1=b1, beta2=b2, eps=group["eps"],
                      weight_decay=group["weight_decay"], step=st["step"])
-        regions = self._tcopies.get(p) if master is not None else None
-        if not regions:
-            K.adamw_step(master if master is not None else p.view(-1),
-                         p.grad.view(-1), st["exp_avg"], st["exp_avg_sq"],
-                         lowp_out=p.view(-1) if master is not None else None, **hyper)
-        else:
-            self._step_regions(p, st, master, regions, hyper)
+        K.adamw_step(master if master is not None else p.view(-1),
+                     p.grad.view(-1), st["exp_avg"], st["exp_avg_sq"],
+                     lowp_out=p.view(-1) if master is not None else None, **hyper)
         # the kernel wrote p through a raw pointer: advance its version
         # counter as an in-place torch op would, so caches keyed on it
         # (compute-dtype weight copies, attention caches) see the update
         torch.autograd.graph.increment_version(p)
         for fn in self._step_hooks.get(p, ()):
             fn(p)
-
-    @staticmethod
-    def _step_regions(p, st, master, regions, hyper):
-        """The step over the whole shard (one flat launch, which also writes the
-        rounded compute copy), then each registered matrix's transposed copy
-        out of that compute copy.  zk_adamw_step_t does both in one launch
-        over 64 x 128 tiles; measured in the 8-layer 7B stage, where the step
-        runs beside the attention backward and the next GEMMs, the flat
-        kernel plus transposes ran 1.05 ms per step faster (43.2 against
-        44.2 ms), though alone the two forms differ by 0.08 ms per layer."""
-        flat = p.view(-1)
-        K.adamw_step(master, p.grad.view(-1), st["exp_avg"], st["exp_avg_sq"], lowp_out=flat,
-                     **hyper)
-        for off, rows, cols, out in regions:
-            K.transpose(flat[off:off + rows * cols].view(rows, cols), out=out)
 
     def master_param(self, p: torch.Tensor) -> torch.Tensor:
         """fp32 master of ``p`` (``p`` itself when it is fp32)."""

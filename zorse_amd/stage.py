@@ -9,9 +9,6 @@ Reference behaviour reproduced (single GPU, no communication):
     waits for the compute stream (utils/patch.py:76-154, the
     ``--optimizer_in_backwards`` path built at zorse_utils/pipeline.py:
     150-181), then the gradient is released;
-  * with ``transposed_weights`` (the default) each bf16 / fp16 layer's step
-    also writes transposed copies of its projection weights, which the next
-    backward's input-gradient GEMMs read along their reduction;
   * ``offload_inputs=True`` (recompute mode) keeps each layer's input in
     pinned host memory between the two forwards: D2H during the forward and
     H2D one layer ahead during the backward, on a copy stream (the
@@ -48,8 +45,7 @@ def _call(layer: nn.Module, x: torch.Tensor) -> torch.Tensor:
 class StageRunner:
     def __init__(self, layers: Sequence[nn.Module], lr=1e-4, betas=(0.9, 0.95), eps=1e-8,
                  weight_decay=0.1, optimizer_in_backwards=True, recompute=False,
-                 cache_attention=True, optimizer_overlap="attention", transposed_weights=True,
-                 offload_inputs=False):
+                 cache_attention=True, optimizer_overlap="attention", offload_inputs=False):
         if optimizer_overlap not in ("attention", "immediate"):
             raise ValueError(f"optimizer_overlap {optimizer_overlap!r}: 'attention' or 'immediate'")
         if offload_inputs and not recompute:
@@ -95,13 +91,6 @@ class StageRunner:
             params = [p for p in layer.parameters() if p.requires_grad]
             opt = FusedAdamW(params, lr=lr, betas=betas, eps=eps, weight_decay=weight_decay)
             self.optimizers.append(opt)
-            if transposed_weights:
-                # the step also writes W^T of the projections for the next
-                # backward's input-gradient GEMMs (bf16 / fp16 parameters)
-                for m in layer.modules():
-                    if hasattr(m, "enable_transposed_weights") and \
-                            m.flat_param.dtype in (torch.bfloat16, torch.float16):
-                        m.enable_transposed_weights(opt)
             if optimizer_in_backwards:
                 for p in params:
                     self._hooks.append(p.register_post_accumulate_grad_hook(
