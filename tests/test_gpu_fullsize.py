@@ -27,7 +27,7 @@ import pytest
 import torch
 
 from oracle import decoder as O
-from tests._tol import assert_close, assert_loss, assert_matched
+from tests._tol import assert_close, assert_loss, assert_loss_literal, assert_matched
 
 pytestmark = pytest.mark.gpu
 
@@ -120,7 +120,24 @@ def test_layer_full_size(dev, name):
         a, b = offs[k]
         _close(layer.flat_param.grad[a:b].view(rg[k].shape), rg[k], dtype, "d" + k, lg[k])
     assert_loss(out, rout, lout, dout)
-    del rout, rdx, rg, lout, ldx, lg
+    del rdx, rg, lout, ldx, lg
+    # the last stage's tail on this layer's output: final RMSNorm, a
+    # vocabulary-32000 head and cross-entropy over uniform labels
+    # (models/llama_simple.py:559-561, zorse_utils/pipeline_schedule_v2.py:
+    # 181-184) -- a positive, well-conditioned loss, held to the literal 1e-3
+    # against the same tail on the fp32 oracle's output
+    from zorse_amd.functional import rms_norm
+    from zorse_amd.lm_head import lm_head_cross_entropy
+    V, h = 32000, s.hidden
+    gh = torch.Generator(device=dev).manual_seed(13)
+    head_w = (0.02 * torch.randn(V, h, generator=gh, device=dev)).to(dtype)
+    labels = torch.randint(0, V, (B, S), generator=gh, device=dev)
+    norm_w = (1 + 0.1 * torch.randn(h, generator=gh, device=dev)).to(dtype)
+    with torch.no_grad():
+        loss = lm_head_cross_entropy(rms_norm(out.detach(), norm_w, 1e-6), head_w, labels)
+        rloss = O.lm_head_ce(rout, norm_w.float(), head_w.float(), labels, 1e-6)
+    assert_loss_literal(loss, rloss, f"{name} CE loss through the output head")
+    del rout, head_w
     if name.startswith("cfg3"):
         # the cfg3 step: fused AdamW on the flat fp32 master shard
         from zorse_amd import kernels as K

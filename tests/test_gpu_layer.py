@@ -55,6 +55,12 @@ def _check_layer(layer, x, dout, dtype, what, rope="half"):
     out = layer(xg)[0]
     assert out.dtype == dtype and out.shape == x.shape
     out.backward(dout.to(xg.device))
+    return _compare_layer(layer, x, xg, out, dout, dtype, what, rope)
+
+
+def _compare_layer(layer, x, xg, out, dout, dtype, what, rope="half"):
+    """The checks of _check_layer on a forward / backward already run (out,
+    xg.grad, the layer's flat gradient)."""
     p = _oracle_params(layer, dtype)
     shape = _oracle_shape(layer)
     rout, rdx, rgrads = O.layer_fwd_bwd(x.double(), p, shape, dout.double(), rope=rope)
@@ -241,13 +247,17 @@ def test_layer_every_product_hand_written(dev, name, monkeypatch):
     monkeypatch.setattr(K, "gemm", gemm)
     monkeypatch.setattr(K, "gemm_swiglu", gemm_swiglu)
     monkeypatch.setattr(K, "transpose", no_transpose)
+    xg = x.to(dev).requires_grad_(True)
     with monkeypatch.context() as m:
         _forbid_library_products(m)
         prev = LY.set_fused_gate_up(True)
         try:
-            _check_layer(layer, x, dout, dtype, f"{name} hand-written GEMMs")
+            out = layer(xg)[0]
+            out.backward(dout.to(dev))
+            torch.cuda.synchronize()
         finally:
             LY.set_fused_gate_up(prev)
+    _compare_layer(layer, x, xg, out, dout, dtype, f"{name} hand-written GEMMs")
     # the layer step itself: 4 forward + 8 backward products (the oracle runs
     # on the CPU, outside these wrappers)
     assert len(calls) == 12, calls
@@ -531,15 +541,54 @@ def test_stage_no_transposes_no_library_gemm(dev, monkeypatch):
         assert torch.isfinite(l.flat_param).all() and not torch.equal(b, l.flat_param)
 
 
+def _check_stack_against_oracle(layers, before, xs, douts, captured, masters, dtype, what,
+                                lr=1e-4, betas=(0.9, 0.95), eps=1e-8, wd=0.1):
+    """A stack of layers run by the stage runner over len(xs) steps, against
+    the fp64 oracle: per step, layer and each of the nine parameter slices,
+    the gradient the optimizer consumed (``captured[step][i]``) against the
+    oracle's gradient of the stack at the weights that step saw
+    (``before[step][i]``, oracle parameter dicts), with the precision-matched
+    bar (plain PyTorch in ``dtype`` as the reference layer); after the last
+    step each fp32 master against the oracle's AdamW applied to the captured
+    gradients."""
+    shape = _oracle_shape(layers[0])
+    offs = layers[0].spec.offsets()
+    for step, (x, dout) in enumerate(zip(xs, douts)):
+        x, dout = x.detach().cpu(), dout.detach().cpu()
+        xr = x.double().requires_grad_(True)
+        prs = [{k: v.clone().requires_grad_(True) for k, v in p.items()} for p in before[step]]
+        pls = [{k: v.to(dtype).requires_grad_(True) for k, v in p.items()} for p in before[step]]
+        y, yl = xr, x
+        for pr, pl in zip(prs, pls):
+            y = O.decoder_layer(y, pr, shape)
+            yl = O.decoder_layer(yl, pl, shape, attn="flash")
+        y.backward(dout.double())
+        yl.backward(dout)
+        for i in range(len(layers)):
+            got = captured[step][i]
+            for k in O.PARAM_ORDER:
+                a, b = offs[k]
+                assert_matched(got[a:b].view(prs[i][k].shape), prs[i][k].grad, pls[i][k].grad,
+                               dtype, f"{what} step {step + 1} layer {i} d{k}")
+    for i, master in enumerate(masters):
+        p = O.flatten(before[0][i]).clone()
+        m, v = torch.zeros_like(p), torch.zeros_like(p)
+        for t in range(len(xs)):
+            O.adamw_step(p, captured[t][i].double().cpu(), m, v, t + 1, lr, betas[0], betas[1],
+                         eps, wd)
+        assert_close(master, p, torch.float32, f"{what} layer {i} master")
+
+
 @pytest.mark.parametrize("S", [256, 1024])
 def test_stage_recompute_attention_cache(dev, S):
     """Recompute mode (the reference pipeline's second forward inside the
     backward, zorse_utils/pipeline_schedule_v2.py:157-200): with the attention
     cache the re-forward launches no attention kernel, and every layer
     gradient is bit-identical to recompute without the cache and to the
-    single-forward path (the kernels are deterministic).  At 1024 tokens the
-    backward takes its transposed-operand form, so the cache also carries the
-    O^T the forward wrote."""
+    single-forward path (the kernels are deterministic); and the cached
+    recompute's gradients (each parameter slice) and fp32 masters against the
+    fp64 oracle.  1024 tokens run every GEMM on the tiled pipeline, 256 on
+    the masked kernel for the token-sized dimensions."""
     from zorse_amd import layer as L
     from zorse_amd.stage import StageRunner
     kw = dict(hidden_size=256, num_attention_heads=2, intermediate_size=512, rope_theta=1e4)
@@ -560,6 +609,7 @@ def test_stage_recompute_attention_cache(dev, S):
         for name, rc, cache in (("plain", False, False), ("recompute", True, False),
                                 ("cached", True, True)):
             layers = [_layer(kw, dev, param_dtype=dtype, seed=s) for s in (1, 2)]
+            before = [_oracle_params(l, dtype) for l in layers]
             grads = {}
             for i, l in enumerate(layers):
                 l.flat_param.register_post_accumulate_grad_hook(
@@ -569,7 +619,9 @@ def test_stage_recompute_attention_cache(dev, S):
             runner.step(x, dout)
             runner.wait_optimizer()
             torch.cuda.synchronize()
-            results[name] = (grads, calls["n"], [len(c) for c in runner.attn_caches])
+            masters = [o.master_param(l.flat_param) for o, l in zip(runner.optimizers, layers)]
+            results[name] = (grads, calls["n"], [len(c) for c in runner.attn_caches], layers,
+                             before, masters)
     finally:
         L.K.attn_fwd = real
     assert results["plain"][1] == 2 and results["recompute"][1] == 4
@@ -578,6 +630,10 @@ def test_stage_recompute_attention_cache(dev, S):
     for i in (0, 1):
         assert torch.equal(results["cached"][0][i], results["recompute"][0][i])
         assert torch.equal(results["cached"][0][i], results["plain"][0][i])
+    # and against the oracle, not only against the plain path
+    grads, _, _, layers, before, masters = results["cached"]
+    _check_stack_against_oracle(layers, [before], [x], [dout], [grads], masters, dtype,
+                                f"recompute S={S}")
 
 
 def test_stage_offload_inputs(dev):
@@ -585,8 +641,10 @@ def test_stage_offload_inputs(dev):
     buffers on mem_copy_stream, zorse_utils/pipeline_schedule_v2.py:119-136):
     each layer input goes D2H to pinned memory in the forward and returns H2D
     one layer ahead in the backward.  Over two steps the gradients and weights
-    are bit-identical to recompute without offload, and the attention cache
-    still hits across the round trip (one attention forward per layer)."""
+    are bit-identical to recompute without offload, the attention cache still
+    hits across the round trip (one attention forward per layer), and the
+    gradients of both steps (each parameter slice) and the fp32 masters agree
+    with the fp64 oracle of the three-layer stack."""
     from zorse_amd import layer as L
     from zorse_amd.stage import StageRunner
     kw = dict(hidden_size=256, num_attention_heads=2, intermediate_size=512, rope_theta=1e4)
@@ -612,8 +670,9 @@ def test_stage_offload_inputs(dev):
                     lambda p, i=i: grads.__setitem__(i, p.grad.detach().clone()))
             runner = StageRunner(layers, lr=1e-4, recompute=True, cache_attention=True,
                                  offload_inputs=off)
-            per_step = []
+            per_step, weights_seen = [], []
             for x, dout in zip(xs, douts):
+                weights_seen.append([_oracle_params(l, dtype) for l in layers])
                 calls["n"] = 0
                 torch.cuda.synchronize()
                 before = torch.cuda.memory_allocated()
@@ -626,7 +685,8 @@ def test_stage_offload_inputs(dev):
                 torch.cuda.synchronize()
                 per_step.append(({i: t.clone() for i, t in grads.items()}, calls["n"], held))
             weights = [l.flat_param.detach().clone() for l in layers]
-            results[name] = (per_step, weights, runner)
+            masters = [o.master_param(l.flat_param) for o, l in zip(runner.optimizers, layers)]
+            results[name] = (per_step, weights, runner, layers, weights_seen, masters)
     finally:
         L.K.attn_fwd = real
     off = results["offload"][2]
@@ -647,6 +707,10 @@ def test_stage_offload_inputs(dev):
             assert torch.equal(g_off[i], g_ref[i]), (step, i)
     for a, b in zip(results["offload"][1], results["recompute"][1]):
         assert torch.equal(a, b)
+    # and against the oracle: both steps' gradients and the masters after them
+    per_step, _, _, layers, weights_seen, masters = results["offload"]
+    _check_stack_against_oracle(layers, weights_seen, xs, douts, [g for g, _, _ in per_step],
+                                masters, dtype, "offload")
     with pytest.raises(ValueError):
         StageRunner([_layer(kw, dev, param_dtype=dtype, seed=1)], offload_inputs=True)
 

@@ -6,12 +6,13 @@ Replaces ``output_layer = Sequential(norm, lm_head)`` (models/llama_simple.py:
 1))`` (zorse_utils/pipeline_schedule_v2.py:181-184).  The reference
 materialises [tokens, vocab] logits (and their fp32 softmax under autocast);
 here the vocabulary is processed in chunks of ``chunk`` columns:
-  forward   per chunk: logits_c = x W_c^T (hipBLASLt), then zk_ce_fwd_chunk
+  forward   per chunk: logits_c = x W_c^T (zk_gemm), then zk_ce_fwd_chunk
             folds it into a running log-sum-exp and picks the label logit;
             loss = mean over non-ignored tokens of (lse - label logit);
   backward  per chunk: logits_c is recomputed, zk_ce_bwd_chunk turns it in
             place into g (softmax - onehot) / n_valid, then dx += dlogits_c
-            W_c (fp32 accumulator) and dW_c = dlogits_c^T x.
+            W_c (fp32 accumulator) and dW_c = dlogits_c^T x, both products on
+            zk_gemm with the operands as stored.
 Only [tokens, chunk] logits and fp32 per-token vectors are ever live.
 """
 from __future__ import annotations
@@ -63,7 +64,7 @@ class LMHeadCrossEntropyFunction(torch.autograd.Function):
         run_sum = torch.zeros(T, device=x.device, dtype=torch.float32)
         target = torch.zeros(T, device=x.device, dtype=torch.float32)
         for c0 in range(0, V, chunk):
-            logits = torch.mm(x, w[c0:c0 + chunk].t())
+            logits = K.gemm(x, w[c0:c0 + chunk])
             _fwd_chunk(logits, labels, c0, run_max, run_sum, target)
         lse = run_max + torch.log(run_sum)
         valid = labels >= 0
@@ -84,10 +85,10 @@ class LMHeadCrossEntropyFunction(torch.autograd.Function):
         dw = torch.empty_like(w)
         for c0 in range(0, V, chunk):
             wc = w[c0:c0 + chunk]
-            dlog = torch.mm(x, wc.t())
+            dlog = K.gemm(x, wc)
             _bwd_chunk(dlog, labels, c0, lse, scale)
-            dx.add_(torch.mm(dlog, wc))
-            torch.mm(dlog.t(), x, out=dw[c0:c0 + chunk])
+            dx.add_(K.gemm(dlog, wc, b_kmajor=True))
+            K.gemm(dlog, x, a_kmajor=True, b_kmajor=True, out=dw[c0:c0 + chunk])
         if dw.dtype != ctx.weight_dtype:
             dw = dw.to(ctx.weight_dtype)
         return dx.to(x.dtype), dw, None, None, None
