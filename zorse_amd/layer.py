@@ -118,6 +118,57 @@ def _wgrad(dy, x, out):
     K.gemm(dy, x, a_kmajor=True, b_kmajor=True, out=out)
 
 
+# The four weight-gradient GEMMs of a layer's backward are off its critical
+# path: nothing in the layer's backward reads them.  With a side stream they
+# run beside the input-gradient chain (dgrad GEMMs, SwiGLU / RMSNorm / attention
+# backward), so the partial last round of one GEMM's tiles (e.g. 1376 tiles of
+# the gate|up weight gradient on 256 CUs) fills with work of the other instead
+# of idling.  The layer's backward joins the side stream before it returns its
+# gradient.  ZORSE_WGRAD_STREAM=0 or set_wgrad_stream(False) runs them in order
+# on the compute stream.
+_wgrad_side = os.environ.get("ZORSE_WGRAD_STREAM", "1") != "0"
+_side_streams: dict = {}
+
+
+def set_wgrad_stream(enable: bool) -> bool:
+    """Run the weight-gradient GEMMs on a side stream (True) or in order on the
+    compute stream; returns the previous setting."""
+    global _wgrad_side
+    prev, _wgrad_side = _wgrad_side, bool(enable)
+    return prev
+
+
+class _WeightGrads:
+    """Enqueues a layer backward's weight-gradient GEMMs on a default-priority
+    side stream (after the compute stream's work so far) or, when disabled,
+    on the compute stream; join() makes the compute stream wait for them."""
+
+    def __init__(self, device, grad_flat):
+        self.main = torch.cuda.current_stream(device)
+        self.side = None
+        if _wgrad_side:
+            self.side = _side_streams.get(device)
+            if self.side is None:
+                self.side = _side_streams[device] = torch.cuda.Stream(device=device)
+            grad_flat.record_stream(self.side)
+
+    def __call__(self, dy, x, out):
+        if self.side is None:
+            _wgrad(dy, x, out)
+            return
+        self.side.wait_stream(self.main)
+        with torch.cuda.stream(self.side):
+            _wgrad(dy, x, out)
+        # the compute stream may free and reuse dy / x before the side stream
+        # has read them
+        dy.record_stream(self.side)
+        x.record_stream(self.side)
+
+    def join(self):
+        if self.side is not None:
+            self.main.wait_stream(self.side)
+
+
 # gate|up GEMM with the SwiGLU activation in its epilogue (zk_gemm_swiglu:
 # writes g, u and z in one pass) for 2-byte types; otherwise the GEMM and a
 # separate SwiGLU pass.  On by default: in the 7B stage it measured equal to
@@ -215,22 +266,23 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
     d, Hq, Hkv, F = spec.head_dim, spec.heads, spec.kv_heads, spec.ffn
     g = FlatViews(spec, grad_flat)
     dout2 = dout.reshape(T, h)
+    wgrad = _WeightGrads(dout.device, grad_flat)
 
     # MLP: out = hdn + z W_down^T
+    wgrad(dout2, z, g.down)
     dz = _dgrad(dout2, w.down)                       # [T, F]
-    _wgrad(dout2, z, g.down)
     dgu = torch.empty_like(gu)
     K.swiglu_bwd(dz, gu[:, :F], gu[:, F:], dgu[:, :F], dgu[:, F:])
     del dz
+    wgrad(dgu, n2, g.gu)
     dn2 = _dgrad(dgu, w.gu)                          # [T, h]
-    _wgrad(dgu, n2, g.gu)
     del dgu
     dh, _ = K.rmsnorm_bwd(dn2, hdn, w.ln2, rstd2, dres=dout2, dw=g.ln2)
     del dn2
 
     # attention: hdn = x + o W_o^T
+    wgrad(dh, o2, g.o)
     do2 = _dgrad(dh, w.o)                            # [T, Hq d]
-    _wgrad(dh, o2, g.o)
     q = qkv[:, :spec.q_dim].view(B, S, Hq, d)
     k = qkv[:, spec.q_dim:spec.q_dim + spec.kv_dim].view(B, S, Hkv, d)
     v = qkv[:, spec.q_dim + spec.kv_dim:].view(B, S, Hkv, d)
@@ -246,10 +298,11 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
                causal=spec.causal, window=spec.window, dq=dq, dk=dk, dv=dv,
                rope=(cos, sin, positions, spec.interleaved_rope))
     del do2
+    wgrad(dqkv, n1, g.qkv)
     dn1 = _dgrad(dqkv, w.qkv)                        # [T, h]
-    _wgrad(dqkv, n1, g.qkv)
     del dqkv
     dx, _ = K.rmsnorm_bwd(dn1, x2, w.ln1, rstd1, dres=dh, dw=g.ln1)
+    wgrad.join()
     return dx.view(B, S, h)
 
 
