@@ -472,3 +472,39 @@ def test_attention_bwd_transposed_output_checks():
     assert call(desc(16), 16, dq_t=None) == -1
     assert call(desc(16, _abi.ZK_F32), 16) == -4
     assert "transposed" in lib.zk_last_error().decode()
+
+
+def test_hf_factory_routes_structure():
+    """The llama_* / mistral_* factories (models/llama.py, models/mistral.py):
+    HF's attribute layout as models/hub.py reads it, the shapes the factories
+    set (FFN = 4 x hidden for llama_*, MistralConfig's GQA 8 / window 4096),
+    HF's parameter count, and head dims the attention kernels cannot take
+    rejected at construction (built on the meta device: no memory)."""
+    from zorse_amd import hf_models as H
+    from zorse_amd.llama_simple import LlamaDecoderLayer
+    with torch.device("meta"):
+        m = H.get_model("llama_6.7b", vocab_size=49152, seq_length=4096, layers=2)
+    layers = H.get_layers(m)
+    assert m._model_name == "llama_6.7b" and m._num_layers == 2 and m._hidden_size == 4096
+    assert all(isinstance(l, LlamaDecoderLayer) for l in layers)
+    l0 = layers[0]
+    assert l0.spec.ffn == 4 * 4096 and l0.spec.kv_heads == 32 and l0.spec.window == 0
+    assert l0.self_attn.q_proj.weight.shape == (4096, 4096)
+    assert l0.mlp.down_proj.weight.shape == (4096, 16384)
+    assert tuple(m.model.embed_tokens.weight.shape) == (49152, 4096)
+    assert tuple(m.model.norm.weight.shape) == (4096,)
+    assert tuple(m.lm_head.weight.shape) == (49152, 4096)
+    per_layer = 4 * 4096 ** 2 + 3 * 4096 * 16384 + 2 * 4096
+    assert l0.flat_param.numel() == per_layer
+    total = sum(p.numel() for p in m.parameters())
+    assert total == 2 * per_layer + 2 * 49152 * 4096 + 4096
+    with torch.device("meta"):
+        mm = H.get_model("mistral_7b", layers=1)
+    s = H.get_layers(mm)[0].spec
+    assert (s.kv_heads, s.window, s.ffn, s.rope_theta) == (8, 4096, 14336, 1e4)
+    assert H.get_layers(mm)[0].flat_param.numel() == 218_112_000
+    for name in ("llama_1b", "llama_2b", "llama_3b", "llama_4b", "llama_5b"):
+        with pytest.raises(NotImplementedError, match="head dim"):
+            H.get_model(name, layers=1)
+    with pytest.raises(ValueError):
+        H.get_model("llama_7b", layers=1)

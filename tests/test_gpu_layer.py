@@ -770,3 +770,92 @@ def test_profiler_protocol_small(dev):
     assert P.get_optimizer_latency(layer, 1, num_iterations=3) > 0
     assert P.get_optimizer_latency(layer, 4, num_iterations=3) > 0
     assert P.gpu_name() == "mi355x"
+
+
+# ------------------------------------------------------------- HF-factory routes --
+
+def test_hf_llama_route_vs_oracle(dev):
+    """The llama_* route (models/llama.py:5-56 through models/hub.py): the
+    factory's model form -- LlamaConfig defaults, FFN = 4 x hidden, HF's
+    attribute layout (model.model.layers, .embed_tokens, .norm, .lm_head) --
+    at a scaled shape (hidden 512, 4 heads x 128, 2 layers, vocab 1000, seq
+    128, batch 2), fp32 parameters.  forward(input_ids, labels) gives HF's
+    causal-LM loss (position t predicts label t + 1) through the chunked
+    vocabulary head; the loss and every parameter gradient (embedding, each
+    layer's nine slices, final norm, head) against the fp64 oracle of the same
+    composition (fp32 bar: 1e-4 normwise; loss 1e-4 relative)."""
+    from zorse_amd import hf_models as H
+    from zorse_amd.llama_simple import llama_config
+    cfg = llama_config(vocab_size=1000, max_position_embeddings=128, hidden_size=512,
+                       num_hidden_layers=2, num_attention_heads=4, intermediate_size=4 * 512)
+    torch.manual_seed(21)
+    model = H.CausalLM(cfg, init_std=0.02, generator=torch.Generator().manual_seed(22))
+    with torch.no_grad():   # norm weights other than one
+        for l in model.model.layers:
+            for ln in ("ln1", "ln2"):
+                l.param_view(ln).copy_(1 + 0.1 * torch.randn(512))
+        model.model.norm.weight.copy_(1 + 0.1 * torch.randn(512))
+    model = model.to(dev)
+    assert isinstance(H.get_layers(model), torch.nn.ModuleList) and len(model.model.layers) == 2
+    g = torch.Generator().manual_seed(23)
+    ids = torch.randint(0, 1000, (2, 128), generator=g)
+    labels = torch.randint(0, 1000, (2, 128), generator=g)
+    labels[0, 17] = -100
+    out = model(ids.to(dev), labels=labels.to(dev))
+    out.loss.backward()
+    # the oracle, fp64 on the CPU
+    emb = model.model.embed_tokens.weight.detach().double().cpu().requires_grad_(True)
+    ps = [{k: v.clone().requires_grad_(True) for k, v in _oracle_params(l, torch.float32).items()}
+          for l in model.model.layers]
+    nw = model.model.norm.weight.detach().double().cpu().requires_grad_(True)
+    hw = model.lm_head.weight.detach().double().cpu().requires_grad_(True)
+    x = emb[ids]
+    shape = _oracle_shape(model.model.layers[0])
+    for p in ps:
+        x = O.decoder_layer(x, p, shape)
+    rl = O.lm_head_ce(x[:, :-1], nw, hw, labels[:, 1:], 1e-6)
+    rl.backward()
+    print(f"  HF llama route loss: hip {out.loss.item():.8f} fp64 {rl.item():.8f}", flush=True)
+    assert abs(out.loss.item() - rl.item()) <= 1e-4 * abs(rl.item())
+    assert_close(model.model.embed_tokens.weight.grad, emb.grad, torch.float32, "d embed")
+    assert_close(model.model.norm.weight.grad, nw.grad, torch.float32, "d norm")
+    assert_close(model.lm_head.weight.grad, hw.grad, torch.float32, "d lm_head")
+    offs = model.model.layers[0].spec.offsets()
+    for i, (l, p) in enumerate(zip(model.model.layers, ps)):
+        for k in O.PARAM_ORDER:
+            a, b = offs[k]
+            assert_close(l.flat_param.grad[a:b].view(p[k].shape), p[k].grad, torch.float32,
+                         f"layer {i} d{k}")
+    # without labels: the logits of the same forward (hand-written GEMM head)
+    with torch.no_grad():
+        logits = model(ids.to(dev)).logits
+        rlog = torch.nn.functional.linear(O.rmsnorm(x.detach(), nw.detach(), 1e-6), hw.detach())
+    assert logits.shape == (2, 128, 1000)
+    assert_close(logits, rlog, torch.float32, "logits")
+
+
+def test_hf_mistral_route_layer_and_profiler_protocol(dev):
+    """The mistral_* route (models/mistral.py:5-35): MistralConfig's form
+    (8 KV heads, sliding window 4096, FFN as given) at a scaled shape (hidden
+    512, 4 q-heads / 1 kv-head of 128, window 96, seq 160, bf16 parameters):
+    a layer of model.model.layers against the oracle with the precision-matched
+    bar, then the layer profiler's protocol on it (utils/runtime_estimator.py:
+    187-253: forward under autocast, backward with retain_graph)."""
+    from zorse_amd import hf_models as H
+    from zorse_amd import profiler as P
+    from zorse_amd.mistral_simple import mistral_config
+    cfg = mistral_config(vocab_size=1000, max_position_embeddings=160, hidden_size=512,
+                         num_hidden_layers=1, num_attention_heads=4, num_key_value_heads=1,
+                         intermediate_size=1536, sliding_window=96)
+    model = H.CausalLM(cfg, sliding_window=cfg.sliding_window, init_std=0.02,
+                       generator=torch.Generator().manual_seed(31),
+                       param_dtype=torch.bfloat16).to(dev)
+    layer = H.get_layers(model)[0]
+    assert layer.spec.window == 96 and layer.spec.kv_heads == 1
+    g = torch.Generator().manual_seed(32)
+    x = torch.randn(1, 160, 512, generator=g).to(torch.bfloat16)
+    dout = torch.randn(1, 160, 512, generator=g).to(torch.bfloat16)
+    _check_layer(layer, x, dout, torch.bfloat16, "HF mistral route layer")
+    times = [P.get_compute_latency(layer, bs, 160, 512, torch.bfloat16, vocab_size=1000,
+                                   num_iterations=3, delay=0.0) for bs in (1, 2)]
+    assert all(f > 0 and b > 0 for f, b in times)

@@ -108,10 +108,19 @@ def get_compute_latency(layer, batch_size, seq_length, hidden, dtype, vocab_size
             o = layer(emb)
         out_box[:] = [o[0] if isinstance(o, tuple) else o]
 
-    fwd_ms = _kernel_ms(fwd, num_iterations, delay)
-    out = out_box[0]
-    grads = torch.rand(out.shape, device=out.device, dtype=out.dtype)
-    bwd_ms = _kernel_ms(lambda: out.backward(grads, retain_graph=True), num_iterations, delay)
+    # the protocol sums kernel durations, which counts kernels that overlap
+    # on two streams twice: the layer backward's weight-gradient GEMMs run in
+    # order on the compute stream while it is measured
+    from .layer import set_wgrad_stream
+    prev = set_wgrad_stream(False)
+    try:
+        fwd_ms = _kernel_ms(fwd, num_iterations, delay)
+        out = out_box[0]
+        grads = torch.rand(out.shape, device=out.device, dtype=out.dtype)
+        bwd_ms = _kernel_ms(lambda: out.backward(grads, retain_graph=True), num_iterations,
+                            delay)
+    finally:
+        set_wgrad_stream(prev)
     return fwd_ms, bwd_ms
 
 
@@ -135,10 +144,15 @@ def profile_model(model_name, seq_length=4096, dtype=torch.bfloat16, profile_bat
                   device="cuda"):
     """Profile the first layer of a 1-layer model; returns (entry, optimizer
     ms per shard count)."""
-    from . import llama_simple, mistral_simple
-    mod = mistral_simple if model_name.startswith("deepspeedmistral") else llama_simple
-    model = mod.get_model(model_name, vocab_size=vocab_size, seq_length=seq_length, layers=1)
-    layer = model.layers[0].to(device)
+    from . import hf_models, llama_simple, mistral_simple
+    name = model_name.lower()
+    if name.startswith(("llama", "mistral")):   # the HF-factory routes
+        model = hf_models.get_model(name, vocab_size=vocab_size, seq_length=seq_length, layers=1)
+        layer = hf_models.get_layers(model)[0].to(device)
+    else:
+        mod = mistral_simple if name.startswith("deepspeedmistral") else llama_simple
+        model = mod.get_model(model_name, vocab_size=vocab_size, seq_length=seq_length, layers=1)
+        layer = model.layers[0].to(device)
     opt_ms = {n: get_optimizer_latency(layer, n) for n in range(1, max_shards + 1)}
     fwd, bwd = [], []
     for bs in range(1, profile_batches + 1):
