@@ -89,7 +89,10 @@ int zk_rmsnorm_bwd(const void* dy, const void* h, const void* w,
  * ZK_RMSNORM_BWD_SCRATCH_FLOATS floats (16 MiB) that each GPU the library
  * runs on holds until the process ends; its address is looked up on the
  * first call on a device, which must be the current device (the stream must
- * belong to it).  The entry point allocates nothing.  (rows, hidden) whose
+ * belong to it).  That lookup is not an operation a graph can capture: make
+ * one call on each device before capturing later ones (the calls themselves
+ * launch kernels only, no memset or copy).  The entry point allocates
+ * nothing.  (rows, hidden) whose
  * zk_rmsnorm_bwd_workspace() exceeds the array are rejected with
  * ZK_EWORKSPACE (any rows at hidden <= 8192: at most 512 partial rows).
  * Every call on a GPU shares that GPU's array: calls that overlap on one GPU

@@ -77,3 +77,67 @@ def test_noalloc_matches_workspace_entry_point(dev):
         assert torch.isfinite(dx_na).all()
         assert torch.equal(dx_na, dx_ws), (rows, hidden)
         assert torch.equal(dw_na, dw_ws), (rows, hidden)
+
+
+@pytest.mark.gpu
+def test_noalloc_under_graph_capture(dev):
+    """The allocation-free entry point inside a captured HIP graph (what it
+    exists for): after one eager call on the device (which resolves the
+    scratch address), a call captured with torch.cuda.graph is replayed three
+    times, the inputs refilled in place by eager work between replays; every
+    replay's dx and dw equal the workspace entry point's eager result on the
+    same inputs, bit for bit."""
+    lib = _abi.lib()
+    rows, hidden, adt = 4096, 4096, torch.bfloat16
+    code = _abi.dtype_code(adt)
+    dy = torch.empty(rows, hidden, device=dev, dtype=adt)
+    h = torch.empty_like(dy)
+    dres = torch.empty_like(dy)
+    w = torch.empty(hidden, device=dev, dtype=adt)
+    rstd = torch.empty(rows, device=dev)
+    dx = torch.empty_like(dy)
+    dw = torch.empty(hidden, device=dev, dtype=adt)
+
+    def fill(seed):
+        g = torch.Generator().manual_seed(seed)
+        dy.copy_(torch.randn(rows, hidden, generator=g))
+        h.copy_(torch.randn(rows, hidden, generator=g))
+        dres.copy_(torch.randn(rows, hidden, generator=g))
+        w.copy_(1 + 0.1 * torch.randn(hidden, generator=g))
+        rstd.copy_(torch.rand(rows, generator=g) + 0.5)
+
+    def call_noalloc():
+        stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        rc = lib.zk_rmsnorm_bwd_noalloc(_ptr(dy), _ptr(h), _ptr(w), _ptr(rstd), _ptr(dres),
+                                        _ptr(dx), _ptr(dw), 0, rows, hidden, code, code, stream)
+        assert rc == 0, lib.zk_last_error()
+
+    def reference():
+        rdx, rdw = torch.empty_like(dx), torch.empty_like(dw)
+        n = lib.zk_rmsnorm_bwd_workspace(rows, hidden)
+        ws = torch.empty(n, device=dev, dtype=torch.float32)
+        stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        rc = lib.zk_rmsnorm_bwd(_ptr(dy), _ptr(h), _ptr(w), _ptr(rstd), _ptr(dres), _ptr(rdx),
+                                _ptr(rdw), 0, _ptr(ws), n, rows, hidden, code, code, stream)
+        assert rc == 0, lib.zk_last_error()
+        torch.cuda.synchronize()
+        return rdx, rdw
+
+    fill(1)
+    call_noalloc()                      # eager: resolves the scratch address
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call_noalloc()
+    torch.cuda.synchronize()
+    for seed in (2, 3, 4):
+        print(f"rmsnorm_bwd_noalloc graph replay, inputs seed {seed}", flush=True)
+        fill(seed)
+        dx.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got_dx, got_dw = dx.clone(), dw.clone()
+        rdx, rdw = reference()
+        assert torch.equal(got_dx, rdx), seed
+        assert torch.equal(got_dw, rdw), seed

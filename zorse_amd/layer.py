@@ -157,6 +157,10 @@ class _WeightGrads:
             _wgrad(dy, x, out)
             return
         self.side.wait_stream(self.main)
+        self.issue(dy, x, out)
+
+    def issue(self, dy, x, out):
+        """The side-stream launch (the caller has made the side stream wait)."""
         with torch.cuda.stream(self.side):
             _wgrad(dy, x, out)
         # the compute stream may free and reuse dy / x before the side stream
