@@ -478,8 +478,8 @@ def test_hf_factory_routes_structure():
     """The llama_* / mistral_* factories (models/llama.py, models/mistral.py):
     HF's attribute layout as models/hub.py reads it, the shapes the factories
     set (FFN = 4 x hidden for llama_*, MistralConfig's GQA 8 / window 4096),
-    HF's parameter count, and head dims the attention kernels cannot take
-    rejected at construction (built on the meta device: no memory)."""
+    HF's parameter count, and the smaller models' head dims 48 - 110 (built on
+    the meta device: no memory)."""
     from zorse_amd import hf_models as H
     from zorse_amd.llama_simple import LlamaDecoderLayer
     with torch.device("meta"):
@@ -503,8 +503,12 @@ def test_hf_factory_routes_structure():
     s = H.get_layers(mm)[0].spec
     assert (s.kv_heads, s.window, s.ffn, s.rope_theta) == (8, 4096, 14336, 1e4)
     assert H.get_layers(mm)[0].flat_param.numel() == 218_112_000
-    for name in ("llama_1b", "llama_2b", "llama_3b", "llama_4b", "llama_5b"):
-        with pytest.raises(NotImplementedError, match="head dim"):
-            H.get_model(name, layers=1)
+    # the smaller llama_* models' head dims (padded around the attention kernels)
+    for name, d in (("llama_1b", 48), ("llama_2b", 68), ("llama_3b", 84), ("llama_4b", 98),
+                    ("llama_5b", 110)):
+        with torch.device("meta"):
+            ms = H.get_model(name, layers=1)
+        s = H.get_layers(ms)[0].spec
+        assert s.head_dim == d and s.ffn == 4 * s.hidden
     with pytest.raises(ValueError):
         H.get_model("llama_7b", layers=1)

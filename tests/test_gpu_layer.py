@@ -859,3 +859,22 @@ def test_hf_mistral_route_layer_and_profiler_protocol(dev):
     times = [P.get_compute_latency(layer, bs, 160, 512, torch.bfloat16, vocab_size=1000,
                                    num_iterations=3, delay=0.0) for bs in (1, 2)]
     assert all(f > 0 and b > 0 for f, b in times)
+
+
+@pytest.mark.parametrize("d,dtype", [(48, torch.bfloat16), (68, torch.float16),
+                                     (110, torch.bfloat16)])
+def test_layer_padded_head_dims(dev, d, dtype):
+    """Head dims of the smaller llama_* HF-factory models (llama_1b: 48,
+    llama_2b: 68, llama_5b: 110), which the attention kernels take zero-padded
+    to 64 / 128: a 4-head layer (hidden 4 d, FFN 16 d, 2 x 96 tokens, GQA 4:2
+    for d = 68) against the fp64 oracle with the precision-matched bar."""
+    from zorse_amd import layer as LY
+    kv = 2 if d == 68 else 4
+    kw = dict(hidden_size=4 * d, num_attention_heads=4, num_key_value_heads=kv,
+              intermediate_size=16 * d, rope_theta=1e4)
+    layer = _layer(kw, dev, param_dtype=dtype, seed=401 + d)
+    assert layer.spec.head_dim == d and LY._attn_padded_dim(layer.spec, dtype) in (64, 128)
+    g = torch.Generator().manual_seed(402 + d)
+    x = torch.randn(2, 96, 4 * d, generator=g).to(dtype)
+    dout = torch.randn(2, 96, 4 * d, generator=g).to(dtype)
+    _check_layer(layer, x, dout, dtype, f"padded head dim {d}")

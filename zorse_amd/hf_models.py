@@ -26,9 +26,10 @@ Shapes, as the factories set them:
   * mistral_*: MistralConfig defaults (8 KV heads, rms eps 1e-6, rope theta
     1e4, sliding window 4096; causal attention over the last 4096 keys, the
     mask HF's Mistral model builds) with models/mistral.py:16-26.
-The attention kernels take head dims 64 and 128: llama_6.7b, 13b, 33b and 65b
-and the Mistral models (128); llama_1b..5b have head dims 48, 68, 84, 98, 110
-and are rejected at construction.
+llama_6.7b, 13b, 33b, 65b and the Mistral models have head dim 128, which the
+attention kernels take directly; llama_1b..5b have head dims 48, 68, 84, 98,
+110, for which the layer zero-pads q, k, v to 64 / 128 around the attention
+kernels (layer._attn_padded_dim).
 """
 from __future__ import annotations
 
@@ -61,7 +62,6 @@ MISTRAL_SHAPES = {
     "mistral_toy": (4096, 5, 32, 14336),
 }
 
-SUPPORTED_HEAD_DIMS = (64, 128)
 INIT_STD = 0.02  # LlamaConfig / MistralConfig initializer_range
 
 
@@ -118,11 +118,10 @@ class CausalLM(nn.Module):
 
 
 def _check_head_dim(model_name, hidden, heads):
-    d = hidden // heads
-    if d not in SUPPORTED_HEAD_DIMS:
+    if hidden % heads or (hidden // heads) % 2 or hidden // heads > 128:
         raise NotImplementedError(
-            f"{model_name}: head dim {hidden} / {heads} = {d}; the attention kernels take "
-            f"head dims {SUPPORTED_HEAD_DIMS}")
+            f"{model_name}: head dim {hidden} / {heads}; the attention kernels take even head "
+            f"dims up to 128")
 
 
 def get_llama_model(model_name, vocab_size=49152, seq_length=2048, layers=None, **layer_kw):

@@ -197,6 +197,32 @@ def _fused_gate_up_takes(n2, F):
             and h % 64 == 0 and T % 8 == 0 and F % 8 == 0)
 
 
+# Head dims the MFMA attention kernels do not take (they take 64 and 128; the
+# fp32 kernels any head dim up to 128): q, k, v are zero-padded to the next of
+# those, attention runs with the real head dim's scale -- the padded
+# coordinates add nothing to Q K^T, P V or any gradient -- and the results are
+# sliced back.  RoPE rotates the real coordinates in place before (forward),
+# and its transpose is applied to dq / dk after the backward.  The padding
+# copies are torch copies into zeroed buffers (head dims 48 - 110 of the
+# smaller llama_* HF-factory models only).
+def _attn_padded_dim(spec, dtype):
+    d = spec.head_dim
+    if dtype == torch.float32 or d in (64, 128):
+        return None
+    if d < 64:
+        return 64
+    if d < 128:
+        return 128
+    raise NotImplementedError(f"head_dim {d}: the attention kernels take head dims up to 128")
+
+
+def _pad_heads(t, dp):
+    """[B, S, H, d] -> a zero-padded [B, S, H, dp] copy."""
+    out = t.new_zeros(*t.shape[:3], dp)
+    out[..., :t.shape[3]].copy_(t)
+    return out
+
+
 def _rope_for(S, spec, dtype, device, positions):
     """RoPE tables covering positions 0 .. S-1, or 0 .. max(positions) when
     explicit positions are given (int64 [S] on the device)."""
@@ -232,7 +258,14 @@ def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=Non
     if hit is not None:
         o, lse = hit
     else:
-        o, lse = K.attn_fwd(q, k, v, causal=spec.causal, window=spec.window)
+        dp = _attn_padded_dim(spec, x.dtype)
+        if dp is None:
+            o, lse = K.attn_fwd(q, k, v, causal=spec.causal, window=spec.window)
+        else:
+            o, lse = K.attn_fwd(_pad_heads(q, dp), _pad_heads(k, dp), _pad_heads(v, dp),
+                                causal=spec.causal, window=spec.window,
+                                scale=1.0 / math.sqrt(d))
+            o = o[..., :d].contiguous()
         if attn_cache is not None:
             attn_cache.put(o, lse)
     o2 = o.view(T, spec.q_dim)
@@ -296,11 +329,22 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
     dv = dqkv[:, spec.q_dim + spec.kv_dim:].view(B, S, Hkv, d)
     for fn in list(BEFORE_ATTENTION_BACKWARD):
         fn()
-    # the attention backward also takes dq / dk back through RoPE's rotation
     cos, sin = _rope_for(S, spec, dout.dtype, dout.device, positions)
-    K.attn_bwd(q, k, v, o2.view(B, S, Hq, d), do2.view(B, S, Hq, d), lse,
-               causal=spec.causal, window=spec.window, dq=dq, dk=dk, dv=dv,
-               rope=(cos, sin, positions, spec.interleaved_rope))
+    dp = _attn_padded_dim(spec, dout.dtype)
+    if dp is None:
+        # the attention backward also takes dq / dk back through RoPE's rotation
+        K.attn_bwd(q, k, v, o2.view(B, S, Hq, d), do2.view(B, S, Hq, d), lse,
+                   causal=spec.causal, window=spec.window, dq=dq, dk=dk, dv=dv,
+                   rope=(cos, sin, positions, spec.interleaved_rope))
+    else:
+        grads = K.attn_bwd(*(_pad_heads(t, dp) for t in (q, k, v, o2.view(B, S, Hq, d),
+                                                         do2.view(B, S, Hq, d))), lse,
+                           causal=spec.causal, window=spec.window, scale=1.0 / math.sqrt(d))
+        for dst, src in zip((dq, dk, dv), grads):
+            dst.copy_(src[..., :d])
+        del grads
+        K.rope_(dq, dk, cos, sin, positions=positions, interleaved=spec.interleaved_rope,
+                inverse=True)
     del do2
     wgrad(dqkv, n1, g.qkv)
     dn1 = _dgrad(dqkv, w.qkv)                        # [T, h]
