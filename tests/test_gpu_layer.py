@@ -211,9 +211,11 @@ def _forbid_library_products(monkeypatch):
 def test_layer_every_product_hand_written(dev, name, monkeypatch):
     """All twelve projection products of a layer step go through the
     hand-written GEMMs -- the four forward ones (gate|up with the SwiGLU
-    epilogue), the four input gradients dY W and the four weight gradients
-    dY^T X on the operands as stored (no transposes) -- each on the MFMA
-    pipeline (zk_gemm_path "tiled"); no torch GEMM is called.  Parity against
+    epilogue), the four input gradients dY W on W as stored, and the four
+    weight gradients dY^T X (o and down on the token-major dY, X as stored;
+    gate|up and q|k|v on the dY^T the SwiGLU / attention backward kernels
+    write from their epilogues) -- each on the MFMA pipeline (zk_gemm_path
+    "tiled"); no torch GEMM and no transpose pass is called.  Parity against
     the fp64 oracle as every layer test."""
     from zorse_amd import kernels as K
     from zorse_amd import layer as LY
@@ -262,8 +264,10 @@ def test_layer_every_product_hand_written(dev, name, monkeypatch):
     # on the CPU, outside these wrappers)
     assert len(calls) == 12, calls
     assert sum(c[0] == "gemm_swiglu" for c in calls) == 1, calls
-    assert sum(c[1:3] == (False, True) for c in calls) == 4, calls   # dY W
-    assert sum(c[1:3] == (True, True) for c in calls) == 4, calls    # dY^T X
+    # dY W (4) and the gate|up / q|k|v weight gradients on the dY^T their
+    # producers wrote (2); the o / down weight gradients on dY, X as stored (2)
+    assert sum(c[1:3] == (False, True) for c in calls) == 6, calls
+    assert sum(c[1:3] == (True, True) for c in calls) == 2, calls
     assert all(c[3] == "tiled" for c in calls), calls
 
 

@@ -303,7 +303,9 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_scalar(
 // dw[c] = sum_p part[p][c]  (optionally added to the existing dw).  A
 // workgroup owns 64 columns; its 16 waves stride over the partial rows with 4
 // independent running sums each and meet in LDS.  nparts == 0 writes zeros
-// (or leaves dw unchanged).
+// (or leaves dw unchanged).  (16 columns per workgroup, which spreads the
+// reduction over every CU, read the partial rows in 64-byte segments: 8 %
+// more HBM traffic for the whole backward and no gain in time.)
 __global__ __launch_bounds__(1024) void rmsnorm_dw_reduce(
     const float* __restrict__ part, int64_t nparts, int64_t hidden,
     void* __restrict__ dw, int wdt, int accumulate) {
@@ -346,10 +348,17 @@ static void launch_fwd_vec(const void* x, const void* res, void* hout,
                            int64_t hidden, float eps, hipStream_t s) {
   int nt, ch;
   pick_shape(hidden, nt, ch);
-  // the forward keeps one row per workgroup: prefer 128 threads x up to 4
-  // chunks (more bytes in flight per thread, more workgroups per CU)
+  // The forward keeps one row per workgroup.  Rows of up to 4096 elements
+  // take ONE wave (64 threads x up to 8 chunks): the row sum is a wave
+  // reduction with no LDS exchange or barrier, and each wave keeps the whole
+  // row's loads in flight -- 12.2 against 13.2 us for 128 threads x 4 chunks
+  // at 4096 x 4096 bf16 (one box, rotating buffers).  Wider rows: 128 threads
+  // x up to 4 chunks, then 256.
   const int64_t nchunk = hidden / 8;
-  if (nt == 256 && nchunk <= 128 * kMaxCh) {
+  if (nchunk <= 64 * 8) {
+    nt = 64;
+    ch = nchunk <= 64 ? 1 : nchunk <= 128 ? 2 : nchunk <= 256 ? 4 : 8;
+  } else if (nt == 256 && nchunk <= 128 * kMaxCh) {
     nt = 128;
     ch = static_cast<int>((nchunk + 127) / 128);
   }
@@ -357,7 +366,10 @@ static void launch_fwd_vec(const void* x, const void* res, void* hout,
   hipLaunchKernelGGL((rmsnorm_fwd_vec<T, W, NT, CH>), dim3(rows), dim3(NT), 0, s,  \
                      (const T*)x, (const T*)res, (T*)hout, (const W*)w, (T*)y, rstd, \
                      hidden, eps)
-  if (nt == 64) ZK_LAUNCH(64, 1);
+  if (nt == 64 && ch == 1) ZK_LAUNCH(64, 1);
+  else if (nt == 64 && ch == 2) ZK_LAUNCH(64, 2);
+  else if (nt == 64 && ch == 4) ZK_LAUNCH(64, 4);
+  else if (nt == 64) ZK_LAUNCH(64, 8);
   else if (nt == 128 && ch == 1) ZK_LAUNCH(128, 1);
   else if (nt == 128 && ch == 2) ZK_LAUNCH(128, 2);
   else if (nt == 128 && ch == 3) ZK_LAUNCH(128, 3);
