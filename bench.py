@@ -394,17 +394,17 @@ def summarize_stage(root: str, layers: int, steps: int, warmup: int) -> str:
                  "other")
         ev += [(int(r["Start_Timestamp"]), 1, g), (int(r["End_Timestamp"]), -1, g)]
     ev.sort()
-    active, share, alone, last = collections.Counter(), collections.Counter(), \
+    active, share, alone, prev = collections.Counter(), collections.Counter(), \
         collections.Counter(), t0
     for t, d, g in ev:
         running = [k for k, c in active.items() if c]
         n = sum(active.values())
         for k in running:
-            share[k] += (t - last) * active[k] / n
+            share[k] += (t - prev) * active[k] / n
         if n == 1:
-            alone[running[0]] += t - last
+            alone[running[0]] += t - prev
         active[g] += d
-        last = t
+        prev = t
     lines += ["", "The same window as a timeline: each instant split evenly among the kernel groups "
                   "running then (the shares sum to the GPU's busy time), and the time each group "
                   "runs with nothing beside it:", "",
