@@ -394,6 +394,11 @@ ATTN_CASES = [
     (1, 130, 4, 2, 128, True, 1, torch.bfloat16),
     (1, 50, 2, 1, 16, True, 0, torch.float32),
     (1, 90, 4, 2, 64, True, 30, torch.float32),
+    # d = 128 over many key tiles (the forward's three-stage V ring wraps)
+    (2, 320, 4, 4, 128, False, 0, torch.bfloat16),
+    (1, 100, 2, 1, 128, False, 0, torch.float16),
+    (1, 1024, 2, 2, 128, True, 0, torch.bfloat16),
+    (1, 700, 2, 2, 128, True, 200, torch.bfloat16),
 ]
 
 

@@ -38,10 +38,15 @@ HIPCC_FLAGS = [
 # vectoriser forms two-wide fp32 negations that this compiler cannot select
 # (a backend "Cannot select: v2f32 bitcast" crash in the position-major
 # kernel); the kernels there are memory-bound, so scalar code costs nothing.
-# gemm.hip: its LDS-DMA asm declares M0 clobbered, which clang reports as a
-# clobber of a reserved register (the intent: the compiler keeps nothing in
-# M0 across the asm).
-FILE_FLAGS = {"rope.hip": ["-fno-slp-vectorize"], "gemm.hip": ["-Wno-inline-asm"]}
+# gemm.hip, gemm_kmajor.hip: the GEMM's LDS-DMA asm declares M0 clobbered,
+# which clang reports as a clobber of a reserved register (the intent: the
+# compiler keeps nothing in M0 across the asm).  gemm_kmajor.hip (the tiled
+# forms with a K-major operand): the greedy register allocator assigns local
+# live ranges in reverse order, which keeps the 256 accumulators in place
+# through the loop (with the default order the both-K-major form moved ~80
+# of them between AGPRs per pass; the NT forms do better with the default).
+FILE_FLAGS = {"rope.hip": ["-fno-slp-vectorize"], "gemm.hip": ["-Wno-inline-asm"],
+              "gemm_kmajor.hip": ["-Wno-inline-asm", "-mllvm", "-greedy-reverse-local-assignment=1"]}
 
 
 def _hipcc() -> str:
