@@ -244,7 +244,7 @@ def measure_kernels(dev, spec, S):
     spec_of = {
         "attn_fwd": ("attn_fwd_kernel<bf16,128,full>", "mfma", 20),
         "attn_bwd": ("zk_attn_bwd (attn_bwd_dq + attn_bwd_dkdv)", "mfma", 10),
-        "rmsnorm_fwd": ("rmsnorm_fwd_vec<bf16,bf16,64,8>", "hbm", 32),
+        "rmsnorm_fwd": ("rmsnorm_fwd_vec<bf16,bf16,128,4>", "hbm", 32),
         "rmsnorm_bwd": ("rmsnorm_bwd_vec<bf16,bf16,256,2,2> + dw reduce", "hbm", 32),
         "adamw": ("adamw_elem<bf16,bf16,true>", "hbm", 10),
         "adamw_t": ("adamw_tile_t<bf16,bf16> (layer step with W^T copies)", "hbm", 10),
@@ -449,7 +449,7 @@ TRAFFIC_CASES = {
     "attn_fwd": ("attn_fwd_kernel<bf16,128,full>", ("attn_fwd_kernel",)),
     "attn_bwd": ("zk_attn_bwd (attn_bwd_dq + attn_bwd_dkdv)",
                  ("attn_bwd_dkdv", "attn_bwd_dq")),
-    "rmsnorm_fwd": ("rmsnorm_fwd_vec<bf16,bf16,64,8>", ("rmsnorm_fwd_vec",)),
+    "rmsnorm_fwd": ("rmsnorm_fwd_vec<bf16,bf16,128,4>", ("rmsnorm_fwd_vec",)),
     "rmsnorm_bwd": ("rmsnorm_bwd_vec<bf16,bf16,256,2,2> + dw reduce",
                     ("rmsnorm_bwd_vec", "rmsnorm_dw_reduce")),
     "adamw": ("adamw_elem<bf16,bf16,true>", ("adamw_elem",)),

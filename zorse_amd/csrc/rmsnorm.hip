@@ -49,18 +49,32 @@ __global__ __launch_bounds__(NT) void rmsnorm_fwd_vec(
   const int64_t row = blockIdx.x;
   const T* xr = x + row * hidden;
   const int nchunk = static_cast<int>(hidden / 8);
+  // every load of the row (and of its residual) first, in storage format, so
+  // that all of them are in flight together; widened afterwards
+  Raw8<T> xraw[CH], rraw[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ch = threadIdx.x + c * NT;
+    if (ch < nchunk) xraw[c].load(xr + ch * 8);
+  }
+  if (res != nullptr) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int ch = threadIdx.x + c * NT;
+      if (ch < nchunk) rraw[c].load(res + row * hidden + ch * 8);
+    }
+  }
   float v[CH][8];
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int ch = threadIdx.x + c * NT;
     if (ch < nchunk) {
-      Vec8<T>::load(xr + ch * 8, v[c]);
-      if (res != nullptr) {
-        float r8[8];
-        Vec8<T>::load(res + row * hidden + ch * 8, r8);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[c][i] = round_to<T>(v[c][i] + r8[i]);
+      for (int i = 0; i < 8; ++i) v[c][i] = xraw[c][i];
+      if (res != nullptr) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[c][i] = round_to<T>(v[c][i] + rraw[c][i]);
         Vec8<T>::store(hout + row * hidden + ch * 8, v[c]);
       }
 #pragma unroll
@@ -348,17 +362,13 @@ static void launch_fwd_vec(const void* x, const void* res, void* hout,
                            int64_t hidden, float eps, hipStream_t s) {
   int nt, ch;
   pick_shape(hidden, nt, ch);
-  // The forward keeps one row per workgroup.  Rows of up to 4096 elements
-  // take ONE wave (64 threads x up to 8 chunks): the row sum is a wave
-  // reduction with no LDS exchange or barrier, and each wave keeps the whole
-  // row's loads in flight -- 12.2 against 13.2 us for 128 threads x 4 chunks
-  // at 4096 x 4096 bf16 (one box, rotating buffers).  Wider rows: 128 threads
-  // x up to 4 chunks, then 256.
+  // The forward keeps one row per workgroup: prefer 128 threads x up to 4
+  // chunks (more bytes in flight per thread, more workgroups per CU).  At
+  // 4096 x 4096 bf16 (one box, rotating buffers): 12.0 us with the kernel's
+  // loads issued before any math, 12.9 for one wave x 8 chunks, 13.0 for
+  // this shape with each chunk's math right after its load.
   const int64_t nchunk = hidden / 8;
-  if (nchunk <= 64 * 8) {
-    nt = 64;
-    ch = nchunk <= 64 ? 1 : nchunk <= 128 ? 2 : nchunk <= 256 ? 4 : 8;
-  } else if (nt == 256 && nchunk <= 128 * kMaxCh) {
+  if (nt == 256 && nchunk <= 128 * kMaxCh) {
     nt = 128;
     ch = static_cast<int>((nchunk + 127) / 128);
   }
@@ -366,10 +376,7 @@ static void launch_fwd_vec(const void* x, const void* res, void* hout,
   hipLaunchKernelGGL((rmsnorm_fwd_vec<T, W, NT, CH>), dim3(rows), dim3(NT), 0, s,  \
                      (const T*)x, (const T*)res, (T*)hout, (const W*)w, (T*)y, rstd, \
                      hidden, eps)
-  if (nt == 64 && ch == 1) ZK_LAUNCH(64, 1);
-  else if (nt == 64 && ch == 2) ZK_LAUNCH(64, 2);
-  else if (nt == 64 && ch == 4) ZK_LAUNCH(64, 4);
-  else if (nt == 64) ZK_LAUNCH(64, 8);
+  if (nt == 64) ZK_LAUNCH(64, 1);
   else if (nt == 128 && ch == 1) ZK_LAUNCH(128, 1);
   else if (nt == 128 && ch == 2) ZK_LAUNCH(128, 2);
   else if (nt == 128 && ch == 3) ZK_LAUNCH(128, 3);
