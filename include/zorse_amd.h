@@ -215,6 +215,25 @@ int zk_rope(void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh, void* k,
             const float* sin, int64_t n_pos, const int64_t* positions,
             int pairing, int inverse, int dtype, zk_stream_t stream);
 
+/* The q|k|v projection with the rotary embedding fused: c = a b^T (the
+ * zk_gemm_nt product: a [M, K], b [N, K], c [M, N] with row strides lda /
+ * ldb / ldc) with the forward rotation applied to its first rot_cols columns
+ * -- the q and k heads of the fused projection, heads of head_dim columns --
+ * exactly as zk_rope would rotate the stored product (the product rounded to
+ * the storage type first, then rotate_half's per-op rounding or the
+ * interleaved pairing's one rounding): the nn.Linear q_proj / k_proj of
+ * models/llama_simple.py:206-221 followed by apply_rotary_pos_emb
+ * (models/llama_simple.py:27-58) or apply_rotary_emb (models/llama_v2.py:
+ * 151-177).  Rows are tokens b S + s (M a multiple of S); positions, tables
+ * and pairing as for zk_rope.  bf16 / fp16 products on the 256 x 256 grid
+ * with head_dim 64 / 128 and rot_cols a multiple of 128 rotate in the GEMM's
+ * epilogue; other launches run zk_gemm then zk_rope (same result). */
+int zk_gemm_rope(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
+                 int64_t ldc, int64_t M, int64_t N, int64_t K, int64_t S,
+                 int64_t rot_cols, int64_t head_dim, const float* cos,
+                 const float* sin, int64_t n_pos, const int64_t* positions,
+                 int pairing, int dtype, zk_stream_t stream);
+
 /* -------------------------------------------------------------- Attention --
  * Replaces the attention core of the decoder layer: softmax(Q K^T * scale +
  * mask) V with GQA (repeat_kv never materialised: kv head = q head / n_rep)

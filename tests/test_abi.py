@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_error_text(lib):
-    assert lib.zk_abi_version() == 3
+    assert lib.zk_abi_version() == 4
     rc = lib.zk_rmsnorm_fwd(None, None, None, None, None, None, 4, 8, 1e-6, 7, 0, None)
     assert rc == -2  # ZK_EDTYPE
     assert b"dtype" in lib.zk_last_error()

@@ -282,6 +282,44 @@ def _assert_z_of_gu(z, gu, F, dtype):
     assert (diff != 0).sum().item() <= max(1, z.numel() // 1000), "too many z elements differ"
 
 
+# B, S, K, Hq, Hkv, d, interleaved, explicit positions, dtype: the first two
+# take the GEMM's RoPE epilogue, the others its fallback (off the 256 grid,
+# rotated columns not whole 128-column blocks, fp32)
+GEMM_ROPE_CASES = [
+    (2, 256, 512, 4, 2, 128, False, False, torch.bfloat16),
+    (1, 512, 256, 8, 4, 64, True, True, torch.float16),
+    (2, 100, 192, 4, 2, 128, False, True, torch.bfloat16),
+    (2, 128, 256, 2, 1, 64, False, False, torch.bfloat16),
+    (1, 64, 128, 2, 2, 64, True, False, torch.float32),
+]
+
+
+@pytest.mark.parametrize("case", GEMM_ROPE_CASES, ids=lambda c: "-".join(str(v) for v in c))
+def test_gemm_rope_equals_gemm_then_rope(dev, case):
+    """zk_gemm_rope (the q|k|v projection with RoPE in the GEMM's epilogue)
+    writes exactly what the product followed by the RoPE pass writes, for
+    both pairings, explicit positions and the fallback shapes."""
+    from zorse_amd import kernels as K
+    from zorse_amd.functional import rope_tables
+    B, S, Kd, Hq, Hkv, d, inter, explicit, dtype = case
+    print(f"gemm_rope {case}", flush=True)
+    g = torch.Generator().manual_seed(41)
+    N = (Hq + 2 * Hkv) * d
+    x = torch.randn(B * S, Kd, generator=g).to(dtype).to(dev)
+    w = (0.05 * torch.randn(N, Kd, generator=g)).to(dtype).to(dev)
+    n_pos = S + 37 if explicit else S
+    pos = torch.randperm(n_pos, generator=g)[:S].to(torch.int64).to(dev) if explicit else None
+    cos, sin = rope_tables(n_pos, d, 1e4, dtype, dev, inter)
+    got = K.gemm_rope(x, w, seq_len=S, rot_cols=(Hq + Hkv) * d, head_dim=d, cos=cos, sin=sin,
+                      positions=pos, interleaved=inter)
+    ref = K.gemm(x, w)
+    q = ref[:, :Hq * d].view(B, S, Hq, d)
+    k = ref[:, Hq * d:(Hq + Hkv) * d].view(B, S, Hkv, d)
+    K.rope_(q, k, cos, sin, positions=pos, interleaved=inter)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref), (got.float() - ref.float()).abs().max().item()
+
+
 @pytest.mark.parametrize("M,F,K,dtype", [(200, 72, 128, torch.bfloat16), (136, 200, 192, torch.float16),
                                           (8, 8, 64, torch.bfloat16), (1024, 704, 512, torch.bfloat16),
                                           # the 256 x 256 pipeline (M % 256, F % 128, K % 128)

@@ -210,13 +210,14 @@ def _forbid_library_products(monkeypatch):
 @pytest.mark.parametrize("name", list(HIP_GEMM))
 def test_layer_every_product_hand_written(dev, name, monkeypatch):
     """All twelve projection products of a layer step go through the
-    hand-written GEMMs -- the four forward ones (gate|up with the SwiGLU
-    epilogue), the four input gradients dY W on W as stored, and the four
+    hand-written GEMMs -- the four forward ones (q|k|v with RoPE in its
+    epilogue, gate|up with the SwiGLU epilogue), the four input gradients
+    dY W on W as stored, and the four
     weight gradients dY^T X (o and down on the token-major dY, X as stored;
     gate|up and q|k|v on the dY^T the SwiGLU / attention backward kernels
     write from their epilogues) -- each on the MFMA pipeline (zk_gemm_path
-    "tiled"); no torch GEMM and no transpose pass is called.  Parity against
-    the fp64 oracle as every layer test."""
+    "tiled"); no torch GEMM, no transpose pass and no separate RoPE pass is
+    called.  Parity against the fp64 oracle as every layer test."""
     from zorse_amd import kernels as K
     from zorse_amd import layer as LY
     kw, window, dtype, (B, S) = HIP_GEMM[name]
@@ -226,7 +227,7 @@ def test_layer_every_product_hand_written(dev, name, monkeypatch):
     x = torch.randn(B, S, kw["hidden_size"], generator=g).to(dtype)
     dout = torch.randn(B, S, kw["hidden_size"], generator=g).to(dtype)
     calls = []
-    real_gemm, real_swiglu = K.gemm, K.gemm_swiglu
+    real_gemm, real_swiglu, real_rope_gemm = K.gemm, K.gemm_swiglu, K.gemm_rope
 
     def gemm(a, b, *, a_kmajor=False, b_kmajor=False, residual=None, out=None):
         M, Kd = (a.shape[1], a.shape[0]) if a_kmajor else a.shape
@@ -243,12 +244,26 @@ def test_layer_every_product_hand_written(dev, name, monkeypatch):
                                                      a[0].shape[1]) else "general"))
         return real_swiglu(*a, **k)
 
+    def gemm_rope(x, w, **k):
+        # the epilogue takes launches on the tiled grid with head dim 64 / 128
+        # and whole 128-column blocks of rotated heads
+        on = (K.gemm_path(x.shape[0], w.shape[0], x.shape[1], x.stride(0), w.stride(0),
+                          w.shape[0], x.dtype) == "tiled" and k["head_dim"] in (64, 128)
+              and k["rot_cols"] % 128 == 0)
+        calls.append(("gemm_rope", False, False, "tiled" if on else "general"))
+        return real_rope_gemm(x, w, **k)
+
     def no_transpose(*a, **k):
         raise AssertionError("zk_transpose called on the layer's path")
 
+    def no_rope(*a, **k):
+        raise AssertionError("a separate RoPE pass called on the layer's path")
+
     monkeypatch.setattr(K, "gemm", gemm)
     monkeypatch.setattr(K, "gemm_swiglu", gemm_swiglu)
+    monkeypatch.setattr(K, "gemm_rope", gemm_rope)
     monkeypatch.setattr(K, "transpose", no_transpose)
+    monkeypatch.setattr(K, "rope_", no_rope)
     xg = x.to(dev).requires_grad_(True)
     with monkeypatch.context() as m:
         _forbid_library_products(m)
@@ -264,6 +279,7 @@ def test_layer_every_product_hand_written(dev, name, monkeypatch):
     # on the CPU, outside these wrappers)
     assert len(calls) == 12, calls
     assert sum(c[0] == "gemm_swiglu" for c in calls) == 1, calls
+    assert sum(c[0] == "gemm_rope" for c in calls) == 1, calls
     # dY W (4) and the gate|up / q|k|v weight gradients on the dY^T their
     # producers wrote (2); the o / down weight gradients on dY, X as stored (2)
     assert sum(c[1:3] == (False, True) for c in calls) == 6, calls

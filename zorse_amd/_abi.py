@@ -93,6 +93,8 @@ SIGNATURES = {
                                 _ptr]),
     "zk_swiglu_bwd_t": (_int, [_ptr, _i64, _ptr, _ptr, _i64, _ptr, _ptr, _i64, _ptr, _ptr,
                                 _i64, _i64, _i64, _int, _ptr]),
+    "zk_gemm_rope": (_int, [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _i64, _i64,
+                            _i64, _i64, _ptr, _ptr, _i64, _ptr, _int, _int, _ptr]),
     "zk_rope": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _i64,
                        _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _int,
                        _int, _int, _ptr]),

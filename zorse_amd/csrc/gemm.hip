@@ -136,6 +136,67 @@ extern "C" int zk_gemm_nt(const void* a, int64_t lda, const void* b, int64_t ldb
   return zk_gemm(a, lda, 0, b, ldb, 0, c, ldc, r, ldr, M, N, K, dtype, stream);
 }
 
+// The q|k|v projection with the rotary embedding applied in the GEMM's
+// epilogue (EPI 2) when the 256 x 256 pipeline takes the launch; otherwise
+// zk_gemm followed by zk_rope on the rotated columns, which rounds the same.
+extern "C" int zk_gemm_rope(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
+                            int64_t ldc, int64_t M, int64_t N, int64_t K, int64_t S,
+                            int64_t rot_cols, int64_t head_dim, const float* cos,
+                            const float* sin, int64_t n_pos, const int64_t* positions,
+                            int pairing, int dtype, zk_stream_t stream) {
+  ZK_REQUIRE(valid_dtype(dtype), ZK_EDTYPE, "zk_gemm_rope: bad dtype %d", dtype);
+  ZK_REQUIRE(pairing == ZK_ROPE_HALF || pairing == ZK_ROPE_INTERLEAVED, ZK_EINVAL,
+             "zk_gemm_rope: bad pairing %d", pairing);
+  ZK_REQUIRE(M >= 0 && N >= 0 && K >= 0 && S > 0 && M % S == 0, ZK_EINVAL,
+             "zk_gemm_rope: bad shape (M = %lld rows must be whole sequences of S = %lld)",
+             (long long)M, (long long)S);
+  ZK_REQUIRE(head_dim > 0 && head_dim % 2 == 0 && rot_cols >= 0 && rot_cols % head_dim == 0 &&
+                 rot_cols <= N,
+             ZK_EINVAL, "zk_gemm_rope: rotated columns %lld must be whole heads of %lld within N",
+             (long long)rot_cols, (long long)head_dim);
+  ZK_REQUIRE(cos != nullptr && sin != nullptr && n_pos > 0, ZK_EINVAL,
+             "zk_gemm_rope: null or empty rotation table");
+  ZK_REQUIRE(positions != nullptr || n_pos >= S, ZK_EINVAL,
+             "zk_gemm_rope: table has %lld positions < S = %lld", (long long)n_pos, (long long)S);
+  if (M == 0 || N == 0) return ZK_OK;
+  const bool epi = tiled_takes(M, N, K, lda, 0, ldb, 0, ldc, 8, dtype) && aligned(a, 16) &&
+                   aligned(b, 16) && aligned(c, 16) && (head_dim == 64 || head_dim == 128) &&
+                   rot_cols % 128 == 0 && aligned(cos, 16) && aligned(sin, 16) &&
+                   (M / gemm::BM) * (N / gemm::BN) < 0x7fffffffLL;
+  if (!epi) {
+    const int rc = zk_gemm(a, lda, 0, b, ldb, 0, c, ldc, nullptr, 0, M, N, K, dtype, stream);
+    if (rc != ZK_OK || rot_cols == 0) return rc;
+    // the rotated heads as the "q" heads of a [B, S, H, d] view of c
+    return zk_rope(c, S * ldc, ldc, head_dim, nullptr, 0, 0, 0, M / S, S, rot_cols / head_dim,
+                   0, head_dim, cos, sin, n_pos, positions, pairing, 0, dtype, stream);
+  }
+  gemm::GemmArgs ga{};
+  ga.a = a;
+  ga.lda = lda;
+  ga.b = b;
+  ga.ldb = ldb;
+  ga.c = c;
+  ga.ldc = ldc;
+  ga.M = M;
+  ga.N = N;
+  ga.K = K;
+  ga.rcos = cos;
+  ga.rsin = sin;
+  ga.rpos = positions;
+  ga.rnpos = n_pos;
+  ga.rS = S;
+  ga.rcols = rot_cols;
+  ga.rhalf = static_cast<int>(head_dim / 2);
+  ga.rpair = pairing;
+  const dim3 grid(static_cast<unsigned>((M / gemm::BM) * (N / gemm::BN)));
+  hipStream_t s = as_stream(stream);
+  if (dtype == ZK_BF16)
+    hipLaunchKernelGGL((gemm::gemm_tiled_kernel<bf16, 2, false, false>), grid, dim3(256), 0, s, ga);
+  else
+    hipLaunchKernelGGL((gemm::gemm_tiled_kernel<f16, 2, false, false>), grid, dim3(256), 0, s, ga);
+  return launch_status("zk_gemm_rope");
+}
+
 namespace zk {
 
 // The gate|up projection with the SwiGLU epilogue on the 256 x 256 pipeline

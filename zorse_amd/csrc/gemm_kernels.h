@@ -55,6 +55,7 @@
 // with the default.
 #pragma once
 #include "attn_common.h"
+#include "rope_math.h"
 #include "vec.h"
 
 namespace zk {
@@ -95,7 +96,12 @@ __device__ __forceinline__ void dma16(v4i r, uint32_t voff, uint32_t soff, uint3
                :: "v"(voff), "s"(r), "s"(soff), "s"(lds) : "memory", "m0");
 }
 
-// Operands and outputs of one launch.  EPI 0: c = a b^T (+ r); EPI 1 (the
+// Operands and outputs of one launch.  EPI 0: c = a b^T (+ r); EPI 2: c =
+// a b^T with the rotary embedding applied to its first rcols columns (the q
+// and k heads of a q|k|v projection, heads of rhalf * 2 columns, row m the
+// token at sequence position m % rS, position index rpos[m % rS] or m % rS
+// into the fp32 tables rcos / rsin [rnpos, rhalf], pairing rpair), exactly as
+// the RoPE pass would rotate the stored product; EPI 1 (the
 // gate|up projection with the SwiGLU epilogue): b = W_gate, b2 = W_up (each
 // [F, K]), N = 2F, c / c2 = g / u (row stride ldc), z = SwiGLU(g, u) and,
 // when zt is not NULL, zt = z^T.
@@ -115,6 +121,11 @@ struct GemmArgs {
   void* zt;
   int64_t ldzt;
   int64_t M, N, K;
+  const float* rcos;
+  const float* rsin;
+  const int64_t* rpos;
+  int64_t rnpos, rS, rcols;
+  int rhalf, rpair;
 };
 
 // NT tile swizzle: the 16-byte chunk c of row r sits at chunk position
@@ -243,7 +254,7 @@ __device__ __forceinline__ float silu_fast(float g) {
 template <typename T, int EPI, bool AKM, bool BKM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_tiled_kernel(GemmArgs args) {
-  static_assert(EPI == 0 || (!AKM && !BKM), "the SwiGLU epilogue takes NT operands");
+  static_assert(EPI == 0 || (!AKM && !BKM), "the SwiGLU and RoPE epilogues take NT operands");
   const T* __restrict__ A = static_cast<const T*>(args.a);
   const T* __restrict__ B = static_cast<const T*>(args.b);
   const int64_t lda = args.lda, ldb = args.ldb;
@@ -343,7 +354,7 @@ void gemm_tiled_kernel(GemmArgs args) {
       adma.issue(&As[sa * (BM * BK)], Ab + k * a_step, lda, p);
   };
   auto loadB = [&](int sb, int64_t k, int p) __attribute__((always_inline)) {
-    if constexpr (EPI == 0) {
+    if constexpr (EPI != 1) {
       if constexpr (BKM)
         bdmak.issue(Bs(sb), Bb + k * b_step, ldb, p);
       else
@@ -457,7 +468,75 @@ void gemm_tiled_kernel(GemmArgs args) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) ws[(4 * eq + e) * 132 + 16 * j + e16] = acc[i][j][e];
     const int64_t row0 = m0 + wm * 128 + 16 * i;
-    if constexpr (EPI == 0) {
+    // EPI 2: the wave's 128 columns hold whole heads (head dim 2 rhalf = 64
+    // or 128); q / k columns (below rcols) are rotated, v columns stored as is
+    const bool rot = EPI == 2 && n0 + wn * 128 < args.rcols;
+    if (EPI == 2 && rot && args.rpair == ZK_ROPE_HALF) {
+      // 16 rows x 8 chunk pairs: chunk a (first half of its head) with the
+      // chunk rhalf / 8 further; the product rounded to T first, as stored
+      T* C = static_cast<T*>(args.c);
+      const int hc = args.rhalf >> 3;  // chunks per half head: 4 or 8
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int it = q * 64 + el;
+        const int rr = it >> 3, pc = it & 7;
+        const int ca = (pc / hc) * (2 * hc) + pc % hc, cb = ca + hc;
+        const int64_t grow = row0 + rr;
+        const int64_t sq = grow % args.rS;
+        int64_t pos = args.rpos != nullptr ? args.rpos[sq] : sq;
+        pos = pos < 0 ? 0 : pos > args.rnpos - 1 ? args.rnpos - 1 : pos;
+        const int i0 = 8 * (pc % hc);
+        const float* cp = args.rcos + pos * args.rhalf + i0;
+        const float* sp = args.rsin + pos * args.rhalf + i0;
+        const float4 c0 = *reinterpret_cast<const float4*>(cp);
+        const float4 c1 = *reinterpret_cast<const float4*>(cp + 4);
+        const float4 s0 = *reinterpret_cast<const float4*>(sp);
+        const float4 s1 = *reinterpret_cast<const float4*>(sp + 4);
+        const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        T8 o1, o2;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x1 = round_to<T>(ws[rr * 132 + 8 * ca + e]);
+          const float x2 = round_to<T>(ws[rr * 132 + 8 * cb + e]);
+          float y1, y2;
+          rotate_pair<T, ZK_ROPE_HALF, false>(x1, x2, cs[e], sn[e], y1, y2);
+          o1[e] = static_cast<T>(y1);
+          o2[e] = static_cast<T>(y2);
+        }
+        const int64_t gcol = n0 + wn * 128;
+        *reinterpret_cast<T8*>(C + grow * args.ldc + gcol + 8 * ca) = o1;
+        *reinterpret_cast<T8*>(C + grow * args.ldc + gcol + 8 * cb) = o2;
+      }
+    } else if (EPI == 2 && rot) {
+      // interleaved pairs (2 i, 2 i + 1) inside each chunk: 16 rows x 16 chunks
+      T* C = static_cast<T*>(args.c);
+      const int cph = args.rhalf >> 2;  // chunks per head: 8 or 16
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c = q * 64 + el;
+        const int rr = c >> 4, ch = c & 15;
+        const int64_t grow = row0 + rr;
+        const int64_t sq = grow % args.rS;
+        int64_t pos = args.rpos != nullptr ? args.rpos[sq] : sq;
+        pos = pos < 0 ? 0 : pos > args.rnpos - 1 ? args.rnpos - 1 : pos;
+        const int i0 = 4 * (ch % cph);  // first pair of the chunk
+        const float4 cv = *reinterpret_cast<const float4*>(args.rcos + pos * args.rhalf + i0);
+        const float4 sv = *reinterpret_cast<const float4*>(args.rsin + pos * args.rhalf + i0);
+        const float cs[4] = {cv.x, cv.y, cv.z, cv.w}, sn[4] = {sv.x, sv.y, sv.z, sv.w};
+        T8 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float x1 = round_to<T>(ws[rr * 132 + 8 * ch + 2 * j]);
+          const float x2 = round_to<T>(ws[rr * 132 + 8 * ch + 2 * j + 1]);
+          float y1, y2;
+          rotate_pair<T, ZK_ROPE_INTERLEAVED, false>(x1, x2, cs[j], sn[j], y1, y2);
+          o[2 * j] = static_cast<T>(y1);
+          o[2 * j + 1] = static_cast<T>(y2);
+        }
+        *reinterpret_cast<T8*>(C + grow * args.ldc + n0 + wn * 128 + 8 * ch) = o;
+      }
+    } else if constexpr (EPI != 1) {
       // c = acc (+ r), one rounding; 16 rows x 16 chunks of 8 columns
       T* C = static_cast<T*>(args.c);
       const T* R = static_cast<const T*>(args.r);

@@ -4,39 +4,11 @@
 // half-split pairing it reads elements i..i+3 and i+d/2..i+d/2+3, for the
 // interleaved pairing the 8 consecutive elements 2i..2i+7.  cos/sin come
 // from fp32 tables [n_pos, d/2] built by the caller with the reference's
-// own formula, so the kernel only does the rotation arithmetic:
-//   half-split (HF rotate_half, per-op rounding in the storage type):
-//     y1 = r(r(x1 c) + r(-x2 s))      y2 = r(r(x2 c) + r(x1 s))
-//   interleaved (complex product in fp32, one rounding):
-//     y1 = r(x1 c - x2 s)             y2 = r(x1 s + x2 c)
-// The inverse (backward) applies the transpose rotation with the same
-// rounding structure as autograd of those expressions.
-#include "vec.h"
+// own formula, so the kernel only does the rotation arithmetic (rotate_pair,
+// rope_math.h).
+#include "rope_math.h"
 
 namespace zk {
-
-template <typename T, int kPairing, bool kInverse>
-__device__ __forceinline__ void rotate_pair(float x1, float x2, float c,
-                                            float s, float& y1, float& y2) {
-  if (kPairing == ZK_ROPE_HALF) {
-    if (!kInverse) {
-      y1 = round_to<T>(round_to<T>(x1 * c) + round_to<T>(-x2 * s));
-      y2 = round_to<T>(round_to<T>(x2 * c) + round_to<T>(x1 * s));
-    } else {
-      // d/dx of the forward: dx1 = dy1 c + dy2 s, dx2 = dy2 c - dy1 s
-      y1 = round_to<T>(round_to<T>(x1 * c) + round_to<T>(x2 * s));
-      y2 = round_to<T>(round_to<T>(x2 * c) - round_to<T>(x1 * s));
-    }
-  } else {
-    if (!kInverse) {
-      y1 = x1 * c - x2 * s;
-      y2 = x1 * s + x2 * c;
-    } else {
-      y1 = x1 * c + x2 * s;
-      y2 = x2 * c - x1 * s;
-    }
-  }
-}
 
 template <typename T, int kPairing, bool kInverse>
 __global__ __launch_bounds__(256) void rope_kernel(

@@ -49,7 +49,7 @@ extern "C" {
 
 const char* zk_last_error(void) { return zk::g_last_error; }
 
-int zk_abi_version(void) { return 3; }
+int zk_abi_version(void) { return 4; }
 
 int zk_device_info(int device, char* arch, int arch_len, int* num_cus,
                    int* max_clock_khz, int64_t* hbm_bytes) {

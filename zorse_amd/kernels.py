@@ -248,6 +248,52 @@ def gemm(a: torch.Tensor, b: torch.Tensor, *, a_kmajor: bool = False, b_kmajor: 
     return out
 
 
+def gemm_rope(x: torch.Tensor, w: torch.Tensor, *, seq_len: int, rot_cols: int, head_dim: int,
+              cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor | None = None,
+              interleaved: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x W^T with the rotary embedding applied to its first ``rot_cols``
+    columns (whole heads of ``head_dim``), rows being tokens b * seq_len + s
+    (zk_gemm_rope): the q|k|v projection and the RoPE pass in one call, equal
+    to gemm(x, w) followed by rope_ on the q and k heads.  cos / sin /
+    positions as for rope_."""
+    dev = _require_gpu(x, w, cos, sin, positions, out)
+    if x.dtype != w.dtype or x.dtype not in (torch.float32, *_LOWP):
+        raise ValueError(f"gemm_rope: x and w must share a float dtype, got {x.dtype} and {w.dtype}")
+    M, K = x.shape
+    N, Kw = w.shape
+    if Kw != K:
+        raise ValueError(f"gemm_rope: reduction sizes differ ({K} and {Kw})")
+    if head_dim <= 0 or head_dim % 2 or rot_cols < 0 or rot_cols % head_dim or rot_cols > N:
+        raise ValueError(f"gemm_rope: rot_cols {rot_cols} must be whole heads of {head_dim} within {N}")
+    if seq_len <= 0 or M % seq_len:
+        raise ValueError(f"gemm_rope: {M} rows are not whole sequences of {seq_len}")
+    for name, t in (("cos", cos), ("sin", sin)):
+        if t.dtype != torch.float32 or t.dim() != 2 or t.shape[1] != head_dim // 2 \
+                or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous fp32 [n_pos, {head_dim // 2}] table")
+    if cos.shape != sin.shape:
+        raise ValueError("cos and sin tables differ in shape")
+    n_pos = cos.shape[0]
+    if positions is not None:
+        if positions.dtype != torch.int64 or positions.numel() != seq_len \
+                or not positions.is_contiguous():
+            raise ValueError("positions must be a contiguous int64 [seq_len] tensor")
+    elif n_pos < seq_len:
+        raise ValueError(f"table holds {n_pos} positions < seq_len={seq_len}")
+    _, _, lda = _gemm_operand("x", x)
+    _, _, ldb = _gemm_operand("w", w)
+    if out is None:
+        out = torch.empty(M, N, device=dev, dtype=x.dtype)
+    if out.shape != (M, N) or out.dtype != x.dtype:
+        raise ValueError(f"gemm_rope: out must be [{M}, {N}] of the operands' dtype")
+    _, _, ldc = _gemm_operand("out", out)
+    check(lib().zk_gemm_rope(ptr(x), lda, ptr(w), ldb, ptr(out), ldc, M, N, K, seq_len, rot_cols,
+                             head_dim, ptr(cos), ptr(sin), n_pos, ptr(positions),
+                             _abi.ZK_ROPE_INTERLEAVED if interleaved else _abi.ZK_ROPE_HALF,
+                             dtype_code(x.dtype), stream_handle(dev)), "zk_gemm_rope")
+    return out
+
+
 def gemm_path(M: int, N: int, K: int, lda: int, ldb: int, ldc: int, dtype: torch.dtype,
               a_kmajor: bool = False, b_kmajor: bool = False, ldr: int = -1) -> str:
     """Which kernel zk_gemm runs for a launch with 16-byte aligned pointers:

@@ -259,12 +259,15 @@ def layer_forward(x: torch.Tensor, w: FlatViews, spec: LayerSpec, attn_cache=Non
     d, Hq, Hkv = spec.head_dim, spec.heads, spec.kv_heads
     x2 = x.reshape(T, h)
     n1, rstd1, _ = K.rmsnorm_fwd(x2, w.ln1, spec.eps)
-    qkv = _linear(n1, w.qkv)                          # [T, (Hq + 2 Hkv) d]
+    # q|k|v [T, (Hq + 2 Hkv) d] with RoPE applied to the q and k heads in the
+    # GEMM's epilogue (zk_gemm_rope; the same values as the product followed
+    # by the rotation pass)
+    cos, sin = _rope_for(S, spec, x.dtype, x.device, positions)
+    qkv = K.gemm_rope(n1, w.qkv, seq_len=S, rot_cols=spec.q_dim + spec.kv_dim, head_dim=d,
+                      cos=cos, sin=sin, positions=positions, interleaved=spec.interleaved_rope)
     q = qkv[:, :spec.q_dim].view(B, S, Hq, d)
     k = qkv[:, spec.q_dim:spec.q_dim + spec.kv_dim].view(B, S, Hkv, d)
     v = qkv[:, spec.q_dim + spec.kv_dim:].view(B, S, Hkv, d)
-    cos, sin = _rope_for(S, spec, x.dtype, x.device, positions)
-    K.rope_(q, k, cos, sin, positions=positions, interleaved=spec.interleaved_rope)
     hit = attn_cache.take() if attn_cache is not None else None
     if hit is not None:
         o, lse = hit
