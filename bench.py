@@ -434,6 +434,15 @@ def summarize_stage(root: str, layers: int, steps: int, warmup: int) -> str:
         lines.append(f"`adamw_elem` alone (bench.py's `adamw` case after the stage): "
                      f"{len(rest)} launches, {avg / 1e6:.3f} ms on average.  The kernel table "
                      f"below averages both groups together.")
+    nn = [r for r in trace[trace.index(adam[last]) + 1:]
+          if "gemm_tiled_kernel" in r["Kernel_Name"] and "Lb0ELb1E" in r["Kernel_Name"]]
+    if nn:
+        avg = sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in nn) / len(nn)
+        lines.append(f"`gemm_tiled_kernel<bf16,0,false,true>` in bench.py's `gemm_dgrad_gu` case "
+                     f"after the stage (the `roofline` kernel; gate|up input gradient, 4096 x "
+                     f"4096 x 22016): {len(nn)} launches, {avg / 1e6:.3f} ms on average.  In the "
+                     f"stage the same kernel runs every input-gradient shape, so its table "
+                     f"average below mixes them.")
     lines += ["", "All kernels of the run (rocprofv3 `bench_kernel_stats.csv`, top 30):", "",
               "| kernel | calls | total ms | avg us | % |", "|---|---|---|---|---|"]
     stats = list(csv.DictReader(open(os.path.join(root, "bench_kernel_stats.csv"))))
@@ -454,6 +463,8 @@ TRAFFIC_CASES = {
                     ("rmsnorm_bwd_vec", "rmsnorm_dw_reduce")),
     "adamw": ("adamw_elem<bf16,bf16,true>", ("adamw_elem",)),
     "adamw_t": ("adamw_tile_t<bf16,bf16> (layer step with W^T copies)", ("adamw_tile_t",)),
+    "gemm_dgrad_gu": ("gemm_tiled_kernel<bf16,0,false,true> gate|up input grad 4096 x 4096 x 22016",
+                      ("gemm_tiled_kernel",)),
 }
 
 
@@ -537,7 +548,9 @@ def summarize_traffic(root: str) -> str:
             "rmsnorm_bwd": flops.rmsnorm_bwd_bytes(T, h),
             "adamw": flops.adamw_bytes(spec.numel, 2, True),
             "adamw_t": flops.adamw_bytes(spec.numel, 2, True)
-            + 2 * (spec.numel - 2 * spec.hidden)}
+            + 2 * (spec.numel - 2 * spec.hidden),
+            # compulsory bytes of dX = dY W: dY [T, 2F] and W [2F, h] read, dX [T, h] written
+            "gemm_dgrad_gu": 2 * (T * 2 * spec.ffn + 2 * spec.ffn * h + T * h)}
     lines = ["| kernel | FETCH_SIZE (MiB) | WRITE_SIZE (MiB) | HBM traffic (MB) | "
              "algorithmic bytes (MB) | traffic / algorithmic |", "|---|---|---|---|---|---|"]
     machine = []
@@ -638,8 +651,11 @@ def main():
     kern = measure_kernels(dev, spec, S)
     print("kernel timings done", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline(spec, S)
-    # the roofline line: the flat AdamW kernel, one launch over a layer's shard
-    # exactly as the stage's optimizer step makes it
+    # the roofline line: the kernel with the largest share of the stage's
+    # kernel time, the hand-written GEMM in its input-gradient form (the four
+    # dY W products and the gate|up / q|k|v weight gradients on dY^T), at its
+    # largest launch; the HBM-bound AdamW step beside it
+    gm = kern["gemm_dgrad_gu"]
     a = kern["adamw"]
     af, ab = kern["attn_fwd"], kern["attn_bwd"]
     line = {
@@ -668,14 +684,23 @@ def main():
                                        "twelve products per layer, on untransposed operands",
                    "stage_tokens_per_s": round(B * S / (ms_step / 1e3), 1),
                    "layer_fwd_bwd_tflops": round(layer_tflops, 1)},
-        "roofline": {"bound": a["bound"], "achieved": a["achieved"], "peak": a["peak"],
-                     "unit": a["unit"], "frac": a["frac"],
-                     "traffic": a["traffic"],
-                     "kernel": a["kernel"], "avg_ms": a["avg_ms"],
-                     "algorithmic_bytes": a["work_per_launch"],
-                     "scope": "one launch over a layer's flat shard: the stage's whole "
-                              "optimizer step per layer; its 5.7 GB per launch is far larger "
-                              "than the Infinity Cache"},
+        "roofline": {"bound": gm["bound"], "achieved": gm["achieved"], "peak": gm["peak"],
+                     "unit": gm["unit"], "frac": gm["frac"],
+                     "traffic": gm["traffic"],
+                     "kernel": gm["kernel"], "avg_ms": gm["avg_ms"],
+                     "algorithmic_flops": gm["work_per_launch"],
+                     "scope": "the kernel with the largest share of the stage's kernel time "
+                              "(the hand-written GEMM's input-gradient form), at the stage's "
+                              "largest launch of it: dX = dY W for gate|up, 2 x 4096 x 4096 x "
+                              "22016 FLOPs"},
+        "hbm_roofline": {"bound": a["bound"], "achieved": a["achieved"], "peak": a["peak"],
+                         "unit": a["unit"], "frac": a["frac"],
+                         "traffic": a["traffic"],
+                         "kernel": a["kernel"], "avg_ms": a["avg_ms"],
+                         "algorithmic_bytes": a["work_per_launch"],
+                         "scope": "one launch over a layer's flat shard: the stage's whole "
+                                  "optimizer step per layer; its 5.7 GB per launch is far "
+                                  "larger than the Infinity Cache"},
         "attention_roofline": {
             "fwd": {"kernel": af["kernel"], "achieved": af["achieved"], "peak": af["peak"],
                     "unit": "TFLOP/s", "frac": af["frac"], "avg_ms": af["avg_ms"],
