@@ -155,6 +155,24 @@ def test_validation_codes(lib):
                        0, None) == -3
     assert lib.zk_gemm(p, 512, 0, p, 512, 0, p, 256, p, 100, 256, 256, 512, 2, None) == -1
     assert lib.zk_gemm(None, 0, 1, None, 0, 1, None, 0, None, 0, 0, 0, 64, 2, None) == 0
+    # gemm_rope (a [M, K], b [N, K], c [M, N], M = tokens of whole sequences of
+    # S, rotated columns whole heads within N; tables and pairing as zk_rope):
+    # bad dtype, bad pairing, M not whole sequences, rotated columns not whole
+    # heads or past N, null table, short table without positions, ld below
+    # the row length, null operand; zero-size is a no-op
+    g = lambda **kw: lib.zk_gemm_rope(*[kw.get(n, v) for n, v in zip(
+        ("a", "lda", "b", "ldb", "c", "ldc", "M", "N", "K", "S", "rot", "hd", "cos", "sin",
+         "npos", "pos", "pair", "dt", "st"),
+        (p, 512, p, 512, p, 768, 512, 768, 512, 256, 512, 128, p, p, 256, None, 0, 2, None))])
+    assert g(dt=7) == -2
+    assert g(pair=3) == -1
+    assert g(S=300) == -1
+    assert g(rot=500) == -1 and g(rot=1024) == -1
+    assert g(cos=None) == -1
+    assert g(npos=100) == -1
+    assert g(ldc=700) == -1 and g(lda=500) == -1
+    assert g(b=None) == -1
+    assert g(M=0, S=256) == 0
     assert lib.zk_gemm_nt_supported(4096, 22016, 4096) == 1
     assert lib.zk_gemm_nt_supported(4096, 22016, 4160) == 0
     assert lib.zk_gemm_nt_supported(4096, 1376, 4096) == 0

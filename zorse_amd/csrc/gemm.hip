@@ -158,7 +158,13 @@ extern "C" int zk_gemm_rope(const void* a, int64_t lda, const void* b, int64_t l
              "zk_gemm_rope: null or empty rotation table");
   ZK_REQUIRE(positions != nullptr || n_pos >= S, ZK_EINVAL,
              "zk_gemm_rope: table has %lld positions < S = %lld", (long long)n_pos, (long long)S);
+  ZK_REQUIRE(lda >= K && ldb >= K && ldc >= N, ZK_EINVAL, "zk_gemm_rope: bad leading dimension");
+  ZK_REQUIRE(lda < (int64_t(1) << 40) && ldb < (int64_t(1) << 40) && ldc < (int64_t(1) << 40) &&
+                 M < (int64_t(1) << 40) && N < (int64_t(1) << 40),
+             ZK_EINVAL, "zk_gemm_rope: sizes out of range");
   if (M == 0 || N == 0) return ZK_OK;
+  ZK_REQUIRE(c != nullptr && (K == 0 || (a != nullptr && b != nullptr)), ZK_EINVAL,
+             "zk_gemm_rope: null pointer");
   const bool epi = tiled_takes(M, N, K, lda, 0, ldb, 0, ldc, 8, dtype) && aligned(a, 16) &&
                    aligned(b, 16) && aligned(c, 16) && (head_dim == 64 || head_dim == 128) &&
                    rot_cols % 128 == 0 && aligned(cos, 16) && aligned(sin, 16) &&
