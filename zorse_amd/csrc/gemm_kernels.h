@@ -366,8 +366,13 @@ void gemm_tiled_kernel(GemmArgs args) {
   };
   // The 64 MFMAs of set q in rows of eight.  After row c: one load (LK 1: A
   // piece c of step k into ring stage lst; LK 2: B piece c into B stage lst)
-  // and, when RD, operand pieces 2c, 2c + 1 of substep s0 of stages (ra, rb)
-  // into set q0.  The fences keep this order.
+  // and, when RD, two operand pieces of substep s0 of stages (ra, rb) into
+  // set q0, in the order the next set's MFMAs use them: its first row needs
+  // A piece 0 and all eight B pieces, row c A piece c, so the reads go A0,
+  // B0 .. B7, A1 .. A7 (B7 is in flight from row 4, three rows before it is
+  // needed; read last, it stalled the next set's first MFMA for the LDS
+  // latency at every substep).  The fences keep this order.
+  constexpr int kReadOrder[16] = {0, 8, 9, 10, 11, 12, 13, 14, 15, 1, 2, 3, 4, 5, 6, 7};
   auto mm_ld = [&](int q, int lk, int lst, int64_t k, bool rd, int ra, int rb, int s0,
                    int q0) __attribute__((always_inline)) {
 #pragma unroll
@@ -375,8 +380,8 @@ void gemm_tiled_kernel(GemmArgs args) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[c][j] = Mm::mma16(xa[q][c], xb[q][j], acc[c][j]);
       if (rd) {
-        rd_piece(ra, rb, s0, q0, 2 * c);
-        rd_piece(ra, rb, s0, q0, 2 * c + 1);
+        rd_piece(ra, rb, s0, q0, kReadOrder[2 * c]);
+        rd_piece(ra, rb, s0, q0, kReadOrder[2 * c + 1]);
       }
       if (lk == 1) loadA(lst, k, c);
       if (lk == 2) loadB(lst, k, c);
