@@ -530,3 +530,14 @@ def test_hf_factory_routes_structure():
         assert s.head_dim == d and s.ffn == 4 * s.hidden
     with pytest.raises(ValueError):
         H.get_model("llama_7b", layers=1)
+
+
+def test_every_package_module_imports():
+    """Every module of the package imports without a GPU (syntax, names)."""
+    import importlib
+    import zorse_amd
+    pkg = os.path.dirname(zorse_amd.__file__)
+    names = sorted(f[:-3] for f in os.listdir(pkg) if f.endswith(".py") and f != "__init__.py")
+    assert "stage" in names and "layer" in names
+    for name in names:
+        importlib.import_module(f"zorse_amd.{name}")
