@@ -434,7 +434,19 @@ def summarize_stage(root: str, layers: int, steps: int, warmup: int) -> str:
         lines.append(f"`adamw_elem` alone (bench.py's `adamw` case after the stage): "
                      f"{len(rest)} launches, {avg / 1e6:.3f} ms on average.  The kernel table "
                      f"below averages both groups together.")
-    nn = [r for r in trace[trace.index(adam[last]) + 1:]
+    # the attention backward in the stage (beside the previous layer's AdamW
+    # and the weight-gradient GEMMs) against bench.py's attn_bwd case after it
+    after = trace[trace.index(adam[last]) + 1:]
+    for kname in ("attn_bwd_dq", "attn_bwd_dkdv", "attn_fwd_kernel"):
+        ins = [r for r in win if kname in r["Kernel_Name"]]
+        out = [r for r in after if kname in r["Kernel_Name"]]
+        if ins and out:
+            avg_i = sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in ins) / len(ins)
+            avg_o = sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in out) / len(out)
+            lines.append(f"`{kname}` in the stage: {len(ins)} launches, {avg_i / 1e3:.1f} us on "
+                         f"average; alone (bench.py's attention cases after the stage): "
+                         f"{len(out)} launches, {avg_o / 1e3:.1f} us.")
+    nn = [r for r in after
           if "gemm_tiled_kernel" in r["Kernel_Name"] and "Lb0ELb1E" in r["Kernel_Name"]]
     if nn:
         avg = sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in nn) / len(nn)
