@@ -291,6 +291,9 @@ GEMM_ROPE_CASES = [
     (2, 100, 192, 4, 2, 128, False, True, torch.bfloat16),
     (2, 128, 256, 2, 1, 64, False, False, torch.bfloat16),
     (1, 64, 128, 2, 2, 64, True, False, torch.float32),
+    # 200-token sequences: a wave's 128 rows cross a sequence boundary
+    (32, 200, 256, 4, 2, 64, False, True, torch.bfloat16),
+    (32, 200, 256, 2, 1, 128, True, False, torch.float16),
 ]
 
 

@@ -168,6 +168,7 @@ extern "C" int zk_gemm_rope(const void* a, int64_t lda, const void* b, int64_t l
   const bool epi = tiled_takes(M, N, K, lda, 0, ldb, 0, ldc, 8, dtype) && aligned(a, 16) &&
                    aligned(b, 16) && aligned(c, 16) && (head_dim == 64 || head_dim == 128) &&
                    rot_cols % 128 == 0 && aligned(cos, 16) && aligned(sin, 16) &&
+                   S >= 128 && S < (int64_t(1) << 30) && n_pos < (int64_t(1) << 24) &&
                    (M / gemm::BM) * (N / gemm::BN) < 0x7fffffffLL;
   if (!epi) {
     const int rc = zk_gemm(a, lda, 0, b, ldb, 0, c, ldc, nullptr, 0, M, N, K, dtype, stream);

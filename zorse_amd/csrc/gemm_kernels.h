@@ -466,39 +466,60 @@ void gemm_tiled_kernel(GemmArgs args) {
   float* ws = reinterpret_cast<float*>(wave < 3 ? &As[wave * (BM * BK)] : Bs0);
   const int e16 = el & 15, eq = el >> 4;
   typedef T T8 __attribute__((ext_vector_type(8)));
+  // EPI 2: the wave's 128 columns hold whole heads (head dim 2 rhalf = 64 or
+  // 128); q / k columns (below rcols) are rotated, v columns stored as is.
+  // Sequence position of the wave's first row; a row 16 i + r further is at
+  // (rs0 + 16 i + r) mod rS (32-bit: the host keeps rS in [128, 2^30)).
+  const bool rot = EPI == 2 && n0 + wn * 128 < args.rcols;
+  const int rs32 = static_cast<int>(args.rS);
+  const int rs0 = EPI == 2 ? static_cast<int>((m0 + wm * 128) % args.rS) : 0;
+  auto rope_pos = [&](int off) -> int {
+    int sq = rs0 + off;
+    sq = sq >= rs32 ? sq - rs32 : sq;  // the host takes this path for rS >= 128 only
+    int64_t pos = args.rpos != nullptr ? args.rpos[sq] : sq;
+    pos = pos < 0 ? 0 : pos > args.rnpos - 1 ? args.rnpos - 1 : pos;
+    return static_cast<int>(pos) * args.rhalf;  // table offset (host: below 2^31)
+  };
+  // chunks per half head (half-split) / per head (interleaved): powers of two
+  const int hcl = args.rhalf == 64 ? 3 : 2, hcm = (1 << hcl) - 1;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
+    // EPI 2, half-split pairing: this block's cos / sin, loaded before the
+    // staging stores below so that their latency overlaps them
+    float4 rc0[2], rc1[2], rsn0[2], rsn1[2];
+    if (EPI == 2 && rot && args.rpair == ZK_ROPE_HALF) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int it = q * 64 + el;
+        const int toff = rope_pos(16 * i + (it >> 3)) + 8 * ((it & 7) & hcm);
+        const float* cp = args.rcos + toff;
+        const float* sp = args.rsin + toff;
+        rc0[q] = *reinterpret_cast<const float4*>(cp);
+        rc1[q] = *reinterpret_cast<const float4*>(cp + 4);
+        rsn0[q] = *reinterpret_cast<const float4*>(sp);
+        rsn1[q] = *reinterpret_cast<const float4*>(sp + 4);
+      }
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e) ws[(4 * eq + e) * 132 + 16 * j + e16] = acc[i][j][e];
     const int64_t row0 = m0 + wm * 128 + 16 * i;
-    // EPI 2: the wave's 128 columns hold whole heads (head dim 2 rhalf = 64
-    // or 128); q / k columns (below rcols) are rotated, v columns stored as is
-    const bool rot = EPI == 2 && n0 + wn * 128 < args.rcols;
     if (EPI == 2 && rot && args.rpair == ZK_ROPE_HALF) {
       // 16 rows x 8 chunk pairs: chunk a (first half of its head) with the
       // chunk rhalf / 8 further; the product rounded to T first, as stored
       T* C = static_cast<T*>(args.c);
-      const int hc = args.rhalf >> 3;  // chunks per half head: 4 or 8
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const int it = q * 64 + el;
         const int rr = it >> 3, pc = it & 7;
-        const int ca = (pc / hc) * (2 * hc) + pc % hc, cb = ca + hc;
+        // chunks per half head hc = 2^hcl (4 or 8)
+        const int ca = ((pc >> hcl) << (hcl + 1)) + (pc & hcm), cb = ca + (1 << hcl);
         const int64_t grow = row0 + rr;
-        const int64_t sq = grow % args.rS;
-        int64_t pos = args.rpos != nullptr ? args.rpos[sq] : sq;
-        pos = pos < 0 ? 0 : pos > args.rnpos - 1 ? args.rnpos - 1 : pos;
-        const int i0 = 8 * (pc % hc);
-        const float* cp = args.rcos + pos * args.rhalf + i0;
-        const float* sp = args.rsin + pos * args.rhalf + i0;
-        const float4 c0 = *reinterpret_cast<const float4*>(cp);
-        const float4 c1 = *reinterpret_cast<const float4*>(cp + 4);
-        const float4 s0 = *reinterpret_cast<const float4*>(sp);
-        const float4 s1 = *reinterpret_cast<const float4*>(sp + 4);
-        const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-        const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        const float cs[8] = {rc0[q].x, rc0[q].y, rc0[q].z, rc0[q].w,
+                             rc1[q].x, rc1[q].y, rc1[q].z, rc1[q].w};
+        const float sn[8] = {rsn0[q].x, rsn0[q].y, rsn0[q].z, rsn0[q].w,
+                             rsn1[q].x, rsn1[q].y, rsn1[q].z, rsn1[q].w};
         T8 o1, o2;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -516,18 +537,15 @@ void gemm_tiled_kernel(GemmArgs args) {
     } else if (EPI == 2 && rot) {
       // interleaved pairs (2 i, 2 i + 1) inside each chunk: 16 rows x 16 chunks
       T* C = static_cast<T*>(args.c);
-      const int cph = args.rhalf >> 2;  // chunks per head: 8 or 16
+      const int cpm = (args.rhalf >> 2) - 1;  // chunks per head (8 or 16), less one
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int c = q * 64 + el;
         const int rr = c >> 4, ch = c & 15;
         const int64_t grow = row0 + rr;
-        const int64_t sq = grow % args.rS;
-        int64_t pos = args.rpos != nullptr ? args.rpos[sq] : sq;
-        pos = pos < 0 ? 0 : pos > args.rnpos - 1 ? args.rnpos - 1 : pos;
-        const int i0 = 4 * (ch % cph);  // first pair of the chunk
-        const float4 cv = *reinterpret_cast<const float4*>(args.rcos + pos * args.rhalf + i0);
-        const float4 sv = *reinterpret_cast<const float4*>(args.rsin + pos * args.rhalf + i0);
+        const int toff = rope_pos(16 * i + rr) + 4 * (ch & cpm);  // the chunk's first pair
+        const float4 cv = *reinterpret_cast<const float4*>(args.rcos + toff);
+        const float4 sv = *reinterpret_cast<const float4*>(args.rsin + toff);
         const float cs[4] = {cv.x, cv.y, cv.z, cv.w}, sn[4] = {sv.x, sv.y, sv.z, sv.w};
         T8 o;
 #pragma unroll
