@@ -207,17 +207,20 @@ def _forbid_library_products(monkeypatch):
     monkeypatch.setattr(torch.Tensor, "__matmul__", forbidden("Tensor.__matmul__"))
 
 
+@pytest.mark.parametrize("transposed", [False, True], ids=["dY", "dYt"])
 @pytest.mark.parametrize("name", list(HIP_GEMM))
-def test_layer_every_product_hand_written(dev, name, monkeypatch):
+def test_layer_every_product_hand_written(dev, name, transposed, monkeypatch):
     """All twelve projection products of a layer step go through the
     hand-written GEMMs -- the four forward ones (q|k|v with RoPE in its
     epilogue, gate|up with the SwiGLU epilogue), the four input gradients
     dY W on W as stored, and the four
     weight gradients dY^T X (o and down on the token-major dY, X as stored;
     gate|up and q|k|v on the dY^T the SwiGLU / attention backward kernels
-    write from their epilogues) -- each on the MFMA pipeline (zk_gemm_path
-    "tiled"); no torch GEMM, no transpose pass and no separate RoPE pass is
-    called.  Parity against the fp64 oracle as every layer test."""
+    write from their epilogues, or with set_transposed_wgrad(False) on dY as
+    stored too) -- each on the
+    MFMA pipeline (zk_gemm_path "tiled"); no torch GEMM, no transpose pass
+    and no separate RoPE pass is called.  Parity against the fp64 oracle as
+    every layer test."""
     from zorse_amd import kernels as K
     from zorse_amd import layer as LY
     kw, window, dtype, (B, S) = HIP_GEMM[name]
@@ -268,22 +271,26 @@ def test_layer_every_product_hand_written(dev, name, monkeypatch):
     with monkeypatch.context() as m:
         _forbid_library_products(m)
         prev = LY.set_fused_gate_up(True)
+        prev_t = LY.set_transposed_wgrad(transposed)
         try:
             out = layer(xg)[0]
             out.backward(dout.to(dev))
             torch.cuda.synchronize()
         finally:
             LY.set_fused_gate_up(prev)
-    _compare_layer(layer, x, xg, out, dout, dtype, f"{name} hand-written GEMMs")
+            LY.set_transposed_wgrad(prev_t)
+    _compare_layer(layer, x, xg, out, dout, dtype,
+                   f"{name} hand-written GEMMs" + (" (dY^T)" if transposed else ""))
     # the layer step itself: 4 forward + 8 backward products (the oracle runs
     # on the CPU, outside these wrappers)
     assert len(calls) == 12, calls
     assert sum(c[0] == "gemm_swiglu" for c in calls) == 1, calls
     assert sum(c[0] == "gemm_rope" for c in calls) == 1, calls
-    # dY W (4) and the gate|up / q|k|v weight gradients on the dY^T their
-    # producers wrote (2); the o / down weight gradients on dY, X as stored (2)
-    assert sum(c[1:3] == (False, True) for c in calls) == 6, calls
-    assert sum(c[1:3] == (True, True) for c in calls) == 2, calls
+    # dY W (4), plus the gate|up / q|k|v weight gradients when they read the
+    # dY^T their producers wrote (2); the other weight gradients on dY, X as
+    # stored
+    assert sum(c[1:3] == (False, True) for c in calls) == (6 if transposed else 4), calls
+    assert sum(c[1:3] == (True, True) for c in calls) == (2 if transposed else 4), calls
     assert all(c[3] == "tiled" for c in calls), calls
 
 

@@ -126,10 +126,33 @@ def _wgrad(dy, x, out, dyt=None):
         K.gemm(dy, x, a_kmajor=True, b_kmajor=True, out=out)
 
 
+# The gate|up and q|k|v weight gradients dY^T X read dY either K-major as the
+# input-gradient chain holds it (both operands K-major) or from a dY^T that the
+# SwiGLU / attention backward kernels also write from their epilogues (the
+# input-gradient form).  The K-major form of those two products is only 1-3 %
+# slower (alone, 7B shapes), and in the 7B stage (one process, alternating,
+# three rounds, on two boxes) the two arrangements measured equal: 42.30-42.48
+# ms/step without the transposed copies against 42.37-42.56 with them.  On by
+# default; set_transposed_wgrad(False) or ZORSE_TRANSPOSED_WGRAD=0 writes no
+# copies (280 MB less written and allocated per layer backward).
+_transposed_wgrad = os.environ.get("ZORSE_TRANSPOSED_WGRAD", "1") != "0"
+
+
+def set_transposed_wgrad(enable: bool) -> bool:
+    """Take the gate|up and q|k|v weight gradients from the dY^T the SwiGLU /
+    attention backward write (True) or from dY as stored (False); returns the
+    previous setting."""
+    global _transposed_wgrad
+    prev, _transposed_wgrad = _transposed_wgrad, bool(enable)
+    return prev
+
+
 def _transposed_outputs(t):
-    """True when the SwiGLU / attention backward kernels can also write their
-    result transposed (2-byte types, token counts multiples of 8)."""
-    return t.dtype in (torch.bfloat16, torch.float16) and t.shape[0] % 8 == 0
+    """True when the SwiGLU / attention backward kernels are to write their
+    result transposed as well (enabled, 2-byte types, token counts multiples
+    of 8)."""
+    return (_transposed_wgrad and t.dtype in (torch.bfloat16, torch.float16)
+            and t.shape[0] % 8 == 0)
 
 
 # The four weight-gradient GEMMs of a layer's backward are off its critical
