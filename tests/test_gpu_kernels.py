@@ -278,7 +278,9 @@ def _assert_z_of_gu(z, gu, F, dtype):
     ulp, tiny = {torch.bfloat16: (2.0 ** -7, 2.0 ** -133), torch.float16: (2.0 ** -10, 2.0 ** -24)}[dtype]
     _, ex = torch.frexp(torch.maximum(z.double().abs(), ref.double().abs()).clamp_min(1e-30))
     one = torch.ldexp(torch.full_like(diff, ulp), ex - 1).clamp_min(tiny)
-    assert (diff.abs() <= 2 * one).all(), "z more than two ulps from the SwiGLU kernel"
+    # (1 + 1e-12): torch.ldexp may land one double ulp off the exact power of
+    # two, and a difference of exactly two storage ulps must pass
+    assert (diff.abs() <= 2 * one * (1 + 1e-12)).all(), "z more than two ulps from the SwiGLU kernel"
     assert (diff != 0).sum().item() <= max(1, z.numel() // 1000), "too many z elements differ"
 
 
