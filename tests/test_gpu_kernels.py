@@ -285,14 +285,18 @@ def _assert_z_of_gu(z, gu, F, dtype):
 
 
 # B, S, K, Hq, Hkv, d, interleaved, explicit positions, dtype: the first two
-# take the GEMM's RoPE epilogue, the others its fallback (off the 256 grid,
-# rotated columns not whole 128-column blocks, fp32)
+# and the 200-token ones take the GEMM's RoPE epilogue, the others the product
+# and the pass (off the 256 grid, rotated columns not whole 128-column blocks,
+# fp32, sequences under 128 tokens)
 GEMM_ROPE_CASES = [
     (2, 256, 512, 4, 2, 128, False, False, torch.bfloat16),
     (1, 512, 256, 8, 4, 64, True, True, torch.float16),
     (2, 100, 192, 4, 2, 128, False, True, torch.bfloat16),
     (2, 128, 256, 2, 1, 64, False, False, torch.bfloat16),
     (1, 64, 128, 2, 2, 64, True, False, torch.float32),
+    # 64-token sequences: on the GEMM's grid, but below the epilogue's 128
+    # (the product and the pass)
+    (4, 64, 256, 4, 2, 64, False, True, torch.bfloat16),
     # 200-token sequences: a wave's 128 rows cross a sequence boundary
     (32, 200, 256, 4, 2, 64, False, True, torch.bfloat16),
     (32, 200, 256, 2, 1, 128, True, False, torch.float16),
