@@ -98,7 +98,11 @@ class KernelCases:
 
     NAMES = ("attn_fwd", "attn_bwd", "rmsnorm_fwd", "rmsnorm_bwd", "adamw", "adamw_t", "copy",
              "gemm_gu", "gemm_dgrad_gu", "gemm_wgrad_gu", "blas_gu", "blas_dgrad_gu",
-             "blas_wgrad_gu", "rope")
+             "blas_wgrad_gu", "rope", "lm_head", "lm_head_chunked", "lm_head_torch")
+
+    # the last stage's LM head: the reference's default vocabulary
+    # (models/llama_simple.py:559-561, vocab 49152)
+    VOCAB = 49152
 
     def __init__(self, dev, spec, S):
         self.dev, self.spec, self.S = dev, spec, S
@@ -228,6 +232,31 @@ class KernelCases:
             if hand:
                 return (lambda: K.gemm(a, w, out=y)), work
             return (lambda: torch.mm(a, w.t(), out=y)), work
+        if name in ("lm_head", "lm_head_chunked", "lm_head_torch"):
+            # LM head + cross-entropy fwd + bwd on [T, h] final hidden states:
+            # lm_head the default chunking (here one chunk: 403 MB of logits,
+            # kept for the backward), lm_head_chunked 8192-column chunks
+            # (logits recomputed in the backward), lm_head_torch F.linear +
+            # F.cross_entropy (hipBLASLt, [T, V] logits and their fp32
+            # softmax) as a reference point.  Work: the three products, 6 T h V
+            # (the chunked form runs a fourth, its recomputation)
+            from zorse_amd.lm_head import lm_head_cross_entropy
+            V = self.VOCAB
+            x = torch.randn(T, h, device=dev, dtype=torch.bfloat16).requires_grad_(True)
+            w = (0.02 * torch.randn(V, h, device=dev, dtype=torch.bfloat16)).requires_grad_(True)
+            labels = torch.randint(0, V, (T,), device=dev)
+            chunk = 8192 if name == "lm_head_chunked" else None
+
+            def run():
+                x.grad = None
+                w.grad = None
+                if name == "lm_head_torch":
+                    loss = torch.nn.functional.cross_entropy(
+                        torch.nn.functional.linear(x, w).float(), labels)
+                else:
+                    loss = lm_head_cross_entropy(x, w, labels, chunk=chunk)
+                loss.backward()
+            return run, 6 * T * h * V
         if name == "copy":
             src = torch.empty(1 << 28, device=dev, dtype=torch.float32).normal_()
             dst = torch.empty_like(src)
@@ -261,6 +290,12 @@ def measure_kernels(dev, spec, S):
                           "mfma", 10),
         "blas_wgrad_gu": ("hipBLASLt gate|up weight grad, same operands (reference point)",
                           "mfma", 10),
+        "lm_head": ("LM head + CE fwd+bwd, 4096 x 4096 x 49152, default chunking: one chunk, "
+                    "logits kept (zk_gemm + zk_ce_*_chunk)", "mfma", 8),
+        "lm_head_chunked": ("LM head + CE fwd+bwd, 4096 x 4096 x 49152, 8192-column chunks "
+                            "(logits recomputed)", "mfma", 8),
+        "lm_head_torch": ("torch F.linear + F.cross_entropy fwd+bwd, same operands (reference "
+                          "point)", "mfma", 8),
     }
     for name, (kname, bound, iters) in spec_of.items():
         run, work = cases.make(name)

@@ -541,3 +541,16 @@ def test_every_package_module_imports():
     assert "stage" in names and "layer" in names
     for name in names:
         importlib.import_module(f"zorse_amd.{name}")
+
+
+def test_lm_head_default_chunk():
+    """The LM head keeps the whole vocabulary's logits while they take at most
+    1 GiB (the 7B head at 4096 tokens: 403 MB) and chunks by 8192 columns
+    beyond."""
+    import torch
+    from zorse_amd.lm_head import SINGLE_CHUNK_BYTES, default_chunk
+    assert default_chunk(4096, 49152, torch.bfloat16) == 49152
+    assert default_chunk(4096, 49152, torch.float32) == 49152
+    assert default_chunk(16384, 128256, torch.bfloat16) == 8192
+    assert default_chunk(SINGLE_CHUNK_BYTES // 2, 1, torch.bfloat16) == 1
+    assert default_chunk(SINGLE_CHUNK_BYTES // 2 + 1, 1, torch.bfloat16) == 8192

@@ -803,6 +803,38 @@ def test_lm_head_cross_entropy_chunked(dev, dtype, V, chunk):
     assert_close(wd.grad, wr.grad, dtype, "dW")
 
 
+def test_lm_head_single_chunk_keeps_logits(dev):
+    """chunk >= vocab: the forward's logits are reused by the backward (no
+    recomputation); the gradients agree with the chunked path's within the
+    bf16 bar against fp64, and a second backward through a retained graph
+    (the kept logits already overwritten) recomputes them and gives the same
+    gradients again."""
+    from zorse_amd.lm_head import lm_head_cross_entropy
+    g = torch.Generator().manual_seed(71)
+    T, h, V = 128, 256, 2048
+    x = torch.randn(T, h, generator=g).to(torch.bfloat16)
+    w = (0.05 * torch.randn(V, h, generator=g)).to(torch.bfloat16)
+    labels = torch.randint(0, V, (T,), generator=g)
+    labels[::5] = -100
+    xr = x.double().requires_grad_(True)
+    wr = w.double().requires_grad_(True)
+    torch.nn.functional.cross_entropy(xr @ wr.t(), labels, ignore_index=-100).backward()
+    grads = []
+    for chunk in (V, 512):
+        xd = x.to(dev).requires_grad_(True)
+        wd = w.to(dev).requires_grad_(True)
+        loss = lm_head_cross_entropy(xd, wd, labels.to(dev), chunk=chunk)
+        loss.backward(retain_graph=True)
+        first = (xd.grad.clone(), wd.grad.clone())
+        xd.grad = None
+        wd.grad = None
+        loss.backward()
+        assert torch.equal(xd.grad, first[0]) and torch.equal(wd.grad, first[1]), chunk
+        assert_close(xd.grad, xr.grad, torch.bfloat16, f"dx chunk {chunk}")
+        assert_close(wd.grad, wr.grad, torch.bfloat16, f"dW chunk {chunk}")
+        grads.append(first)
+
+
 @pytest.mark.parametrize("nbytes,blocks", [(16, 1), (1000003, 16), (32 << 20, 16),
                                            (32 << 20, 1), (5 << 20, 64)])
 def test_copy_host_round_trip(dev, nbytes, blocks):
