@@ -478,9 +478,10 @@ void gemm_tiled_kernel(GemmArgs args) {
     sq = sq >= rs32 ? sq - rs32 : sq;  // the host takes this path for rS >= 128 only
     int64_t pos = args.rpos != nullptr ? args.rpos[sq] : sq;
     pos = pos < 0 ? 0 : pos > args.rnpos - 1 ? args.rnpos - 1 : pos;
-    return static_cast<int>(pos) * args.rhalf;  // table offset (host: below 2^31)
+    return static_cast<int>(pos) * args.rhalf;  // table offset (host: positions below 2^24)
   };
-  // chunks per half head (half-split) / per head (interleaved): powers of two
+  // half-split pairing: 8-column chunks per half head, 2^hcl (8 for head dim
+  // 128, 4 for 64)
   const int hcl = args.rhalf == 64 ? 3 : 2, hcm = (1 << hcl) - 1;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
