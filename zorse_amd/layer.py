@@ -156,13 +156,19 @@ def _transposed_outputs(t):
 
 
 # The four weight-gradient GEMMs of a layer's backward are off its critical
-# path: nothing in the layer's backward reads them.  With a side stream they
-# run beside the input-gradient chain (dgrad GEMMs, SwiGLU / RMSNorm / attention
-# backward), so the partial last round of one GEMM's tiles (e.g. 1376 tiles of
-# the gate|up weight gradient on 256 CUs) fills with work of the other instead
-# of idling.  The layer's backward joins the side stream before it returns its
-# gradient.  ZORSE_WGRAD_STREAM=0 or set_wgrad_stream(False) runs them in order
-# on the compute stream.
+# path: nothing in the layer's backward reads them.  Those of down_proj and
+# o_proj run on a side stream beside the input-gradient chain (the down
+# input-gradient GEMM and the SwiGLU backward; the attention backward), so the
+# partial last round of one GEMM's tiles fills with work of the other instead
+# of idling; those of gate|up and q|k|v run in order on the compute stream.
+# The layer's backward joins the side stream before it returns its gradient,
+# and a cross-stream wait costs ~25 us on this GPU before the waiting queue's
+# next kernel starts: with q|k|v's product last on the side stream, the join
+# waited for it every layer.  7B stage, one process, alternating, two boxes:
+# 41.39-41.54 ms/step this way, 41.52-41.68 with all four on the side stream,
+# 41.98-42.03 with all four in order, 41.54-41.66 with only gate|up in order.
+# ZORSE_WGRAD_STREAM=0 or set_wgrad_stream(False) runs all four in order on the
+# compute stream.
 _wgrad_side = os.environ.get("ZORSE_WGRAD_STREAM", "1") != "0"
 _side_streams: dict = {}
 
@@ -189,8 +195,8 @@ class _WeightGrads:
                 self.side = _side_streams[device] = torch.cuda.Stream(device=device)
             grad_flat.record_stream(self.side)
 
-    def __call__(self, dy, x, out, dyt=None):
-        if self.side is None:
+    def __call__(self, dy, x, out, dyt=None, in_order=False):
+        if self.side is None or in_order:
             _wgrad(dy, x, out, dyt)
             return
         self.side.wait_stream(self.main)
@@ -354,7 +360,7 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
     else:
         K.swiglu_bwd(dz, gu[:, :F], gu[:, F:], dgu[:, :F], dgu[:, F:])
     del dz
-    wgrad(dgu, n2, g.gu, dgut)
+    wgrad(dgu, n2, g.gu, dgut, in_order=True)
     dn2 = _dgrad(dgu, w.gu)                          # [T, h]
     del dgu, dgut
     dh, _ = K.rmsnorm_bwd(dn2, hdn, w.ln2, rstd2, dres=dout2, dw=g.ln2)
@@ -397,7 +403,7 @@ def layer_backward(dout: torch.Tensor, saved, w: FlatViews, spec: LayerSpec,
         K.rope_(dq, dk, cos, sin, positions=positions, interleaved=spec.interleaved_rope,
                 inverse=True)
     del do2
-    wgrad(dqkv, n1, g.qkv, dqkvt)
+    wgrad(dqkv, n1, g.qkv, dqkvt, in_order=True)
     dn1 = _dgrad(dqkv, w.qkv)                        # [T, h]
     del dqkv, dqkvt
     dx, _ = K.rmsnorm_bwd(dn1, x2, w.ln1, rstd1, dres=dh, dw=g.ln1)
