@@ -132,9 +132,12 @@ def _wgrad(dy, x, out, dyt=None):
 # input-gradient form).  The K-major form of those two products is only 1-3 %
 # slower (alone, 7B shapes), and in the 7B stage (one process, alternating,
 # three rounds, on two boxes) the two arrangements measured equal: 42.30-42.48
-# ms/step without the transposed copies against 42.37-42.56 with them.  On by
-# default; set_transposed_wgrad(False) or ZORSE_TRANSPOSED_WGRAD=0 writes no
-# copies (280 MB less written and allocated per layer backward).
+# ms/step without the transposed copies against 42.37-42.56 with them; with
+# those two products in order on the compute stream, 40.87-40.91 without
+# against 40.95-41.10 with (one box, four alternating rounds).  On by default,
+# which keeps the input-gradient form the stage's dominant kernel;
+# set_transposed_wgrad(False) or ZORSE_TRANSPOSED_WGRAD=0 writes no copies
+# (280 MB less written and allocated per layer backward).
 _transposed_wgrad = os.environ.get("ZORSE_TRANSPOSED_WGRAD", "1") != "0"
 
 
