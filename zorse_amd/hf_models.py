@@ -93,8 +93,9 @@ class CausalLM(nn.Module):
     ``lm_head``.  forward(input_ids, labels) returns an object with ``loss``
     and ``logits`` as HF's CausalLMOutputWithPast does: with labels, the
     causal-LM loss (position t predicts label t + 1, mean over labels other
-    than -100) from the chunked-vocabulary head, without materialising the
-    logits (``logits`` is None); without labels, the logits."""
+    than -100) from the LM-head kernels (lm_head.lm_head_cross_entropy: the
+    logits never returned, held whole only up to 1 GiB; ``logits`` is None);
+    without labels, the logits."""
 
     def __init__(self, config, sliding_window=None, **layer_kw):
         super().__init__()
