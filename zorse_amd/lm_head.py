@@ -137,9 +137,10 @@ def lm_head_cross_entropy(x, weight, labels, chunk: int | None = None, ignore_in
 
 
 class OutputLayerLoss(torch.nn.Module):
-    """norm -> lm_head -> cross-entropy, the last stage's tail, without the
-    [tokens, vocab] logits: wraps an existing ``norm`` (RMSNorm module) and
-    ``lm_head`` (nn.Linear without bias)."""
+    """norm -> lm_head -> cross-entropy, the last stage's tail, returning only
+    the loss (the logits are kept whole for the backward only while they take
+    at most SINGLE_CHUNK_BYTES, see default_chunk): wraps an existing ``norm``
+    (RMSNorm module) and ``lm_head`` (nn.Linear without bias)."""
 
     def __init__(self, norm, lm_head, chunk: int | None = None):
         super().__init__()
