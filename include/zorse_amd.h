@@ -226,8 +226,9 @@ int zk_rope(void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh, void* k,
  * (models/llama_simple.py:27-58) or apply_rotary_emb (models/llama_v2.py:
  * 151-177).  Rows are tokens b S + s (M a multiple of S); positions, tables
  * and pairing as for zk_rope.  bf16 / fp16 products on the 256 x 256 grid
- * with head_dim 64 / 128 and rot_cols a multiple of 128 rotate in the GEMM's
- * epilogue; other launches run zk_gemm then zk_rope (same result). */
+ * with head_dim 64 / 128, rot_cols a multiple of 128, S in [128, 2^30) and
+ * fewer than 2^24 table positions rotate in the GEMM's epilogue; other
+ * launches run zk_gemm then zk_rope (same result). */
 int zk_gemm_rope(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
                  int64_t ldc, int64_t M, int64_t N, int64_t K, int64_t S,
                  int64_t rot_cols, int64_t head_dim, const float* cos,
