@@ -267,6 +267,30 @@ def test_gemm_nt_llama7b_shapes(dev):
         del a, b, r, out, ref
 
 
+@pytest.mark.parametrize("b_km", [False, True], ids=["X_Wt", "dY_W"])
+def test_gemm_half_tiles_equal_full_tiles(dev, b_km):
+    """A product whose 256 x 256 tiles fill at most half the CUs runs on
+    128 x 256 tiles (4096 x 2048: 128 tiles); stacked twice along M (8192 x
+    2048: 256 tiles) it runs on the full tiles. Both sum every output in
+    the same order, so the halves are bit-identical to the small product,
+    which is within one ulp of the fp64 one."""
+    from zorse_amd import kernels as K_
+    M, N, Kd = 4096, 2048, 2048
+    cus = K_.device_info(dev.index or 0)["num_cus"]
+    print(f"gemm half tiles {M}x{N}x{Kd} b_kmajor={b_km} cus={cus}", flush=True)
+    if cus < 2 * (M // 256) * (N // 256) or cus >= 2 * (2 * M // 256) * (N // 256):
+        pytest.skip(f"{cus} CUs: both products take the same tile height")
+    g = torch.Generator(device="cpu").manual_seed(88)
+    a = torch.randn(M, Kd, generator=g).to(dev, torch.bfloat16)
+    b = (0.05 * torch.randn(*((Kd, N) if b_km else (N, Kd)), generator=g)).to(dev, torch.bfloat16)
+    small = K_.gemm(a, b, b_kmajor=b_km)
+    big = K_.gemm(torch.cat([a, a.flip(0)]), b, b_kmajor=b_km)
+    assert torch.equal(big[:M], small)
+    assert torch.equal(big[M:], small.flip(0))
+    ref = torch.mm(a.double(), b.double() if b_km else b.double().t())
+    _assert_within_ulp(small, ref, torch.bfloat16, "gemm 128 x 256 tiles")
+
+
 def _assert_z_of_gu(z, gu, F, dtype):
     """z against the SwiGLU kernel on the returned g, u: the same rounding
     points, and with the epilogue's hardware exp2 / reciprocal (the 256 x 256

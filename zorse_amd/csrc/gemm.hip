@@ -52,8 +52,12 @@ void launch_gemm(bool tiled, const gemm::GemmArgs& ga, hipStream_t s) {
         gemm::launch_tiled_kmajor(std::is_same<T, bf16>::value, AKM, BKM, ga, s);
       } else {
         const int64_t nwg = (ga.M / gemm::BM) * (ga.N / gemm::BN);
-        hipLaunchKernelGGL((gemm::gemm_tiled_kernel<T, 0, false, false>),
-                           dim3(static_cast<unsigned>(nwg)), dim3(256), 0, s, ga);
+        if (gemm::half_tiles(nwg))
+          hipLaunchKernelGGL((gemm::gemm_tiled_kernel<T, 0, false, false, 4>),
+                             dim3(static_cast<unsigned>(2 * nwg)), dim3(256), 0, s, ga);
+        else
+          hipLaunchKernelGGL((gemm::gemm_tiled_kernel<T, 0, false, false>),
+                             dim3(static_cast<unsigned>(nwg)), dim3(256), 0, s, ga);
       }
       return;
     }

@@ -251,24 +251,50 @@ __device__ __forceinline__ float silu_fast(float g) {
 
 // AKM / BKM: operand A / B is K-major (see the top of the file).  EPI 1
 // takes NT operands only.
-template <typename T, int EPI, bool AKM, bool BKM>
+// Products with A along the reduction whose 256 x 256 tiles would occupy at
+// most half the CUs (e.g. a 4096 x 2048 product: 128 tiles on 256 CUs) run on
+// 128 x 256 tiles instead, twice the workgroups with half the work each and
+// every output summed in the same order.
+inline bool half_tiles(int64_t nwg) { return nwg > 0 && 2 * nwg <= device_cus(); }
+
+// Operand-read order of a set (see mm_ld): A0, B0 .. B7, A1 .. A(MB-1), with
+// A pieces numbered 0 .. MB-1 and B pieces MB .. MB+7.
+struct ReadOrder {
+  int v[16];
+};
+template <int MB>
+constexpr ReadOrder read_order() {
+  ReadOrder r{};
+  r.v[0] = 0;
+  for (int i = 1; i <= 8; ++i) r.v[i] = MB + i - 1;
+  for (int i = 9; i < MB + 8; ++i) r.v[i] = i - 8;
+  return r;
+}
+
+// MB: 16-row MFMA blocks per wave along M -- 8 (the 256 x 256 tile) or 4 (a
+// 128 x 256 tile: for a product whose 256 x 256 tiles would occupy at most
+// half the CUs, twice the workgroups with half the work each).
+template <typename T, int EPI, bool AKM, bool BKM, int MB = 8>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_tiled_kernel(GemmArgs args) {
   static_assert(EPI == 0 || (!AKM && !BKM), "the SwiGLU and RoPE epilogues take NT operands");
+  static_assert(MB == 8 || (MB == 4 && EPI == 0 && !AKM), "128-row tiles: plain epilogue, A along K");
+  constexpr int TBM = 32 * MB;  // tile rows
+  constexpr int WR = 16 * MB;   // rows per wave
   const T* __restrict__ A = static_cast<const T*>(args.a);
   const T* __restrict__ B = static_cast<const T*>(args.b);
   const int64_t lda = args.lda, ldb = args.ldb;
   const int64_t M = args.M, N = args.N, K = args.K;
   typedef Mfma<T> Mm;
   typedef typename Mm::vec8 V8;
-  __shared__ __attribute__((aligned(16))) T As[3 * BM * BK];  // ring of three
+  __shared__ __attribute__((aligned(16))) T As[3 * TBM * BK];  // ring of three
   __shared__ __attribute__((aligned(16))) T Bs0[BN * BK];
   __shared__ __attribute__((aligned(16))) T Bs1[BN * BK];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, q4 = lane >> 4;
   const int wm = wave >> 1, wn = wave & 1;
-  const int64_t n_m = M / BM, n_n = N / BN, nwg = n_m * n_n;
+  const int64_t n_m = M / TBM, n_n = N / BN, nwg = n_m * n_n;
   int64_t pid = blockIdx.x;
   if ((nwg & 7) == 0) pid = (pid & 7) * (nwg >> 3) + (pid >> 3);
   const int64_t per_group = static_cast<int64_t>(GROUP_M) * n_n;
@@ -276,7 +302,7 @@ void gemm_tiled_kernel(GemmArgs args) {
   const int64_t mf = grp * GROUP_M;
   const int64_t gm = n_m - mf < GROUP_M ? n_m - mf : GROUP_M;
   const int64_t in_grp = pid - grp * per_group;
-  const int64_t m0 = (mf + in_grp % gm) * BM, n0 = (in_grp / gm) * BN;
+  const int64_t m0 = (mf + in_grp % gm) * TBM, n0 = (in_grp / gm) * BN;
   // first element of the tile and the step between K steps, per layout
   const T* Ab = AKM ? A + m0 : A + m0 * lda;
   const T* Bb = BKM ? B + n0 : B + n0 * ldb;
@@ -304,9 +330,9 @@ void gemm_tiled_kernel(GemmArgs args) {
     bdmak.init(ldb);
   else
     bdma.init(ldb);
-  f32x4 acc[8][8];
+  f32x4 acc[MB][8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{};
   // Operand bases.  NT tiles: lane l reads row l % 16 of each 16-row block,
@@ -317,9 +343,9 @@ void gemm_tiled_kernel(GemmArgs args) {
   int ntA[2] = {0, 0}, ntB[2] = {0, 0};
   int abase = 0, bbase = 0;
   if constexpr (AKM) {
-    abase = kmaj_base(wm * 128);
+    abase = kmaj_base(wm * WR);
   } else {
-    ntA[0] = nt_off(wm * 128 + l16, 8 * q4);
+    ntA[0] = nt_off(wm * WR + l16, 8 * q4);
     ntA[1] = ntA[0] ^ 32;
   }
   if constexpr (BKM) {
@@ -328,13 +354,13 @@ void gemm_tiled_kernel(GemmArgs args) {
     ntB[0] = nt_off(wn * 128 + l16, 8 * q4);
     ntB[1] = ntB[0] ^ 32;
   }
-  V8 xa[2][8], xb[2][8];
+  V8 xa[2][MB], xb[2][8];
   auto Bs = [&](int st) __attribute__((always_inline)) -> T* { return st ? Bs1 : Bs0; };
   // operand piece r (0..7: A row blocks, 8..15: B row blocks) of substep s
   // into set q
   auto rd_piece = [&](int sa, int sb, int s, int q, int r) __attribute__((always_inline)) {
-    if (r < 8) {
-      const T* t = &As[sa * (BM * BK)];
+    if (r < MB) {
+      const T* t = &As[sa * (TBM * BK)];
       if constexpr (AKM)
         xa[q][r] = kmaj_operand<T>(t, (abase ^ (16 * r)) + 8192 * s);
       else
@@ -342,16 +368,16 @@ void gemm_tiled_kernel(GemmArgs args) {
     } else {
       const T* t = Bs(sb);
       if constexpr (BKM)
-        xb[q][r - 8] = kmaj_operand<T>(t, (bbase ^ (16 * (r - 8))) + 8192 * s);
+        xb[q][r - MB] = kmaj_operand<T>(t, (bbase ^ (16 * (r - MB))) + 8192 * s);
       else
-        xb[q][r - 8] = *reinterpret_cast<const V8*>(&t[ntB[s] + 1024 * (r - 8)]);
+        xb[q][r - MB] = *reinterpret_cast<const V8*>(&t[ntB[s] + 1024 * (r - MB)]);
     }
   };
   auto loadA = [&](int sa, int64_t k, int p) __attribute__((always_inline)) {
     if constexpr (AKM)
-      admak.issue(&As[sa * (BM * BK)], Ab + k * a_step, lda, p);
+      admak.issue(&As[sa * (TBM * BK)], Ab + k * a_step, lda, p);
     else
-      adma.issue(&As[sa * (BM * BK)], Ab + k * a_step, lda, p);
+      adma.issue(&As[sa * (TBM * BK)], Ab + k * a_step, lda, p);
   };
   auto loadB = [&](int sb, int64_t k, int p) __attribute__((always_inline)) {
     if constexpr (EPI != 1) {
@@ -364,27 +390,32 @@ void gemm_tiled_kernel(GemmArgs args) {
                            static_cast<uint32_t>(16 * p * ldb * static_cast<int64_t>(sizeof(T))), p);
     }
   };
-  // The 64 MFMAs of set q in rows of eight.  After row c: one load (LK 1: A
-  // piece c of step k into ring stage lst; LK 2: B piece c into B stage lst)
-  // and, when RD, two operand pieces of substep s0 of stages (ra, rb) into
-  // set q0, in the order the next set's MFMAs use them: its first row needs
-  // A piece 0 and all eight B pieces, row c A piece c, so the reads go A0,
-  // B0 .. B7, A1 .. A7 (B7 is in flight from row 4, three rows before it is
-  // needed; read last, it stalled the next set's first MFMA for the LDS
-  // latency at every substep).  The fences keep this order.
-  constexpr int kReadOrder[16] = {0, 8, 9, 10, 11, 12, 13, 14, 15, 1, 2, 3, 4, 5, 6, 7};
+  // The 8 MB MFMAs of set q in rows of eight.  After row c: A piece c (LK 1:
+  // of step k into ring stage lst) or 8 / MB B pieces (LK 2: into B stage
+  // lst), and, when RD, (MB + 8) / MB operand pieces of substep s0 of stages
+  // (ra, rb) into set q0, in the order the next set's MFMAs use them: its
+  // first row needs A piece 0 and all eight B pieces, row c A piece c, so the
+  // reads go A0, B0 .. B7, A1 .. A(MB-1) (for MB = 8, B7 is in flight from
+  // row 4, three rows before it is needed; read last, it stalled the next
+  // set's first MFMA for the LDS latency at every substep).  The fences keep
+  // this order.
+  constexpr ReadOrder kRO = read_order<MB>();
+  constexpr int RPR = (MB + 8) / MB, BPR = 8 / MB;
   auto mm_ld = [&](int q, int lk, int lst, int64_t k, bool rd, int ra, int rb, int s0,
                    int q0) __attribute__((always_inline)) {
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
+    for (int c = 0; c < MB; ++c) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[c][j] = Mm::mma16(xa[q][c], xb[q][j], acc[c][j]);
       if (rd) {
-        rd_piece(ra, rb, s0, q0, kReadOrder[2 * c]);
-        rd_piece(ra, rb, s0, q0, kReadOrder[2 * c + 1]);
+#pragma unroll
+        for (int u = 0; u < RPR; ++u) rd_piece(ra, rb, s0, q0, kRO.v[RPR * c + u]);
       }
       if (lk == 1) loadA(lst, k, c);
-      if (lk == 2) loadB(lst, k, c);
+      if (lk == 2) {
+#pragma unroll
+        for (int u = 0; u < BPR; ++u) loadB(lst, k, BPR * c + u);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -392,17 +423,17 @@ void gemm_tiled_kernel(GemmArgs args) {
   const int64_t n_k = K / BK;  // even, >= 4
   // prologue: steps 0 and 1 of A and B
 #pragma unroll
-  for (int p = 0; p < 8; ++p) loadA(0, 0, p);
+  for (int p = 0; p < MB; ++p) loadA(0, 0, p);
 #pragma unroll
   for (int p = 0; p < 8; ++p) loadB(0, 0, p);
 #pragma unroll
-  for (int p = 0; p < 8; ++p) loadA(1, 1, p);
+  for (int p = 0; p < MB; ++p) loadA(1, 1, p);
 #pragma unroll
   for (int p = 0; p < 8; ++p) loadB(1, 1, p);
-  wait_vmcnt<16>();
+  wait_vmcnt<MB + 8>();  // step 0 landed (step 1's MB + 8 loads may be in flight)
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < 16; ++r) rd_piece(0, 0, 0, 0, r);
+  for (int r = 0; r < MB + 8; ++r) rd_piece(0, 0, 0, 0, r);
 
   // K step t: A ring stage sa = t % 3, B stage sb = t % 2; set s = substep s.
   // Part A: set 0 with A(t + 2) (into ring stage (t + 2) % 3, free since the
@@ -426,7 +457,7 @@ void gemm_tiled_kernel(GemmArgs args) {
     if constexpr (SYNC) {
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
       if constexpr (VM8)
-        wait_vmcnt<8>();
+        wait_vmcnt<MB>();
       else
         wait_vmcnt<0>();
       __syncthreads();
@@ -463,7 +494,15 @@ void gemm_tiled_kernel(GemmArgs args) {
   __syncthreads();
   int el = lane;
   asm volatile("" : "+v"(el));  // keep the epilogue's index math after the loop
-  float* ws = reinterpret_cast<float*>(wave < 3 ? &As[wave * (BM * BK)] : Bs0);
+  // each wave's 16 x 132-float staging area (and for EPI 1 the z tile after
+  // it): a 32 KB A stage each for 256-row tiles (Bs0 for wave 3); for 128-row
+  // tiles (EPI 0 only) two in the 48 KB A ring, Bs0 and Bs1
+  float* ws;
+  if constexpr (MB == 8)
+    ws = reinterpret_cast<float*>(wave < 3 ? &As[wave * (TBM * BK)] : Bs0);
+  else
+    ws = wave < 2 ? reinterpret_cast<float*>(As) + wave * (16 * 132)
+                  : reinterpret_cast<float*>(wave == 2 ? Bs0 : Bs1);
   const int e16 = el & 15, eq = el >> 4;
   typedef T T8 __attribute__((ext_vector_type(8)));
   // EPI 2: the wave's 128 columns hold whole heads (head dim 2 rhalf = 64 or
@@ -472,7 +511,7 @@ void gemm_tiled_kernel(GemmArgs args) {
   // (rs0 + 16 i + r) mod rS (32-bit: the host keeps rS in [128, 2^30)).
   const bool rot = EPI == 2 && n0 + wn * 128 < args.rcols;
   const int rs32 = static_cast<int>(args.rS);
-  const int rs0 = EPI == 2 ? static_cast<int>((m0 + wm * 128) % args.rS) : 0;
+  const int rs0 = EPI == 2 ? static_cast<int>((m0 + wm * WR) % args.rS) : 0;
   auto rope_pos = [&](int off) -> int {
     int sq = rs0 + off;
     sq = sq >= rs32 ? sq - rs32 : sq;  // the host takes this path for rS >= 128 only
@@ -484,7 +523,7 @@ void gemm_tiled_kernel(GemmArgs args) {
   // 128, 4 for 64)
   const int hcl = args.rhalf == 64 ? 3 : 2, hcm = (1 << hcl) - 1;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < MB; ++i) {
     // EPI 2, half-split pairing: this block's cos / sin, loaded before the
     // staging stores below so that their latency overlaps them
     float4 rc0[2], rc1[2], rsn0[2], rsn1[2];
@@ -505,7 +544,7 @@ void gemm_tiled_kernel(GemmArgs args) {
     for (int j = 0; j < 8; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e) ws[(4 * eq + e) * 132 + 16 * j + e16] = acc[i][j][e];
-    const int64_t row0 = m0 + wm * 128 + 16 * i;
+    const int64_t row0 = m0 + wm * WR + 16 * i;
     if (EPI == 2 && rot && args.rpair == ZK_ROPE_HALF) {
       // 16 rows x 8 chunk pairs: chunk a (first half of its head) with the
       // chunk rhalf / 8 further; the product rounded to T first, as stored

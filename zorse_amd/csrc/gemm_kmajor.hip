@@ -15,6 +15,9 @@ void launch_t(bool akm, bool bkm, const GemmArgs& ga, hipStream_t s) {
     hipLaunchKernelGGL((gemm_tiled_kernel<T, 0, true, true>), grid, dim3(256), 0, s, ga);
   else if (akm)
     hipLaunchKernelGGL((gemm_tiled_kernel<T, 0, true, false>), grid, dim3(256), 0, s, ga);
+  else if (half_tiles(grid.x))
+    hipLaunchKernelGGL((gemm_tiled_kernel<T, 0, false, true, 4>), dim3(2 * grid.x), dim3(256), 0,
+                       s, ga);
   else
     hipLaunchKernelGGL((gemm_tiled_kernel<T, 0, false, true>), grid, dim3(256), 0, s, ga);
 }
