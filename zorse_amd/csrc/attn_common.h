@@ -277,7 +277,8 @@ __device__ __forceinline__ void tile_load_async(T* tile, const T* gbase, int64_t
   constexpr int CH = ROWS * D / 8;
   static_assert(CH % NT == 0, "tile must be a multiple of NT chunks");
   const int tid = threadIdx.x;
-  const int wave_chunk0 = tid & ~63;
+  // wave-uniform, so the LDS destination is computed in scalar registers
+  const int wave_chunk0 = __builtin_amdgcn_readfirstlane(tid & ~63);
   // offsets from the tile's first row (< ROWS rows, so 32 bits suffice)
   const __amdgpu_buffer_rsrc_t r = raw_rsrc(gbase + g0 * ld);
 #pragma unroll
@@ -317,7 +318,7 @@ struct TileLoader {
   // Rows g0 .. g0 + ROWS - 1 must all lie below the tensor's row count.
   __device__ __forceinline__ void issue_full(T* tile, const T* gbase, int64_t ld,
                                              int64_t g0) const {
-    const int wave_chunk0 = static_cast<int>(threadIdx.x) & ~63;
+    const int wave_chunk0 = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) & ~63);
     const __amdgpu_buffer_rsrc_t r = raw_rsrc(gbase + g0 * ld);
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
