@@ -240,14 +240,21 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv(AttnArgs a) {
     auto scores = [&](int mb, f32x16& sv, f32x16& dpv) {
       sv = f32x16{};
       dpv = f32x16{};
+      // each step's Q operand read one step ahead, before the MFMAs of the
+      // step it follows (the fences keep the compiler from sinking it)
+      V8 qa = *reinterpret_cast<const V8*>(reinterpret_cast<const char*>(Qt) + rb);
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
         const int ro = rb ^ (ks << 5);
-        const V8 qa = *reinterpret_cast<const V8*>(reinterpret_cast<const char*>(Qt) + ro);
-        sv = M::mma(qa, kreg[ks], sv);
         const V8 da = *reinterpret_cast<const V8*>(reinterpret_cast<const char*>(dOt) + ro);
         const V8 vb = *reinterpret_cast<const V8*>(reinterpret_cast<const char*>(Vme) + ro);
+        V8 qn = qa;
+        if (ks + 1 < D / 16)
+          qn = *reinterpret_cast<const V8*>(reinterpret_cast<const char*>(Qt) + (rb ^ ((ks + 1) << 5)));
+        __builtin_amdgcn_sched_barrier(0);
+        sv = M::mma(qa, kreg[ks], sv);
         dpv = M::mma(da, vb, dpv);
+        qa = qn;
       }
     };
     // P and dS of half mb, packed as the B operands of two 16-query MFMA steps;
