@@ -193,7 +193,7 @@ def main(argv=None):
     ap.add_argument("--autocast_dtype", default="bfloat16", choices=["float32", "float16", "bfloat16"])
     ap.add_argument("--profile_batches", type=int, default=4)
     ap.add_argument("--vocab_size", type=int, default=49152)
-    ap.add_argument("--out", default="gpurun_out/model_latencies.json")
+    ap.add_argument("--out", default="model_latencies.json")
     args = ap.parse_args(argv)
     dtype = getattr(torch, args.autocast_dtype)
     entry, opt_ms = profile_model(args.model_name, args.seq_length, dtype, args.profile_batches,
